@@ -1,0 +1,130 @@
+// Row kernels: embedding gather + dequant, RMSNorm, per-group int8 quant.
+//
+//   mode 2  kernels/embedding.h:99-168 embedding_rmsnorm_rows
+//           (ref_qwen3.py:292-296): x = f32(emb8[id]) * emb_s[id]
+//   mode 1  kernels/rmsnorm.h:34-81 rmsnorm_rows (ref_qwen3.py:161-177)
+//   quant   kernels/quant.h:89-138 quant_rows_heads (ref_qwen3.py:86-97),
+//           fused behind modes 1/2 or alone (mode 0)
+//
+// One wave64 per row.  Columns are visited 64 at a time: lanes 0-31 hold
+// 32-column block 2i and lanes 32-63 block 2i+1, so the per-block tree sum
+// is a 5-level butterfly inside each half-wave and the block sums are then
+// added strictly in column order, exactly like the reference's
+// `ss = ss + tree_sum(block**2)` loop.  The row is re-read (L1/L2 resident)
+// instead of held in registers so any width works.
+#include "q3_device.h"
+#include "q3_kernels.h"
+
+namespace q3 {
+namespace {
+
+__device__ __forceinline__ float load_x(const RowArgs &a, int row, int c,
+                                        int32_t id) {
+  if (a.mode == 2) {
+    if (id < 0 || id >= a.table_rows) return 0.0f;
+    const float e = static_cast<float>(a.table[static_cast<int64_t>(id) * a.ldt + c]);
+    return __fmul_rn(e, a.tscale[static_cast<int64_t>(id) * a.tss]);
+  }
+  return a.x[static_cast<int64_t>(row) * a.ldx + c];
+}
+
+__global__ void __launch_bounds__(256) rows_kernel(RowArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.rows) return;
+  int32_t id = 0;
+  if (a.mode == 2) {
+    int64_t base = 0;
+    if (a.ids_base_pos) base = *a.ids_base_pos;
+    id = a.ids[(base + row) * a.ids_stride];
+  }
+  const int cols = a.cols;
+
+  float rinv = 1.0f;
+  if (a.mode != 0) {
+    // pass 1: ordered block sums of squares (and the embedding write-out)
+    float ss = 0.0f;
+    const int nblk = (cols + 31) / 32;
+    for (int c0 = 0; c0 < cols; c0 += 64) {
+      const int c = c0 + lane;
+      float v = 0.0f;
+      if (c < cols) {
+        v = load_x(a, row, c, id);
+        if (a.mode == 2 && a.x_out) a.x_out[static_cast<int64_t>(row) * a.ldxo + c] = v;
+      }
+      const float bsum = tree_sum32(__fmul_rn(v, v));
+      const float b_lo = __shfl(bsum, 0);
+      const float b_hi = __shfl(bsum, 32);
+      ss = __fadd_rn(ss, b_lo);
+      if ((c0 >> 5) + 1 < nblk) ss = __fadd_rn(ss, b_hi);
+    }
+    rinv = rms_factor(ss, a.inv);
+    // pass 2: h = (x * rinv) * w
+    if (a.h) {
+      for (int c = lane; c < cols; c += 64) {
+        const float v = load_x(a, row, c, id);
+        const float y = __fmul_rn(__fmul_rn(v, rinv), a.w[static_cast<int64_t>(c) * a.w_stride]);
+        a.h[static_cast<int64_t>(row) * a.ldh + c] = y;
+      }
+    }
+  }
+  if (!a.h8) return;
+  // per-group quantisation of y (= x in mode 0)
+  const int G = a.group;
+  for (int g0 = 0, gi = 0; g0 < cols; g0 += G, ++gi) {
+    const int g1 = min(cols, g0 + G);
+    float m = 0.0f;
+    for (int c = g0 + lane; c < g1; c += 64) {
+      float y = load_x(a, row, c, id);
+      if (a.mode != 0)
+        y = __fmul_rn(__fmul_rn(y, rinv), a.w[static_cast<int64_t>(c) * a.w_stride]);
+      m = fmaxf(m, fabsf(y));
+    }
+    m = max64(m);
+    const float scale = __fmul_rn(m, inv127());
+    if (lane == 0) a.hs[static_cast<int64_t>(row) * a.ldhs + gi] = scale;
+    for (int c = g0 + lane; c < g1; c += 64) {
+      float y = load_x(a, row, c, id);
+      if (a.mode != 0)
+        y = __fmul_rn(__fmul_rn(y, rinv), a.w[static_cast<int64_t>(c) * a.w_stride]);
+      a.h8[static_cast<int64_t>(row) * a.ldh8 + c] = static_cast<int8_t>(quant1(y, scale));
+    }
+  }
+}
+
+// kernels/norm_rope_quant.h:88-111 norm_rope_quant_heads: one wave per
+// (row, head) of an f32 [rows][heads*128] input.
+__global__ void __launch_bounds__(256) nrq_rows_kernel(NrqArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (item >= a.rows * a.heads) return;
+  const int row = item / a.heads, head = item % a.heads;
+  const float *xr = a.x + static_cast<int64_t>(row) * a.ldx + head * 128;
+  float t0 = xr[lane], t1 = xr[lane + 64];
+  head_norm_rope(t0, t1, lane, a.nw, a.nw_stride, a.cos_t + static_cast<int64_t>(row) * a.ld_cs,
+                 a.sin_t + static_cast<int64_t>(row) * a.ld_cs, a.inv_hd, a.do_rope != 0);
+  const float mx = max64(fmaxf(fabsf(t0), fabsf(t1)));
+  const float scale = __fmul_rn(mx, inv127());
+  int8_t *q = a.q8 + static_cast<int64_t>(row) * a.ldq8 + head * 128;
+  q[lane] = static_cast<int8_t>(quant1(t0, scale));
+  q[lane + 64] = static_cast<int8_t>(quant1(t1, scale));
+  if (lane == 0) a.qs[static_cast<int64_t>(row) * a.ldqs + head * a.qs_col] = scale;
+}
+
+}  // namespace
+
+hipError_t launch_nrq_rows(const NrqArgs &a, hipStream_t s) {
+  const int items = a.rows * a.heads;
+  if (items <= 0) return hipSuccess;
+  hipLaunchKernelGGL(nrq_rows_kernel, dim3((items + 3) / 4), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_rows(const RowArgs &a, hipStream_t s) {
+  if (a.rows <= 0) return hipSuccess;
+  const dim3 grid((a.rows + 3) / 4);
+  hipLaunchKernelGGL(rows_kernel, grid, dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace q3

@@ -1,0 +1,174 @@
+// Internal launch interface shared by the operator ABI (q3_ops.hip) and the
+// model orchestration (q3_model.hip).  All pointers are device addresses;
+// strides are in elements.  Launchers only enqueue work on `stream`.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace q3 {
+
+// ---- row kernels: embedding gather, RMSNorm, per-group quantisation ----
+struct RowArgs {
+  int mode;  // 0: quant only (y = x), 1: rmsnorm, 2: embedding + rmsnorm
+  int rows, cols;
+  // input
+  const float *x;
+  int64_t ldx;
+  const int8_t *table;  // mode 2: [V][cols] i8
+  int64_t ldt;
+  int64_t table_rows;   // mode 2: V (ids outside [0, V) read as a zero row)
+  const float *tscale;  // mode 2: per-row scale, stride tss
+  int64_t tss;
+  const int32_t *ids;   // mode 2: ids, stride ids_stride
+  int64_t ids_stride;
+  const int32_t *ids_base_pos;  // mode 2 (optional): ids += *ids_base_pos
+  float *x_out;         // mode 2: dequantised embedding rows (may be null)
+  int64_t ldxo;
+  // rmsnorm
+  const float *w;
+  int64_t w_stride;
+  float inv;
+  float *h;             // normalised rows (may be null)
+  int64_t ldh;
+  // quantisation (skipped when h8 == null)
+  int8_t *h8;
+  int64_t ldh8;
+  float *hs;
+  int64_t ldhs;
+  int group;
+};
+hipError_t launch_rows(const RowArgs &a, hipStream_t s);
+
+// ---- group GEMM --------------------------------------------------------
+enum Epi : int {
+  EPI_STORE = 0,   // out = D
+  EPI_ADD = 1,     // add += D
+  EPI_HEADQ = 2,   // per-128-column int8 quant (V)
+  EPI_NRQ = 3,     // per-head RMSNorm + RoPE + int8 quant (Q, K)
+  EPI_ARGMAX = 4,  // fold D into per-row (max, first index) keys
+};
+
+// Destination of the HEADQ/NRQ int8 rows: either a dense [M][N] i8 view
+// with [M][N/128] scales, or the paged KV pool (row m -> token pos0 + m).
+struct QDest {
+  int8_t *q8;
+  int64_t ldq8;
+  float *qs;
+  int64_t ldqs;        // elements between rows of qs
+  int64_t qs_col;      // elements between heads of qs
+  // paged (used when table != null)
+  const uint16_t *table;
+  uint32_t page_tokens;
+  int64_t page_bytes, row_bytes;             // i8 pages
+  int64_t scale_page_bytes, scale_row_bytes; // f32 pages
+  uint32_t pos0;
+  const int32_t *pos_dev;  // optional: pos0 += *pos_dev
+};
+
+struct GemmArgs {
+  int M, N, K, group;
+  const int8_t *a;
+  int64_t lda;
+  const float *as;
+  int64_t ldas;       // elements between rows of a_scale
+  const int8_t *b;
+  int64_t ldb;
+  const float *bs;
+  int64_t bs_stride;  // elements between consecutive b_scale entries
+  int epi;
+  float *out;
+  int64_t ldo;        // EPI_STORE / EPI_ADD target
+  QDest qd;
+  // EPI_NRQ
+  const float *nw;
+  int64_t nw_stride;
+  const float *cos_t, *sin_t;  // [rows][64] at the rows' absolute positions
+  int64_t ld_cs;
+  const int32_t *cs_row_dev;   // optional: cos/sin row offset (device scalar)
+  float inv_hd;
+  // EPI_ARGMAX
+  unsigned long long *keys;  // [M] workspace, zero before the first launch
+};
+hipError_t launch_gemm(const GemmArgs &a, hipStream_t s);
+
+// Finishes EPI_ARGMAX: merges keys[m] into (best[m], bidx[m]) with the
+// strict `best < value` rule (init != 0: start from -3e38 / 0 instead of the
+// current contents), optionally writes the winning id to
+// ids[*pos] (greedy loop), and clears keys for the next launch.
+hipError_t launch_argmax_finish(unsigned long long *keys, int M, float *best,
+                                int64_t best_stride, int32_t *bidx,
+                                int64_t bidx_stride, int init, int32_t *ids_out,
+                                const int32_t *pos_dev, int pos_add,
+                                hipStream_t s);
+
+// ---- fused gate/up GEMM + SwiGLU + per-256-column quant -----------------
+struct GateUpArgs {
+  int M, N, K, group;
+  const int8_t *a;
+  int64_t lda;
+  const float *as;
+  int64_t ldas;
+  const int8_t *wg, *wu;
+  int64_t ldw;
+  const float *wgs, *wus;
+  int64_t ws_stride;
+  int8_t *s8;
+  int64_t lds8;
+  float *ss;
+  int64_t ldss;
+  int64_t ss_col;
+};
+hipError_t launch_gate_up(const GateUpArgs &a, hipStream_t s);
+
+// ---- paged GQA attention -------------------------------------------------
+struct AttnArgs {
+  int rows, heads, kv_heads;  // head_dim is 128
+  uint32_t kv_len;
+  const int32_t *kv_len_dev;  // optional: kv_len += *kv_len_dev
+  int causal;
+  float qk_scale;
+  const int8_t *q8;
+  int64_t ldq;
+  const float *qs;
+  int64_t ldqs;
+  int64_t qs_col;
+  const int8_t *k, *v;
+  const float *ks, *vs;
+  const uint16_t *table;
+  uint32_t page_tokens;
+  int64_t page_bytes, row_bytes, scale_page_bytes, scale_row_bytes;
+  int8_t *o8;
+  int64_t ldo;
+  float *os;
+  int64_t ldos;
+  int64_t os_col;
+  float *attn;   // optional f32 attention output [rows][heads*128]
+  int64_t ld_attn;
+};
+hipError_t launch_attention(const AttnArgs &a, hipStream_t s);
+
+// ---- standalone per-head norm + RoPE + quant (f32 input) -----------------
+struct NrqArgs {
+  int rows, heads;
+  const float *x;
+  int64_t ldx;
+  const float *nw;
+  int64_t nw_stride;
+  const float *cos_t, *sin_t;
+  int64_t ld_cs;
+  float inv_hd;
+  int do_rope;
+  int8_t *q8;
+  int64_t ldq8;
+  float *qs;
+  int64_t ldqs, qs_col;
+};
+hipError_t launch_nrq_rows(const NrqArgs &a, hipStream_t s);
+
+// ---- greedy pick over a logits row (main_big.cpp:300-322) ---------------
+hipError_t launch_argmax_logits(const float *logits, int vocab,
+                                int32_t *out_id, const int32_t *pos_dev,
+                                int pos_add, hipStream_t s);
+
+}  // namespace q3

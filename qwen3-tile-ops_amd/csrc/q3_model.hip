@@ -1,0 +1,462 @@
+// Model orchestration over a device-resident PQWF blob.
+//
+//   src/main_big.cpp:55-136   make_model_views / make_layer_views
+//   src/main_big.cpp:145-296  forward_chunk
+//   src/main_big.cpp:332-369  main() greedy loop
+//   tools/ref_qwen3.py:366-490 (the same semantics in numpy)
+//
+// Every buffer is an offset into the one device blob (tools/pqwf.py layout),
+// so the device image after a run can be diffed stage by stage like the
+// reference's blob dump.  The KV pool of each layer is paged with 32-token
+// pages through a logical->physical page table (reversed by default, as in
+// main_big.cpp:168-171); K/V rows are written by the projection GEMMs'
+// epilogues straight into their page slots, one row at a time, so a chunk
+// may start anywhere and span pages.  All work is enqueued on the model's
+// stream; the generated ids are written on the device (no host round trip
+// per token).
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "q3_kernels.h"
+#include "q3ops.h"
+
+struct q3_model {
+  uint8_t *blob;
+  q3_layout lay;
+  hipStream_t stream;
+  uint16_t *ptab;              // device, max_seq / 32 entries
+  uint32_t n_pages;
+  unsigned long long *keys;    // device argmax key (1 row)
+};
+
+namespace {
+
+constexpr uint32_t kPageTokens = 32;
+
+int hip_status(hipError_t e) { return e == hipSuccess ? Q3_OK : Q3_ERR_HIP; }
+
+#define Q3_HIP(expr)                                      \
+  do {                                                    \
+    const hipError_t q3_e_ = (expr);                      \
+    if (q3_e_ != hipSuccess) return Q3_ERR_HIP;           \
+  } while (0)
+
+template <class T>
+T *at(const q3_model *m, int64_t off) {
+  return reinterpret_cast<T *>(m->blob + off);
+}
+
+// Per-layer views (main_big.cpp:100-136).
+struct LayerPtrs {
+  const int8_t *wq, *wk, *wv, *wo, *wg, *wu, *wd;
+  const float *wqs, *wks, *wvs, *wos, *wgs, *wus, *wds;
+  const float *n1, *nq, *nk, *n2;
+  int8_t *kc, *vc;
+  float *kcs, *vcs;
+};
+
+LayerPtrs layer_ptrs(const q3_model *m, uint32_t L) {
+  const q3_layout &y = m->lay;
+  const int64_t w = static_cast<int64_t>(L) * y.kLAYERW_STRIDE;
+  const int64_t n = static_cast<int64_t>(L) * y.kLAYERN_STRIDE;
+  const int64_t kv = y.kKV_BASE + static_cast<int64_t>(L) * y.kKV_STRIDE;
+  LayerPtrs p;
+  p.wq = at<const int8_t>(m, y.kLQ + w);
+  p.wk = at<const int8_t>(m, y.kLK + w);
+  p.wv = at<const int8_t>(m, y.kLV + w);
+  p.wo = at<const int8_t>(m, y.kLO + w);
+  p.wg = at<const int8_t>(m, y.kLG + w);
+  p.wu = at<const int8_t>(m, y.kLU + w);
+  p.wd = at<const int8_t>(m, y.kLD + w);
+  p.wqs = at<const float>(m, y.kLQ_SCALE + w);
+  p.wks = at<const float>(m, y.kLK_SCALE + w);
+  p.wvs = at<const float>(m, y.kLV_SCALE + w);
+  p.wos = at<const float>(m, y.kLO_SCALE + w);
+  p.wgs = at<const float>(m, y.kLG_SCALE + w);
+  p.wus = at<const float>(m, y.kLU_SCALE + w);
+  p.wds = at<const float>(m, y.kLD_SCALE + w);
+  p.n1 = at<const float>(m, y.kN1 + n);
+  p.nq = at<const float>(m, y.kNQ + n);
+  p.nk = at<const float>(m, y.kNK + n);
+  p.n2 = at<const float>(m, y.kN2 + n);
+  p.kc = at<int8_t>(m, kv);
+  p.kcs = at<float>(m, kv + y.kKV_SOFF);
+  p.vc = at<int8_t>(m, kv + y.kKV_VOFF);
+  p.vcs = at<float>(m, kv + y.kKV_VOFF + y.kKV_SOFF);
+  return p;
+}
+
+void set_paged(q3::QDest &d, const q3_model *m, int8_t *pool, float *spool, uint32_t pos0) {
+  const q3_layout &y = m->lay;
+  const int64_t KW = static_cast<int64_t>(y.kv_heads) * y.head_dim;
+  d.q8 = pool;
+  d.qs = spool;
+  d.table = m->ptab;
+  d.page_tokens = kPageTokens;
+  d.page_bytes = kPageTokens * KW;
+  d.row_bytes = KW;
+  d.scale_page_bytes = kPageTokens * y.kv_heads * 4;
+  d.scale_row_bytes = y.kv_heads * 4;
+  d.pos0 = pos0;
+}
+
+// Row kernel over x rows [r0, r0+n): RMSNorm with gain w (or the embedding
+// gather for layer 0) into h, then per-256 quant into h8/hs.
+int norm_quant_rows(const q3_model *m, int mode, uint32_t pos, uint32_t r0, uint32_t n,
+                    const float *w, float *x, float *h, int8_t *h8, float *hs) {
+  const q3_layout &y = m->lay;
+  const int64_t H = y.hidden;
+  q3::RowArgs r{};
+  r.mode = mode;
+  r.rows = static_cast<int>(n);
+  r.cols = static_cast<int>(H);
+  r.x = x + r0 * H;
+  r.ldx = H;
+  if (mode == 2) {
+    r.table = at<const int8_t>(m, y.kEMB);
+    r.ldt = H;
+    r.table_rows = y.vocab;
+    r.tscale = at<const float>(m, y.kEMB + static_cast<int64_t>(y.vocab) * H);
+    r.tss = 1;
+    r.ids = at<const int32_t>(m, y.kIDS) + pos + r0;
+    r.ids_stride = 1;
+    r.x_out = x + r0 * H;
+    r.ldxo = H;
+  }
+  r.w = w;
+  r.w_stride = 1;
+  r.inv = 1.0f / static_cast<float>(H);
+  r.h = h + r0 * H;
+  r.ldh = H;
+  r.h8 = h8 + r0 * H;
+  r.ldh8 = H;
+  r.hs = hs + r0 * (H / 256);
+  r.ldhs = H / 256;
+  r.group = 256;
+  return hip_status(q3::launch_rows(r, m->stream));
+}
+
+q3::GemmArgs gemm_args(int M, int N, int K, int group, const int8_t *a, const float *as,
+                       const int8_t *b, const float *bs) {
+  q3::GemmArgs g;
+  std::memset(&g, 0, sizeof(g));
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.group = group;
+  g.a = a;
+  g.lda = K;
+  g.as = as;
+  g.ldas = K / group;
+  g.b = b;
+  g.ldb = K;
+  g.bs = bs;
+  g.bs_stride = 1;
+  return g;
+}
+
+// main_big.cpp:145-296.  id_dst (device, may be null) receives the greedy id
+// of the last row when lm_out != Q3_LM_NONE.
+int forward_chunk_impl(q3_model *m, uint32_t pos, uint32_t rows, int lm_out,
+                       int optimize_tail, int32_t *id_dst) {
+  const q3_layout &y = m->lay;
+  if (rows == 0 || rows > y.seq || pos + rows > y.max_seq) return Q3_ERR_RANGE;
+  if (lm_out < Q3_LM_NONE || lm_out > Q3_LM_ARGMAX) return Q3_ERR_ARG;
+  const int H = static_cast<int>(y.hidden), HD = static_cast<int>(y.head_dim);
+  const int QW = static_cast<int>(y.heads) * HD, KW = static_cast<int>(y.kv_heads) * HD;
+  const int I = static_cast<int>(y.inter), V = static_cast<int>(y.vocab);
+  const int HALF = static_cast<int>(y.half);
+  const hipStream_t s = m->stream;
+
+  float *x = at<float>(m, y.kX);
+  float *h = at<float>(m, y.kH);
+  int8_t *h8 = at<int8_t>(m, y.kH8);
+  float *hs = at<float>(m, y.kHS);
+  int8_t *q8 = at<int8_t>(m, y.kQ8);
+  float *qs = at<float>(m, y.kQS);
+  int8_t *o8 = at<int8_t>(m, y.kO8);
+  float *os = at<float>(m, y.kOS);
+  int8_t *s8 = at<int8_t>(m, y.kS8);
+  float *ss = at<float>(m, y.kSS);
+  const float *cos_t = at<const float>(m, y.kCOS);
+  const float *sin_t = at<const float>(m, y.kSIN);
+  const float inv_hd = 1.0f / static_cast<float>(HD);
+  const float qk_scale = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(HD)));
+
+  // embedding + layer-0 RMSNorm (main_big.cpp:163-166), then its quant
+  {
+    const LayerPtrs l0 = layer_ptrs(m, 0);
+    const int rc = norm_quant_rows(m, 2, pos, 0, rows, l0.n1, x, h, h8, hs);
+    if (rc != Q3_OK) return rc;
+  }
+
+  for (uint32_t L = 0; L < y.layers; ++L) {
+    const LayerPtrs lp = layer_ptrs(m, L);
+    if (L != 0) {
+      const int rc = norm_quant_rows(m, 1, pos, 0, rows, lp.n1, x, h, h8, hs);
+      if (rc != Q3_OK) return rc;
+    }
+    // V: GEMM + per-head quant straight into the page slots
+    {
+      q3::GemmArgs g = gemm_args(static_cast<int>(rows), KW, H, 256, h8, hs, lp.wv, lp.wvs);
+      g.epi = q3::EPI_HEADQ;
+      set_paged(g.qd, m, lp.vc, lp.vcs, pos);
+      Q3_HIP(q3::launch_gemm(g, s));
+    }
+    // K: GEMM + k-norm + RoPE + per-head quant into the page slots
+    {
+      q3::GemmArgs g = gemm_args(static_cast<int>(rows), KW, H, 256, h8, hs, lp.wk, lp.wks);
+      g.epi = q3::EPI_NRQ;
+      set_paged(g.qd, m, lp.kc, lp.kcs, pos);
+      g.nw = lp.nk;
+      g.nw_stride = 1;
+      g.cos_t = cos_t + static_cast<int64_t>(pos) * HALF;
+      g.sin_t = sin_t + static_cast<int64_t>(pos) * HALF;
+      g.ld_cs = HALF;
+      g.inv_hd = inv_hd;
+      Q3_HIP(q3::launch_gemm(g, s));
+    }
+    // main_big.cpp:212-223: the last layer only needs the tail rows
+    const bool is_last = (L + 1 == y.layers);
+    const bool do_tail = !is_last || lm_out != Q3_LM_NONE;
+    if (!do_tail) continue;
+    const bool tail_last_row = optimize_tail && is_last;
+    const uint32_t tr0 = tail_last_row ? rows - 1 : 0;
+    const uint32_t tr = tail_last_row ? 1 : rows;
+    const int M = static_cast<int>(tr);
+
+    // Q: GEMM + q-norm + RoPE + per-head quant
+    {
+      q3::GemmArgs g = gemm_args(M, QW, H, 256, h8 + static_cast<int64_t>(tr0) * H,
+                                 hs + static_cast<int64_t>(tr0) * (H / 256), lp.wq, lp.wqs);
+      g.epi = q3::EPI_NRQ;
+      g.qd.q8 = q8 + static_cast<int64_t>(tr0) * QW;
+      g.qd.ldq8 = QW;
+      g.qd.qs = qs + static_cast<int64_t>(tr0) * y.heads;
+      g.qd.ldqs = y.heads;
+      g.qd.qs_col = 1;
+      g.nw = lp.nq;
+      g.nw_stride = 1;
+      g.cos_t = cos_t + static_cast<int64_t>(pos + tr0) * HALF;
+      g.sin_t = sin_t + static_cast<int64_t>(pos + tr0) * HALF;
+      g.ld_cs = HALF;
+      g.inv_hd = inv_hd;
+      Q3_HIP(q3::launch_gemm(g, s));
+    }
+    // paged GQA attention over kv_len = pos + rows keys
+    {
+      q3::AttnArgs t{};
+      t.rows = M;
+      t.heads = static_cast<int>(y.heads);
+      t.kv_heads = static_cast<int>(y.kv_heads);
+      t.kv_len = pos + rows;
+      t.causal = 1;
+      t.qk_scale = qk_scale;
+      t.q8 = q8 + static_cast<int64_t>(tr0) * QW;
+      t.ldq = QW;
+      t.qs = qs + static_cast<int64_t>(tr0) * y.heads;
+      t.ldqs = y.heads;
+      t.qs_col = 1;
+      t.k = lp.kc;
+      t.v = lp.vc;
+      t.ks = lp.kcs;
+      t.vs = lp.vcs;
+      t.table = m->ptab;
+      t.page_tokens = kPageTokens;
+      t.page_bytes = static_cast<int64_t>(kPageTokens) * KW;
+      t.row_bytes = KW;
+      t.scale_page_bytes = static_cast<int64_t>(kPageTokens) * y.kv_heads * 4;
+      t.scale_row_bytes = y.kv_heads * 4;
+      t.o8 = o8 + static_cast<int64_t>(tr0) * QW;
+      t.ldo = QW;
+      t.os = os + static_cast<int64_t>(tr0) * y.heads;
+      t.ldos = y.heads;
+      t.os_col = 1;
+      Q3_HIP(q3::launch_attention(t, s));
+    }
+    float *xt = x + static_cast<int64_t>(tr0) * H;
+    // O projection (group = head_dim) + residual into x
+    {
+      q3::GemmArgs g = gemm_args(M, H, QW, HD, o8 + static_cast<int64_t>(tr0) * QW,
+                                 os + static_cast<int64_t>(tr0) * y.heads, lp.wo, lp.wos);
+      g.epi = q3::EPI_ADD;
+      g.out = xt;
+      g.ldo = H;
+      Q3_HIP(q3::launch_gemm(g, s));
+    }
+    // post-attention RMSNorm + quant
+    {
+      const int rc = norm_quant_rows(m, 1, pos, tr0, tr, lp.n2, x, h, h8, hs);
+      if (rc != Q3_OK) return rc;
+    }
+    // gate/up + SwiGLU + quant
+    {
+      q3::GateUpArgs u{};
+      u.M = M;
+      u.N = I;
+      u.K = H;
+      u.group = 256;
+      u.a = h8 + static_cast<int64_t>(tr0) * H;
+      u.lda = H;
+      u.as = hs + static_cast<int64_t>(tr0) * (H / 256);
+      u.ldas = H / 256;
+      u.wg = lp.wg;
+      u.wu = lp.wu;
+      u.ldw = H;
+      u.wgs = lp.wgs;
+      u.wus = lp.wus;
+      u.ws_stride = 1;
+      u.s8 = s8 + static_cast<int64_t>(tr0) * I;
+      u.lds8 = I;
+      u.ss = ss + static_cast<int64_t>(tr0) * (I / 256);
+      u.ldss = I / 256;
+      u.ss_col = 1;
+      Q3_HIP(q3::launch_gate_up(u, s));
+    }
+    // down projection + residual into x
+    {
+      q3::GemmArgs g = gemm_args(M, H, I, 256, s8 + static_cast<int64_t>(tr0) * I,
+                                 ss + static_cast<int64_t>(tr0) * (I / 256), lp.wd, lp.wds);
+      g.epi = q3::EPI_ADD;
+      g.out = xt;
+      g.ldo = H;
+      Q3_HIP(q3::launch_gemm(g, s));
+    }
+  }
+
+  if (lm_out == Q3_LM_NONE) return Q3_OK;
+  // final norm of the last row into the borrowed buffers (main_big.cpp:264-274):
+  // hl = o row 0, h8l = q8 row 0 (first H columns), hsl = qs row 0
+  float *hl = at<float>(m, y.kO);
+  int8_t *h8l = q8;
+  float *hsl = qs;
+  {
+    q3::RowArgs r{};
+    r.mode = 1;
+    r.rows = 1;
+    r.cols = H;
+    r.x = x + static_cast<int64_t>(rows - 1) * H;
+    r.ldx = H;
+    r.w = at<const float>(m, y.kNF);
+    r.w_stride = 1;
+    r.inv = 1.0f / static_cast<float>(H);
+    r.h = hl;
+    r.ldh = H;
+    r.h8 = h8l;
+    r.ldh8 = H;
+    r.hs = hsl;
+    r.ldhs = H / 256;
+    r.group = 256;
+    Q3_HIP(q3::launch_rows(r, s));
+  }
+  const int8_t *lm = at<const int8_t>(m, y.kLM);
+  const float *lm_s = at<const float>(m, y.kLM + static_cast<int64_t>(V) * H);
+  if (lm_out == Q3_LM_LOGITS) {
+    float *logits = at<float>(m, y.kLOGITS);
+    q3::GemmArgs g = gemm_args(1, V, H, 256, h8l, hsl, lm, lm_s);
+    g.epi = q3::EPI_STORE;
+    g.out = logits;
+    g.ldo = V;
+    Q3_HIP(q3::launch_gemm(g, s));
+    if (id_dst) Q3_HIP(q3::launch_argmax_logits(logits, V, id_dst, nullptr, 0, s));
+  } else {
+    q3::GemmArgs g = gemm_args(1, V, H, 256, h8l, hsl, lm, lm_s);
+    g.epi = q3::EPI_ARGMAX;
+    g.keys = m->keys;
+    Q3_HIP(q3::launch_gemm(g, s));
+    Q3_HIP(q3::launch_argmax_finish(m->keys, 1, at<float>(m, y.kARGF), 1, at<int32_t>(m, y.kARGI),
+                                    1, /*init=*/1, id_dst, nullptr, 0, s));
+  }
+  return Q3_OK;
+}
+
+}  // namespace
+
+extern "C" int q3_model_open(void *blob, const q3_layout *lay, void *stream, q3_model **out) {
+  if (!blob || !lay || !out) return Q3_ERR_ARG;
+  *out = nullptr;
+  // Shapes the kernels are written for (hd128 heads, 256-column groups).
+  if (lay->head_dim != 128 || lay->hidden % 256 || lay->inter % 256 || lay->vocab % 128 ||
+      lay->max_seq % kPageTokens || lay->heads % lay->kv_heads || lay->seq == 0)
+    return Q3_ERR_UNSUPPORTED;
+  if (lay->max_seq / kPageTokens > 65536) return Q3_ERR_UNSUPPORTED;
+  q3_model *m = new (std::nothrow) q3_model();
+  if (!m) return Q3_ERR_ARG;
+  m->blob = static_cast<uint8_t *>(blob);
+  m->lay = *lay;
+  m->stream = static_cast<hipStream_t>(stream);
+  m->n_pages = lay->max_seq / kPageTokens;
+  if (hipMalloc(&m->ptab, sizeof(uint16_t) * m->n_pages) != hipSuccess ||
+      hipMalloc(&m->keys, sizeof(unsigned long long) * 8) != hipSuccess) {
+    q3_model_close(m);
+    return Q3_ERR_HIP;
+  }
+  std::vector<uint16_t> tab(m->n_pages);
+  for (uint32_t p = 0; p < m->n_pages; ++p) tab[p] = static_cast<uint16_t>(m->n_pages - 1 - p);
+  if (hipMemcpy(m->ptab, tab.data(), sizeof(uint16_t) * m->n_pages, hipMemcpyHostToDevice) !=
+          hipSuccess ||
+      hipMemset(m->keys, 0, sizeof(unsigned long long) * 8) != hipSuccess) {
+    q3_model_close(m);
+    return Q3_ERR_HIP;
+  }
+  *out = m;
+  return Q3_OK;
+}
+
+extern "C" int q3_model_set_page_table(q3_model *m, const uint16_t *table, uint32_t n) {
+  if (!m || !table || n != m->n_pages) return Q3_ERR_ARG;
+  for (uint32_t i = 0; i < n; ++i)
+    if (table[i] >= m->n_pages) return Q3_ERR_RANGE;
+  Q3_HIP(hipMemcpyAsync(m->ptab, table, sizeof(uint16_t) * n, hipMemcpyHostToDevice, m->stream));
+  Q3_HIP(hipStreamSynchronize(m->stream));
+  return Q3_OK;
+}
+
+extern "C" int q3_forward_chunk(q3_model *m, uint32_t pos, uint32_t rows, int lm_out,
+                                int optimize_tail) {
+  if (!m) return Q3_ERR_ARG;
+  return forward_chunk_impl(m, pos, rows, lm_out, optimize_tail, nullptr);
+}
+
+extern "C" int q3_generate(q3_model *m) {
+  if (!m) return Q3_ERR_ARG;
+  const q3_layout &y = m->lay;
+  int32_t ctrl[4];
+  Q3_HIP(hipMemcpyAsync(ctrl, m->blob + y.kCTRL, sizeof(ctrl), hipMemcpyDeviceToHost, m->stream));
+  Q3_HIP(hipStreamSynchronize(m->stream));
+  const int32_t n_prompt = ctrl[0], n_gen = ctrl[1], mode = ctrl[3];
+  if (mode < 0 || mode > 1) return Q3_ERR_MODE;  // main_big.cpp:346-348
+  if (n_prompt < 0 || n_gen < 0 || static_cast<int64_t>(n_prompt) + n_gen > y.max_seq)
+    return Q3_ERR_RANGE;
+  const bool fused = (mode == 0);
+  const uint32_t total = static_cast<uint32_t>(n_prompt + n_gen);
+  int32_t *ids = at<int32_t>(m, y.kIDS);
+  uint32_t pos = 0;
+  while (pos < total) {
+    const uint32_t np = static_cast<uint32_t>(n_prompt);
+    const uint32_t rows = (pos < np) ? ((np - pos < y.seq) ? np - pos : y.seq) : 1;
+    const bool need_out = (pos + rows >= np);
+    const int lm_out = need_out ? (fused ? Q3_LM_ARGMAX : Q3_LM_LOGITS) : Q3_LM_NONE;
+    const uint32_t next = pos + rows;
+    // the id of the next token goes straight to ids[next] on the device
+    int32_t *id_dst = (need_out && next >= np && next < total) ? ids + next : nullptr;
+    const int rc = forward_chunk_impl(m, pos, rows, lm_out, fused ? 1 : 0, id_dst);
+    if (rc != Q3_OK) return rc;
+    pos = next;
+  }
+  return Q3_OK;
+}
+
+extern "C" int q3_model_close(q3_model *m) {
+  if (!m) return Q3_ERR_ARG;
+  int rc = Q3_OK;
+  if (m->stream || m->ptab) {
+    if (hipStreamSynchronize(m->stream) != hipSuccess) rc = Q3_ERR_HIP;
+  }
+  if (m->ptab) (void)hipFree(m->ptab);
+  if (m->keys) (void)hipFree(m->keys);
+  delete m;
+  return rc;
+}
