@@ -1,0 +1,246 @@
+#!/usr/bin/env python3
+"""Benchmark of the Qwen3 W8A8 forward path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 5] [--warmup 2] [--no-cpu]
+
+Workload (perf leg): the 28-layer Qwen3-0.6B shape with
+random-init int8 weights (per-row scales), one 512-token prefill chunk and
+64 greedy decode steps at batch 1 with the fused lm_head+argmax (CTRL mode
+0), i.e. one q3_generate over CTRL = [512, 64, 640, 0].  One step = that
+whole generation; inputs (weights, prompt ids) are resident in HBM before
+the timed region.  value = (512 + 64) tokens / step time.
+
+Also reported:
+  - prefill and decode rates separately (prefill timed alone through
+    q3_forward_chunk with the same arguments generate uses);
+  - roofline: the dominant kernel, timed live with HIP events on the stream
+    it is launched on, against its algorithmic bytes or ops;
+  - cpu_baseline: the CPU oracle (oracle/, a C port of tools/ref_qwen3.py)
+    running the same generation on the host cores (rank 0 only).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "qwen3-tile-ops_amd"))
+sys.path.insert(0, str(REPO))
+
+METRIC = "tok/s prefill(512)+decode(b=1,64), Qwen3-0.6B W8A8, 1 MI355X; %HBM/MFMA peak"
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+N_PROMPT, N_GEN = 512, 64
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def time_events(fn, reps: int, stream) -> float:
+    """Average milliseconds of fn() over reps, HIP events on `stream`."""
+    import torch
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    fn()
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(reps):
+        fn()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def kernel_rooflines(stream) -> dict:
+    """Times single-kernel shapes of the path through the C ABI, on the
+    stream they are launched on, and derives achieved bandwidth / ops."""
+    import numpy as np
+    import torch
+    from q3ops import ops
+
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(0)
+    res = {}
+
+    def t8(*shape):
+        return torch.from_numpy(rng.integers(-127, 128, shape).astype(np.int8)).to(dev)
+
+    def tf(*shape):
+        return torch.from_numpy(rng.uniform(1e-3, 1e-1, shape).astype(np.float32)).to(dev)
+
+    # rotate over copies so the 256 MB MALL cannot serve repeated reads
+    def copies(nbytes):
+        return max(1, min(8, int(2.0e9 // max(nbytes, 1))))
+
+    # lm_head fused argmax GEMV: M=1, N=151936, K=1024 (decode, HBM bound)
+    V, H = 151936, 1024
+    nb = V * H
+    ws = [(t8(V, H), tf(V)) for _ in range(copies(nb))]
+    a, as_ = t8(1, H), tf(1, H // 256)
+    best = torch.empty(1, dtype=torch.float32, device=dev)
+    bidx = torch.empty(1, dtype=torch.int32, device=dev)
+    it = [0]
+
+    def lm():
+        w, s = ws[it[0] % len(ws)]
+        it[0] += 1
+        ops.gemm_nt_group_argmax(a, as_, w, s, best, bidx, 256, stream=stream)
+
+    ms = time_events(lm, 20, stream)
+    byts = V * H + 4 * V + H + 4 * (H // 256) + 8
+    res["lm_argmax_gemv"] = {"ms": ms, "bytes": byts, "GBs": byts / ms / 1e6, "bound": "hbm"}
+    del ws
+
+    # decode gate/up GEMV (M=1, N=3072 x2, K=1024): HBM bound
+    I = 3072
+    ws = [(t8(I, H), tf(I), t8(I, H), tf(I)) for _ in range(copies(2 * I * H))]
+    s8 = torch.empty((1, I), dtype=torch.int8, device=dev)
+    ss = torch.empty((1, I // 256), dtype=torch.float32, device=dev)
+
+    def gu1():
+        wg, wgs, wu, wus = ws[it[0] % len(ws)]
+        it[0] += 1
+        ops.gemm_gate_up_swiglu_quant(a, as_, wg, wgs, wu, wus, s8, ss, 256, stream=stream)
+
+    ms = time_events(gu1, 50, stream)
+    byts = 2 * I * H + 8 * I + H + 16 + I + 4 * (I // 256)
+    res["gate_up_gemv_m1"] = {"ms": ms, "bytes": byts, "GBs": byts / ms / 1e6, "bound": "hbm"}
+    del ws
+
+    # prefill gate/up GEMM (M=512): the largest prefill GEMM
+    M = 512
+    a5, as5 = t8(M, H), tf(M, H // 256)
+    wg, wgs, wu, wus = t8(I, H), tf(I), t8(I, H), tf(I)
+    s85 = torch.empty((M, I), dtype=torch.int8, device=dev)
+    ss5 = torch.empty((M, I // 256), dtype=torch.float32, device=dev)
+    ms = time_events(lambda: ops.gemm_gate_up_swiglu_quant(a5, as5, wg, wgs, wu, wus, s85, ss5, 256,
+                                                           stream=stream), 20, stream)
+    flops = 2 * M * (2 * I) * H
+    res["gate_up_gemm_m512"] = {"ms": ms, "ops": flops, "TOPs": flops / ms / 1e9, "bound": "mfma"}
+    return res
+
+
+def cpu_baseline(threads: int) -> dict:
+    import numpy as np
+    import oracle
+    from q3ops.layout import CONFIGS, Layout, init_random_blob
+
+    shape, init = CONFIGS["cfg3_perf"]
+    lay = Layout(shape)
+    blob = init_random_blob(lay, init)
+    oracle.set_threads(threads)
+    om = oracle.OracleModel(blob, lay.offsets, dict(shape.__dict__))
+    ids = lay.global_views(blob)["ids"]
+    t0 = time.perf_counter()
+    _, gen, _, _ = om.generate(ids, N_PROMPT, N_GEN, record=False)
+    dt = time.perf_counter() - t0
+    return {"value": (N_PROMPT + N_GEN) / dt, "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": (f"the full workload once: oracle/ C port of tools/ref_qwen3.py, "
+                       f"512-token prefill + 64 greedy decode steps, {dt:.1f} s, "
+                       f"{threads} OpenMP threads"),
+            "generated_head": [int(v) for v in np.asarray(gen)[:8]]}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-roofline", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (this build has no multi-GPU path); "
+              f"got --gpus {args.gpus}", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+    from q3ops import LM_ARGMAX
+    from q3ops.layout import CONFIGS, Layout, init_random_blob
+    from q3ops.model import Model
+
+    assert torch.cuda.is_available(), "bench.py needs a ROCm device"
+    torch.cuda.set_device(0)
+    shape, init = CONFIGS["cfg3_perf"]
+    lay = Layout(shape)
+    log(f"writing random-init blob ({lay.size / 1e9:.2f} GB) ...")
+    blob = init_random_blob(lay, init)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        m = Model(lay, blob, stream=stream)
+    m.set_ctrl(N_PROMPT, N_GEN, 0)
+    torch.cuda.synchronize()
+    log("warmup ...")
+    for _ in range(args.warmup):
+        m.generate()
+    torch.cuda.synchronize()
+
+    log(f"timing {args.steps} steps ...")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        m.generate()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    gen_ids = m.ids()[N_PROMPT:N_PROMPT + N_GEN]
+
+    # prefill alone (the first chunk of generate), HIP events on the model stream
+    prefill_ms = time_events(lambda: m.forward_chunk(0, N_PROMPT, LM_ARGMAX, True),
+                             max(3, args.steps), stream)
+    step_ms = dt * 1e3
+    decode_ms = max(step_ms - prefill_ms, 1e-9) / N_GEN
+    out = {
+        "metric": METRIC,
+        "value": (N_PROMPT + N_GEN) / dt,
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": step_ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (random-init weights N(0,0.02) int8 per-row, uniform prompt ids)",
+        "config": {"workload": "cfg3 perf: 28-layer Qwen3-0.6B shape, one 512-token prefill "
+                               "chunk + 64 greedy decode steps (b=1), fused lm_head+argmax",
+                   "prefill_tokens": N_PROMPT, "decode_tokens": N_GEN, "chunk": shape.seq,
+                   "max_seq": shape.max_seq},
+        "prefill_ms": prefill_ms,
+        "prefill_tok_s": N_PROMPT / (prefill_ms / 1e3),
+        "decode_ms_per_token": decode_ms,
+        "decode_tok_s": 1e3 / decode_ms,
+        "generated_head": [int(v) for v in gen_ids[:8]],
+    }
+    m.close()
+    del m
+    torch.cuda.synchronize()
+
+    if not args.no_roofline:
+        log("kernel rooflines ...")
+        kr = kernel_rooflines(stream)
+        out["kernels"] = kr
+        dom = kr["lm_argmax_gemv"]
+        out["roofline"] = {"kernel": "lm_argmax_gemv (M=1, N=151936, K=1024)", "bound": "hbm",
+                           "achieved": dom["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                           "frac": dom["GBs"] / HBM_PEAK_GBS, "traffic": None,
+                           "avg_ms": dom["ms"], "bytes_per_launch": dom["bytes"]}
+    if not args.no_cpu:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        log(f"cpu baseline ({threads} threads) ...")
+        cb = cpu_baseline(threads)
+        cb_ok = cb.pop("generated_head") == out["generated_head"]
+        cb["matches_gpu_ids"] = bool(cb_ok)
+        out["cpu_baseline"] = cb
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -114,10 +114,16 @@ __device__ __forceinline__ float max64(float v) {
 
 // RMSNorm factor from the ordered 32-column block sums (ref_qwen3.py:161-170):
 // ss = (((0 + b0) + b1) + ...) * inv + eps, then 1 / sqrt(ss).
+// sqrt here must be the correctly rounded one: __builtin_sqrtf lowers to
+// v_sqrt_f32 plus an FMA residual correction, whereas HIP's __fsqrt_rn is
+// the bare approximate v_sqrt_f32 unless OCML_BASIC_ROUNDED_OPERATIONS is
+// defined.
+__device__ __forceinline__ float sqrt_rn(float x) { return __builtin_sqrtf(x); }
+
 __device__ __forceinline__ float rms_factor(float ss, float inv) {
   ss = __fmul_rn(ss, inv);
   ss = __fadd_rn(ss, 1e-6f);
-  return __fdiv_rn(1.0f, __fsqrt_rn(ss));
+  return __fdiv_rn(1.0f, sqrt_rn(ss));
 }
 
 // One 128-wide head row held by a wave as t0 = x[lane], t1 = x[lane + 64]:

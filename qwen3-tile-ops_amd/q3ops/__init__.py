@@ -17,10 +17,8 @@ from .layout import (CONFIGS, InitConfig, Layout, ModelShape, init_random_blob, 
 
 
 def __getattr__(name):
-    if name in ("Model",):
-        from .model import Model
-        return Model
-    if name == "ops":
-        from . import ops
-        return ops
+    # torch is only needed by the device-side modules: import them lazily
+    if name == "Model":
+        import importlib
+        return importlib.import_module(".model", __name__).Model
     raise AttributeError(name)

@@ -47,14 +47,38 @@ def paged_kv(k: torch.Tensor, v: torch.Tensor, ks: torch.Tensor, vs: torch.Tenso
              table: torch.Tensor, page_tokens: int = 32) -> PagedKV:
     """kernels/kv_pages.h:13-24.  k/v: [pages, page_tokens, kv_dim] int8,
     ks/vs: [pages, page_tokens, kv_heads] f32, table: int16/uint16-compatible
-    logical->physical map on the device."""
-    assert k.dtype == torch.int8 and ks.dtype == torch.float32 and k.is_contiguous()
-    assert table.dtype in (torch.int16, torch.uint16) and table.is_cuda
+    logical->physical map on the device.
+
+    The returned struct holds only device addresses, so it also keeps the
+    five tensors alive (a freed table would be reallocated under the
+    kernel's feet).  Every table entry is checked against the page count,
+    because the C ABI, like the reference PagedKV, carries no page count."""
+    for t in (k, v, ks, vs):
+        assert t.is_cuda and t.is_contiguous()
+    assert k.dtype == torch.int8 and v.dtype == torch.int8
+    assert ks.dtype == torch.float32 and vs.dtype == torch.float32
+    assert table.dtype in (torch.int16, torch.uint16) and table.is_cuda and table.is_contiguous()
+    n_pages = k.shape[0]
+    assert v.shape[0] == n_pages and ks.shape[0] == n_pages and vs.shape[0] == n_pages
+    tab = table.cpu().numpy().view("uint16")
+    if tab.size and int(tab.max()) >= n_pages:
+        raise ValueError(f"page table entry {int(tab.max())} >= {n_pages} pages")
     kv_dim = k.shape[-1]
     kv_heads = ks.shape[-1]
-    return PagedKV(k.data_ptr(), v.data_ptr(), ks.data_ptr(), vs.data_ptr(), table.data_ptr(),
-                   page_tokens, page_tokens * kv_dim, kv_dim, page_tokens * kv_heads * 4,
-                   kv_heads * 4)
+    kv = PagedKV(k.data_ptr(), v.data_ptr(), ks.data_ptr(), vs.data_ptr(), table.data_ptr(),
+                 page_tokens, page_tokens * kv_dim, kv_dim, page_tokens * kv_heads * 4,
+                 kv_heads * 4)
+    kv._keep = (k, v, ks, vs, table)
+    kv.n_pages = n_pages
+    kv.n_logical = table.numel()
+    return kv
+
+
+def _check_tokens(kv: PagedKV, end_token: int) -> None:
+    n_logical = getattr(kv, "n_logical", None)
+    if n_logical is not None and end_token > n_logical * kv.page_tokens:
+        raise ValueError(f"token {end_token - 1} is beyond the page table "
+                         f"({n_logical} pages of {kv.page_tokens})")
 
 
 def embedding_rmsnorm_rows(table, scale, ids, tmp, w, out, inv, stream=None):
@@ -89,6 +113,7 @@ def gemm_nt_group_kv_paged(a, a_scale, b, b_scale, group_k, kv: PagedKV, pos0, i
                            cos=None, sin=None, inv_hd=0.0, stream=None):
     """K/V epilogues of gemm_nt_group_store writing page slots
     (main_big.cpp:185-209)."""
+    _check_tokens(kv, pos0 + a.shape[0])
     check(lib().q3_gemm_nt_group_kv_paged(view(a), view(a_scale), view(b), view(b_scale),
                                           group_k, C.byref(kv), pos0, int(is_v), view(nw),
                                           view(cos), view(sin), C.c_float(inv_hd),
@@ -105,6 +130,7 @@ def norm_rope_quant_heads(x, w, cos, sin, q8, scale, heads, inv_hd, do_rope=True
 def attention_heads_gqa_tokscale_paged(q8, q_scale, kv: PagedKV, kv_len, o8, os, heads,
                                        kv_heads, head_dim, causal, qk_scale, stream=None):
     """kernels/attention_gqa.h:549-572."""
+    _check_tokens(kv, kv_len)
     check(lib().q3_attention_heads_gqa_tokscale_paged(view(q8), view(q_scale), C.byref(kv),
                                                       kv_len, view(o8), view(os), heads,
                                                       kv_heads, head_dim, int(causal),

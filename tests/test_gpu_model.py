@@ -1,0 +1,177 @@
+"""GPU model path (q3_forward_chunk / q3_generate through the C ABI) against
+the reference goldens of tools/ref_qwen3.py and against the oracle."""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import bits_equal, describe_diff
+from paritylib import compare_stage, load_cfg, sha
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+from q3ops import LM_ARGMAX, LM_LOGITS, LM_NONE  # noqa: E402
+from q3ops.layout import CONFIGS, InitConfig, Layout, ModelShape, init_random_blob  # noqa: E402
+from q3ops.model import Model  # noqa: E402
+
+_cache = {}
+
+
+def note(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def host_blob(name: str, shape: ModelShape | None = None, init: InitConfig | None = None):
+    key = (name, shape, init)
+    if key not in _cache:
+        s0, i0 = CONFIGS[name]
+        lay = Layout(shape or s0)
+        _cache[key] = (lay, init_random_blob(lay, init or i0))
+    return _cache[key]
+
+
+def stage_problems(g, prefix, m: Model, rows: int, kv_len: int, layer: int,
+                   last_row_only: bool) -> list[str]:
+    probs = []
+    sel = slice(rows - 1, rows) if last_row_only else None
+    for st in ("h", "h8", "hs", "x", "s8", "ss", "o8", "os", "q8", "qs"):
+        if last_row_only and st in ("q8", "qs"):
+            continue  # row 0 doubles as the final-norm scratch (compare.py:49-51)
+        got = m.stage(st, rows)
+        if st in ("q8", "qs") and not last_row_only:
+            # compare.py:197-205: row 0 of q8/qs is reused by the final norm
+            got, gold_rows = got[1:], slice(1, None)
+            spec = f"{prefix}{st}"
+            if spec in g.files:
+                exp = g[spec][1:]
+                if not bits_equal(got, exp):
+                    probs.append(f"{prefix}{st}: {describe_diff(got, exp)}")
+            continue
+        p = compare_stage(g, prefix, st, got, rows=sel)
+        if p:
+            probs.append(p)
+    caches = m.kv_cache(layer, kv_len)
+    for st in ("kc", "ks", "vc", "vs"):
+        p = compare_stage(g, prefix, st, caches[st])
+        if p:
+            probs.append(p)
+    return probs
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_cfg0_generate(cuda, mode, gold_meta):
+    note(f"cfg0 generate mode={mode}")
+    lay, blob = host_blob("cfg0")
+    assert sha(blob[lay["kEMB"]:lay["kLOGITS"]]) == gold_meta["cfg0"]["weights_sha256"]
+    g = load_cfg("cfg0")
+    m = Model(lay, blob)
+    m.set_ctrl(40, 2, mode)
+    m.generate()
+    ids = m.ids()
+    assert np.array_equal(ids[40:42], g["generated"]), (ids[40:42], g["generated"])
+    gl = g["logits"]
+    if mode == 1:
+        got = m.stage("logits", 1)[0]
+        assert bits_equal(got, gl), describe_diff(got, gl)
+    else:
+        best, idx = m.argmax()
+        assert idx == int(np.argmax(gl)) and bits_equal(np.float32(best), gl.max())
+    last = int(g["n_forwards_with_logits"]) - 1
+    probs = stage_problems(g, f"f{last}_", m, 1, 42, 0, last_row_only=(mode == 0))
+    m.close()
+    assert not probs, probs
+
+
+def test_cfg0_each_forward(cuda):
+    """forward_chunk step by step, non-fused (all rows of the last layer):
+    every recorded stage of every forward, bit for bit.  Chunk 0 runs with
+    logits on so its last layer is computed in full (with Q3_LM_NONE the
+    device stops the last layer after the K/V writes, main_big.cpp:212-220,
+    which is covered by the generate tests); the reference has no logits
+    for chunk 0, so only its stages are compared."""
+    lay, blob = host_blob("cfg0")
+    g = load_cfg("cfg0")
+    m = Model(lay, blob)
+    ids = np.array(g["ids_in"], np.int32).copy()
+    ids[40:] = g["generated"]
+    m.set_ids(ids)
+    for pos, rows, lm, prefix in ((0, 32, LM_LOGITS, "c0_"), (32, 8, LM_LOGITS, "f0_"),
+                                  (40, 1, LM_LOGITS, "f1_"), (41, 1, LM_LOGITS, "f2_")):
+        note(f"cfg0 forward pos={pos} rows={rows}")
+        m.forward_chunk(pos, rows, lm, optimize_tail=False)
+        probs = stage_problems(g, prefix, m, rows, pos + rows, 0, last_row_only=False)
+        if f"{prefix}logits" in g.files:
+            got = m.stage("logits", 1)[0]
+            gl = g[f"{prefix}logits"].reshape(-1)
+            if not bits_equal(got, gl):
+                probs.append(f"{prefix}logits: {describe_diff(got, gl)}")
+        assert not probs, (prefix, probs)
+    m.close()
+
+
+def test_cfg0_nonfinal_chunk_writes_kv_only(cuda):
+    """Q3_LM_NONE on the last layer: K/V rows are written (bit-exact with the
+    reference cache) and the tail is skipped."""
+    lay, blob = host_blob("cfg0")
+    g = load_cfg("cfg0")
+    m = Model(lay, blob)
+    m.forward_chunk(0, 32, LM_NONE)
+    caches = m.kv_cache(0, 32)
+    probs = [p for st in ("kc", "ks", "vc", "vs")
+             if (p := compare_stage(g, "c0_", st, caches[st]))]
+    m.close()
+    assert not probs, probs
+
+
+def test_cfg0_chunk_and_page_invariance(cuda):
+    """One 40-row chunk (seq=64 layout, same weights) and a shuffled page
+    table give the reference's ids and logits."""
+    g = load_cfg("cfg0")
+    shape = ModelShape(layers=1, vocab=1024, seq=64, max_seq=256)
+    lay, blob = host_blob("cfg0", shape=shape)
+    m = Model(lay, blob)
+    rng = np.random.default_rng(3)
+    tab = np.arange(lay.max_seq // 32, dtype=np.uint16)
+    rng.shuffle(tab)
+    m.set_page_table(tab)
+    m.set_ctrl(40, 2, 1)
+    m.generate()
+    assert np.array_equal(m.ids()[40:42], g["generated"])
+    got = m.stage("logits", 1)[0]
+    assert bits_equal(got, g["logits"]), describe_diff(got, g["logits"])
+    m.close()
+
+
+def test_cfg2_full_depth(cuda, gold_meta):
+    note("cfg2 28 layers, 32-token prefill, mode 1")
+    lay, blob = host_blob("cfg2")
+    assert sha(blob[lay["kEMB"]:lay["kLOGITS"]]) == gold_meta["cfg2"]["weights_sha256"]
+    g = load_cfg("cfg2")
+    m = Model(lay, blob)
+    m.generate()
+    got = m.stage("logits", 1)[0]
+    assert bits_equal(got, g["logits"]), describe_diff(got, g["logits"])
+    probs = stage_problems(g, "f0_", m, 32, 32, lay.layers - 1, last_row_only=False)
+    m.close()
+    assert not probs, probs
+
+
+def test_cfg3_greedy(cuda, gold_meta):
+    note("cfg3 28 layers, 15-token prompt + 6 greedy tokens, mode 0")
+    lay, blob = host_blob("cfg3")
+    g = load_cfg("cfg3")
+    m = Model(lay, blob)
+    m.generate()
+    ids = m.ids()
+    assert np.array_equal(ids[15:21], g["generated"]), (ids[15:21], g["generated"])
+    best, idx = m.argmax()
+    gl = g["logits"]
+    assert idx == int(np.argmax(gl)) and bits_equal(np.float32(best), gl.max())
+    last = int(g["n_forwards_with_logits"]) - 1
+    probs = stage_problems(g, f"f{last}_", m, 1, 21, lay.layers - 1, last_row_only=True)
+    m.close()
+    assert not probs, probs

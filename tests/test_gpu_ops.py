@@ -1,0 +1,344 @@
+"""GPU parity of every operator, called through the C ABI, against the CPU
+oracle (and the reference goldens where they exist).  Integer stages and
+f32 stages are both required to be bit-exact."""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import bits_equal, describe_diff, golden
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+from q3ops import ops  # noqa: E402
+
+F = np.float32
+QK = F(0.08838834764831845)
+
+
+def dev(a: np.ndarray):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t) -> np.ndarray:
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def note(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def rand_gemm(rng, M, K, N, group):
+    a = rng.integers(-127, 128, (M, K)).astype(np.int8)
+    b = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    as_ = rng.uniform(1e-3, 1e-1, (M, K // group)).astype(F)
+    bs = rng.uniform(1e-3, 1e-1, N).astype(F)
+    return a, as_, b, bs
+
+
+SHAPES = [(1024, 2048, 256), (1024, 1024, 256), (1024, 6144, 256), (3072, 1024, 256),
+          (2048, 1024, 128)]
+
+
+@pytest.mark.parametrize("M", [1, 5, 32, 512])
+@pytest.mark.parametrize("K,N,group", SHAPES)
+def test_gemm_store(cuda, M, K, N, group):
+    note(f"gemm store M={M} K={K} N={N} g={group}")
+    rng = np.random.default_rng(M * 7 + K + N)
+    a, as_, b, bs = rand_gemm(rng, M, K, N, group)
+    out = torch.zeros((M, N), dtype=torch.float32, device=cuda)
+    ops.gemm_nt_group_store(dev(a), dev(as_), dev(b), dev(bs), out, group)
+    ref = oracle.gemm_nt_group(a, as_, b, bs, group)
+    got = host(out)
+    assert bits_equal(got, ref), describe_diff(got, ref)
+
+
+def test_gemm_2048_rows(cuda):
+    note("gemm store M=2048 K=3072 N=1024")
+    rng = np.random.default_rng(99)
+    a, as_, b, bs = rand_gemm(rng, 2048, 3072, 1024, 256)
+    out = torch.zeros((2048, 1024), dtype=torch.float32, device=cuda)
+    ops.gemm_nt_group_store(dev(a), dev(as_), dev(b), dev(bs), out, 256)
+    ref = oracle.gemm_nt_group(a, as_, b, bs, 256)
+    got = host(out)
+    assert bits_equal(got, ref), describe_diff(got, ref)
+
+
+def test_gemm_golden_guest_fixture(cuda):
+    g = golden("ops.npz")
+    for group, key, ns in ((128, "gg_out128", 2), (256, "gg_out256", 1)):
+        out = torch.zeros((32, 128), dtype=torch.float32, device=cuda)
+        ops.gemm_nt_group_store(dev(g["gg_a"]), dev(np.ones((32, ns), F)), dev(g["gg_b"]),
+                                dev(np.ones(128, F)), out, group)
+        got = host(out)
+        assert bits_equal(got, g[key]), describe_diff(got, g[key])
+
+
+@pytest.mark.parametrize("M", [1, 7, 64])
+def test_gemm_residual_add(cuda, M):
+    rng = np.random.default_rng(M)
+    a, as_, b, bs = rand_gemm(rng, M, 2048, 1024, 128)
+    x = rng.normal(size=(M, 1024)).astype(F)
+    xt = dev(x)
+    ops.gemm_nt_group_store(dev(a), dev(as_), dev(b), dev(bs), None, 128, add=xt)
+    ref = (x + oracle.gemm_nt_group(a, as_, b, bs, 128)).astype(F)
+    got = host(xt)
+    assert bits_equal(got, ref), describe_diff(got, ref)
+
+
+@pytest.mark.parametrize("M", [1, 9, 40])
+def test_gemm_head_quant(cuda, M):
+    """V epilogue: per-head int8 quant (group_gemm.h:173-193)."""
+    rng = np.random.default_rng(10 + M)
+    a, as_, b, bs = rand_gemm(rng, M, 1024, 1024, 256)
+    q8 = torch.zeros((M, 1024), dtype=torch.int8, device=cuda)
+    qs = torch.zeros((M, 8), dtype=torch.float32, device=cuda)
+    ops.gemm_nt_group_store(dev(a), dev(as_), dev(b), dev(bs), None, 256, q8=q8, qs=qs)
+    rq, rs = oracle.quant_rows_heads(oracle.gemm_nt_group(a, as_, b, bs, 256), 128)
+    assert bits_equal(host(q8), rq), describe_diff(host(q8), rq)
+    assert bits_equal(host(qs), rs)
+
+
+def nrq_ref(x, nw, cos, sin, heads):
+    out = x.copy()
+    for h in range(heads):
+        hx = oracle.rmsnorm_rows(x[:, h * 128:(h + 1) * 128], nw, F(1 / 128))
+        out[:, h * 128:(h + 1) * 128] = oracle.rope_head_hd(hx, cos, sin)
+    return oracle.quant_rows_heads(out, 128)
+
+
+@pytest.mark.parametrize("M", [1, 13, 32])
+def test_gemm_norm_rope_quant(cuda, M):
+    """Q/K epilogue: head RMSNorm + RoPE + quant (norm_rope_quant.h:17-86)."""
+    rng = np.random.default_rng(20 + M)
+    a, as_, b, bs = rand_gemm(rng, M, 1024, 2048, 256)
+    nw = (1 + 0.05 * rng.normal(size=128)).astype(F)
+    ang = rng.uniform(0, 100, (M, 64))
+    cos, sin = np.cos(ang).astype(F), np.sin(ang).astype(F)
+    q8 = torch.zeros((M, 2048), dtype=torch.int8, device=cuda)
+    qs = torch.zeros((M, 16), dtype=torch.float32, device=cuda)
+    ops.gemm_nt_group_store(dev(a), dev(as_), dev(b), dev(bs), None, 256, q8=q8, qs=qs,
+                            nw=dev(nw), cos=dev(cos), sin=dev(sin), inv_hd=F(1 / 128))
+    rq, rs = nrq_ref(oracle.gemm_nt_group(a, as_, b, bs, 256), nw, cos, sin, 16)
+    assert bits_equal(host(q8), rq), describe_diff(host(q8), rq)
+    assert bits_equal(host(qs), rs), describe_diff(host(qs), rs)
+
+
+def test_norm_rope_quant_heads_unfused(cuda):
+    rng = np.random.default_rng(30)
+    x = rng.normal(size=(6, 1024)).astype(F)
+    nw = (1 + 0.05 * rng.normal(size=128)).astype(F)
+    ang = rng.uniform(0, 100, (6, 64))
+    cos, sin = np.cos(ang).astype(F), np.sin(ang).astype(F)
+    q8 = torch.zeros((6, 1024), dtype=torch.int8, device=cuda)
+    qs = torch.zeros((6, 8), dtype=torch.float32, device=cuda)
+    ops.norm_rope_quant_heads(dev(x), dev(nw), dev(cos), dev(sin), q8, qs, 8, F(1 / 128), True)
+    rq, rs = nrq_ref(x, nw, cos, sin, 8)
+    assert bits_equal(host(q8), rq) and bits_equal(host(qs), rs)
+
+
+def make_pages(rng, kv_len, kv_dim, kv_heads, n_pages, shuffle=True):
+    table = np.arange(n_pages, dtype=np.uint16)
+    if shuffle:
+        rng.shuffle(table)
+    k8 = rng.integers(-127, 128, (kv_len, kv_dim)).astype(np.int8)
+    v8 = rng.integers(-127, 128, (kv_len, kv_dim)).astype(np.int8)
+    ks = rng.uniform(1e-3, 5e-2, (kv_len, kv_heads)).astype(F)
+    vs = rng.uniform(1e-3, 5e-2, (kv_len, kv_heads)).astype(F)
+    kp = rng.integers(-127, 128, (n_pages, 32, kv_dim)).astype(np.int8)  # garbage elsewhere
+    vp = rng.integers(-127, 128, (n_pages, 32, kv_dim)).astype(np.int8)
+    ksp = np.full((n_pages, 32, kv_heads), np.nan, F)
+    vsp = np.full((n_pages, 32, kv_heads), np.nan, F)
+    t = np.arange(kv_len)
+    kp[table[t // 32], t % 32] = k8
+    vp[table[t // 32], t % 32] = v8
+    ksp[table[t // 32], t % 32] = ks
+    vsp[table[t // 32], t % 32] = vs
+    return (k8, v8, ks, vs), (kp, vp, ksp, vsp, table)
+
+
+@pytest.mark.parametrize("rows,kv_len", [(1, 1), (1, 33), (1, 600), (4, 80), (8, 48),
+                                         (40, 40), (33, 97), (512, 512)])
+def test_attention_paged(cuda, rows, kv_len):
+    note(f"attention rows={rows} kv_len={kv_len}")
+    rng = np.random.default_rng(rows * 1000 + kv_len)
+    heads, kvh = 16, 8
+    n_pages = (kv_len + 31) // 32 + 3
+    (k8, v8, ks, vs), (kp, vp, ksp, vsp, table) = make_pages(rng, kv_len, kvh * 128, kvh, n_pages)
+    q8 = rng.integers(-127, 128, (rows, heads * 128)).astype(np.int8)
+    qs = rng.uniform(1e-3, 5e-2, (rows, heads)).astype(F)
+    tk, tv, tks, tvs, tt = dev(kp), dev(vp), dev(ksp), dev(vsp), dev(table.view(np.int16))
+    kv = ops.paged_kv(tk, tv, tks, tvs, tt)
+    o8 = torch.zeros((rows, heads * 128), dtype=torch.int8, device=cuda)
+    os_ = torch.zeros((rows, heads), dtype=torch.float32, device=cuda)
+    ops.attention_heads_gqa_tokscale_paged(dev(q8), dev(qs), kv, kv_len, o8, os_, heads, kvh, 128,
+                                           True, QK)
+    attn = oracle.attention_heads_gqa_tokscale(q8, qs, k8, ks, v8, vs, heads, kvh, 128, True, QK)
+    ro8, ros = oracle.quant_rows_heads(attn, 128)
+    assert bits_equal(host(o8), ro8), describe_diff(host(o8), ro8)
+    assert bits_equal(host(os_), ros), describe_diff(host(os_), ros)
+
+
+@pytest.mark.parametrize("case,rows,kv_len", [("pa", 4, 80), ("pm1", 8, 48)])
+def test_attention_guest_fixture(cuda, case, rows, kv_len):
+    """The reference's paged-attention guest inputs (4 heads / 2 kv heads,
+    shuffled page table as in paged_attn.cpp) against its golden outputs."""
+    g = golden("ops.npz")
+    n_pages = (kv_len + 31) // 32
+    table = np.array([2, 0, 1] if n_pages == 3 else list(range(n_pages))[::-1], np.uint16)
+    kd = 2 * 128
+    kp = np.zeros((n_pages, 32, kd), np.int8)
+    vp = np.zeros_like(kp)
+    ksp = np.zeros((n_pages, 32, 2), F)
+    vsp = np.zeros_like(ksp)
+    t = np.arange(kv_len)
+    kp[table[t // 32], t % 32] = g[f"{case}_k8"]
+    vp[table[t // 32], t % 32] = g[f"{case}_v8"]
+    ksp[table[t // 32], t % 32] = g[f"{case}_ks"]
+    vsp[table[t // 32], t % 32] = g[f"{case}_vs"]
+    kv = ops.paged_kv(dev(kp), dev(vp), dev(ksp), dev(vsp), dev(table.view(np.int16)))
+    o8 = torch.zeros((rows, 512), dtype=torch.int8, device=cuda)
+    os_ = torch.zeros((rows, 4), dtype=torch.float32, device=cuda)
+    ops.attention_heads_gqa_tokscale_paged(dev(g[f"{case}_q8"]), dev(g[f"{case}_qs"]), kv, kv_len,
+                                           o8, os_, 4, 2, 128, True, QK)
+    assert bits_equal(host(o8), g[f"{case}_o8"]), describe_diff(host(o8), g[f"{case}_o8"])
+    assert bits_equal(host(os_), g[f"{case}_os"])
+
+
+def test_kv_paged_epilogues(cuda):
+    """K (norm+RoPE) and V rows written into shuffled pages from a chunk that
+    starts mid-page and crosses two page boundaries."""
+    rng = np.random.default_rng(40)
+    M, pos0, n_pages = 70, 21, 6
+    a, as_, bk, bks = rand_gemm(rng, M, 1024, 1024, 256)
+    _, _, bv, bvs = rand_gemm(rng, M, 1024, 1024, 256)
+    nk = (1 + 0.05 * rng.normal(size=128)).astype(F)
+    ang = rng.uniform(0, 100, (M, 64))
+    cos, sin = np.cos(ang).astype(F), np.sin(ang).astype(F)
+    table = np.array([4, 1, 5, 0, 3, 2], np.uint16)
+    kp = torch.zeros((n_pages, 32, 1024), dtype=torch.int8, device=cuda)
+    vp = torch.zeros_like(kp)
+    ksp = torch.zeros((n_pages, 32, 8), dtype=torch.float32, device=cuda)
+    vsp = torch.zeros_like(ksp)
+    kv = ops.paged_kv(kp, vp, ksp, vsp, dev(table.view(np.int16)))
+    ta, tas = dev(a), dev(as_)
+    ops.gemm_nt_group_kv_paged(ta, tas, dev(bv), dev(bvs), 256, kv, pos0, True)
+    ops.gemm_nt_group_kv_paged(ta, tas, dev(bk), dev(bks), 256, kv, pos0, False, nw=dev(nk),
+                               cos=dev(cos), sin=dev(sin), inv_hd=F(1 / 128))
+    rv8, rvs = oracle.quant_rows_heads(oracle.gemm_nt_group(a, as_, bv, bvs, 256), 128)
+    rk8, rks = nrq_ref(oracle.gemm_nt_group(a, as_, bk, bks, 256), nk, cos, sin, 8)
+    t = pos0 + np.arange(M)
+    pg, sl = table[t // 32], t % 32
+    assert bits_equal(host(vp)[pg, sl], rv8) and bits_equal(host(vsp)[pg, sl], rvs)
+    assert bits_equal(host(kp)[pg, sl], rk8) and bits_equal(host(ksp)[pg, sl], rks)
+    # nothing outside the written slots was touched
+    mask = np.ones((n_pages, 32), bool)
+    mask[pg, sl] = False
+    assert not host(kp)[mask].any() and not host(vsp)[mask].any()
+
+
+@pytest.mark.parametrize("M", [1, 11, 64])
+def test_gate_up_swiglu_quant(cuda, M):
+    rng = np.random.default_rng(50 + M)
+    a, as_, wg, wgs = rand_gemm(rng, M, 1024, 3072, 256)
+    _, _, wu, wus = rand_gemm(rng, M, 1024, 3072, 256)
+    s8 = torch.zeros((M, 3072), dtype=torch.int8, device=cuda)
+    ss = torch.zeros((M, 12), dtype=torch.float32, device=cuda)
+    ops.gemm_gate_up_swiglu_quant(dev(a), dev(as_), dev(wg), dev(wgs), dev(wu), dev(wus), s8, ss,
+                                  256)
+    g = oracle.gemm_nt_group(a, as_, wg, wgs, 256)
+    u = oracle.gemm_nt_group(a, as_, wu, wus, 256)
+    rs8, rss = oracle.quant_rows_heads(oracle.swiglu(g, u), 256)
+    assert bits_equal(host(s8), rs8), describe_diff(host(s8), rs8)
+    assert bits_equal(host(ss), rss), describe_diff(host(ss), rss)
+
+
+def test_gate_up_guest_fixture(cuda):
+    g = golden("ops.npz")
+    s8 = torch.zeros((32, 256), dtype=torch.int8, device=cuda)
+    ss = torch.zeros((32, 1), dtype=torch.float32, device=cuda)
+    ops.gemm_gate_up_swiglu_quant(dev(g["gu_a"]), dev(g["gu_as"]), dev(g["gu_wg"]),
+                                  dev(g["gu_wgs"]), dev(g["gu_wu"]), dev(g["gu_wus"]), s8, ss, 256)
+    assert bits_equal(host(s8), g["gu_s8"]) and bits_equal(host(ss), g["gu_ss"])
+
+
+@pytest.mark.parametrize("N", [1024, 151936])
+def test_lm_argmax(cuda, N):
+    rng = np.random.default_rng(N)
+    a, as_, b, bs = rand_gemm(rng, 1, 1024, N, 256)
+    best = torch.tensor([-3.0e38], dtype=torch.float32, device=cuda)
+    bidx = torch.zeros(1, dtype=torch.int32, device=cuda)
+    ops.gemm_nt_group_argmax(dev(a), dev(as_), dev(b), dev(bs), best, bidx, 256)
+    logits = oracle.gemm_nt_group(a, as_, b, bs, 256)[0]
+    assert int(host(bidx)[0]) == int(np.argmax(logits))
+    assert bits_equal(host(best), logits.max(keepdims=True))
+    # merging into a running (best, idx) that is not beaten keeps it
+    best2 = torch.tensor([1e30], dtype=torch.float32, device=cuda)
+    bidx2 = torch.tensor([-5], dtype=torch.int32, device=cuda)
+    ops.gemm_nt_group_argmax(dev(a), dev(as_), dev(b), dev(bs), best2, bidx2, 256)
+    assert int(host(bidx2)[0]) == -5 and host(best2)[0] == np.float32(1e30)
+
+
+def test_lm_argmax_ties_first_index(cuda):
+    """Duplicate the winning weight row at a later index and an earlier one:
+    the earliest index of the maximum wins."""
+    rng = np.random.default_rng(7)
+    a, as_, b, bs = rand_gemm(rng, 1, 1024, 4096, 256)
+    logits = oracle.gemm_nt_group(a, as_, b, bs, 256)[0]
+    w = int(np.argmax(logits))
+    b[3000] = b[w]
+    bs[3000] = bs[w]
+    b[17] = b[w]
+    bs[17] = bs[w]
+    best = torch.tensor([-3.0e38], dtype=torch.float32, device=cuda)
+    bidx = torch.zeros(1, dtype=torch.int32, device=cuda)
+    ops.gemm_nt_group_argmax(dev(a), dev(as_), dev(b), dev(bs), best, bidx, 256)
+    assert int(host(bidx)[0]) == min(17, w)
+
+
+def test_argmax_logits(cuda):
+    rng = np.random.default_rng(8)
+    v = rng.normal(size=151936).astype(F)
+    v[[100, 5000]] = v.max() + 1
+    out = torch.zeros(4, dtype=torch.int32, device=cuda)
+    ops.argmax_logits(dev(v.reshape(1, -1)), out)
+    assert int(host(out)[0]) == oracle.argmax_logits(v) == 100
+
+
+def test_rows_kernels(cuda):
+    rng = np.random.default_rng(9)
+    V, H, R = 1024, 1024, 37
+    emb = rng.integers(-127, 128, (V, H)).astype(np.int8)
+    es = rng.uniform(1e-4, 1e-3, V).astype(F)
+    ids = rng.integers(0, V, R).astype(np.int32)
+    w = (1 + 0.05 * rng.normal(size=H)).astype(F)
+    tmp = torch.zeros((R, H), dtype=torch.float32, device=cuda)
+    out = torch.zeros((R, H), dtype=torch.float32, device=cuda)
+    ops.embedding_rmsnorm_rows(dev(emb), dev(es), dev(ids.reshape(-1, 1)), tmp, dev(w), out,
+                               F(1 / H))
+    rh, rx = oracle.embedding_rmsnorm(emb, es, ids, w, F(1 / H))
+    assert bits_equal(host(tmp), rx) and bits_equal(host(out), rh), describe_diff(host(out), rh)
+    x = rng.normal(size=(R, H)).astype(F)
+    ops.rmsnorm_rows(dev(x), dev(w), out, F(1 / H))
+    ref = oracle.rmsnorm_rows(x, w, F(1 / H))
+    assert bits_equal(host(out), ref), describe_diff(host(out), ref)
+    for group in (128, 256):
+        q = torch.zeros((R, H), dtype=torch.int8, device=cuda)
+        s = torch.zeros((R, H // group), dtype=torch.float32, device=cuda)
+        ops.quant_rows_heads(dev(x), q, s, group)
+        rq, rs = oracle.quant_rows_heads(x, group)
+        assert bits_equal(host(q), rq) and bits_equal(host(s), rs)
+
+
+def test_quant_guest_fixture(cuda):
+    g = golden("ops.npz")
+    q = torch.zeros((32, 256), dtype=torch.int8, device=cuda)
+    s = torch.zeros((32, 2), dtype=torch.float32, device=cuda)
+    ops.quant_rows_heads(dev(g["qh_x"]), q, s, 128)
+    assert bits_equal(host(q), g["qh_q"]) and bits_equal(host(s), g["qh_s"])
