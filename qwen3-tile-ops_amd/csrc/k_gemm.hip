@@ -198,7 +198,7 @@ __global__ void __launch_bounds__(256) gemm_group_kernel(GemmArgs a) {
           const unsigned long long o = shfl_xor_u64(best, s);
           best = o > best ? o : best;
         }
-        if (lane == 0) atomicMax(a.keys + m, best);
+        if (lane == 0) a.keys[static_cast<int64_t>(m) * a.keys_ld + blockIdx.x] = best;
         continue;
       } else {
         if constexpr (EPI == EPI_NRQ) {
@@ -231,14 +231,30 @@ hipError_t launch_epi(const GemmArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
-__global__ void argmax_finish_kernel(unsigned long long *keys, int M, float *best,
-                                     int64_t best_stride, int32_t *bidx,
-                                     int64_t bidx_stride, int init, int32_t *ids_out,
-                                     const int32_t *pos_dev, int pos_add) {
-  const int m = blockIdx.x * blockDim.x + threadIdx.x;
-  if (m >= M) return;
-  const unsigned long long key = keys[m];
-  keys[m] = 0ull;
+// One workgroup per row: maximum of the row's per-workgroup keys, then the
+// strict `best < value` merge (lm_argmax.h:58-66).
+__global__ void __launch_bounds__(256) argmax_finish_kernel(const unsigned long long *keys,
+                                                            int64_t keys_ld, int nslots, float *best,
+                                                            int64_t best_stride, int32_t *bidx,
+                                                            int64_t bidx_stride, int init,
+                                                            int32_t *ids_out,
+                                                            const int32_t *pos_dev, int pos_add) {
+  __shared__ unsigned long long red[4];
+  const int m = blockIdx.x;
+  unsigned long long key = 0ull;
+  for (int i = threadIdx.x; i < nslots; i += 256) {
+    const unsigned long long k = keys[static_cast<int64_t>(m) * keys_ld + i];
+    key = k > key ? k : key;
+  }
+  for (int s = 1; s < 64; s <<= 1) {
+    const unsigned long long o = shfl_xor_u64(key, s);
+    key = o > key ? o : key;
+  }
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = key;
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  key = red[0];
+  for (int w = 1; w < 4; ++w) key = red[w] > key ? red[w] : key;
   // main_big.cpp:281-290 starts the fused argmax from best = -3e38, bidx = 0
   float b = init ? -3.0e38f : best[m * best_stride];
   int32_t bi = init ? 0 : bidx[m * bidx_stride];
@@ -321,14 +337,13 @@ hipError_t launch_gemm(const GemmArgs &a, hipStream_t s) {
   }
 }
 
-hipError_t launch_argmax_finish(unsigned long long *keys, int M, float *best,
-                                int64_t best_stride, int32_t *bidx,
+hipError_t launch_argmax_finish(const unsigned long long *keys, int64_t keys_ld, int nslots,
+                                int M, float *best, int64_t best_stride, int32_t *bidx,
                                 int64_t bidx_stride, int init, int32_t *ids_out,
-                                const int32_t *pos_dev, int pos_add,
-                                hipStream_t s) {
+                                const int32_t *pos_dev, int pos_add, hipStream_t s) {
   if (M <= 0) return hipSuccess;
-  hipLaunchKernelGGL(argmax_finish_kernel, dim3((M + 63) / 64), dim3(64), 0, s, keys, M,
-                     best, best_stride, bidx, bidx_stride, init, ids_out, pos_dev, pos_add);
+  hipLaunchKernelGGL(argmax_finish_kernel, dim3(M), dim3(256), 0, s, keys, keys_ld, nslots, best,
+                     best_stride, bidx, bidx_stride, init, ids_out, pos_dev, pos_add);
   return hipGetLastError();
 }
 

@@ -1,0 +1,403 @@
+// Decode-shaped group GEMM ("GEMV", M <= 16 rows) across the whole chip.
+//
+// Arithmetic of k_gemm.hip (kernels/group_gemm.h:27-222,
+// ref_qwen3.py:145-158): per K-group an exact int32 MFMA partial, dequant
+// RN(RN(f32(I) * bs[n]) * as[m,g]), groups summed in order from +0.0f.
+//
+// Decomposition: a workgroup owns 16*NT output columns and its 4 waves split
+// the K-groups round-robin; each wave issues all of its weight loads before
+// its MFMAs and parks its dequantised per-group tiles in LDS; then one
+// (row, column) per thread adds the groups in order.  Workgroups never wait
+// for each other: there are no grid-wide dependencies, fences or contended
+// atomics in this kernel.
+//
+// Prologue (consumer-side quantisation): instead of reading a pre-quantised
+// int8 A operand, the workgroup may build it in LDS from f32 rows
+//   PRO_NORM   RMSNorm with gain w (rmsnorm.h:34-81) then per-256 quant
+//   PRO_EMBED  embedding gather + dequant (embedding.h:99-168), then as NORM
+//   PRO_QUANT  per-256 quant only (quant.h:89-138)
+// with the reference's exact rounding points; workgroup 0 also stores the
+// stage buffers (x, h, h8, hs) the reference writes.
+//
+// Epilogues: STORE, ADD (residual, group_gemm.h:194-214), SWIGLU (gate and up
+// rows of the same columns, swiglu_quant.h:195-231, stored as f32 for the
+// next prologue) and ARGMAX (lm_argmax.h:55-67: one (max, first index) key
+// per workgroup and row into a slot array, reduced by argmax_finish).
+#include "q3_device.h"
+#include "q3_kernels.h"
+
+namespace q3 {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ v4i zero4() {
+  v4i z = {0, 0, 0, 0};
+  return z;
+}
+
+__device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v, int m) {
+  const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), m);
+  const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), m);
+  return (static_cast<unsigned long long>(hi) << 32) | lo;
+}
+
+__device__ __forceinline__ uint32_t ordered_key(float v) {
+  uint32_t b = f32_bits(v);
+  if (b == 0x80000000u) b = 0u;
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// ref_qwen3.py:194-200 (exp table staged in LDS).
+__device__ __forceinline__ float swiglu1(float g, float u, const uint64_t *tab) {
+  float e = __fmul_rn(g, -1.0f);
+  e = exp_f32_tab(e, tab);
+  e = __fadd_rn(e, 1.0f);
+  e = __fdiv_rn(1.0f, e);
+  return __fmul_rn(__fmul_rn(g, e), u);
+}
+
+// Builds the int8 A operand of M rows (K columns, 256-column groups) in LDS.
+// Thread layout: wave w walks groups w, w+4, ...; lane l owns columns
+// 4l..4l+3 of the group, so a 32-column RMSNorm block is 8 lanes (the
+// reference's pairwise tree: in-thread pairs, then xor 1/2/4), and a
+// quantisation group is one wave.
+__device__ void gemv_prologue(const GemvArgs &a, int8_t *a_lds, float *as_lds, float *blk) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int K = a.K;
+  const int ngr = K / 256;
+  const int nblk = K / 32;
+  const bool write_stage = blockIdx.x == 0;
+  for (int m = 0; m < a.M; ++m) {
+    int32_t id = 0;
+    bool id_ok = false;
+    if (a.pro == PRO_EMBED) {
+      id = a.ids[m];
+      id_ok = id >= 0 && id < a.vocab;
+    }
+    auto load4 = [&](int c, float v[4]) {
+      if (a.pro == PRO_EMBED) {
+        if (id_ok) {
+          const char4 e = *reinterpret_cast<const char4 *>(a.emb + static_cast<int64_t>(id) * K + c);
+          const float sc = a.emb_s[id];
+          v[0] = __fmul_rn(static_cast<float>(e.x), sc);
+          v[1] = __fmul_rn(static_cast<float>(e.y), sc);
+          v[2] = __fmul_rn(static_cast<float>(e.z), sc);
+          v[3] = __fmul_rn(static_cast<float>(e.w), sc);
+        } else {
+          v[0] = v[1] = v[2] = v[3] = 0.0f;
+        }
+      } else {
+        const float4 x = *reinterpret_cast<const float4 *>(a.x + static_cast<int64_t>(m) * a.ldx + c);
+        v[0] = x.x;
+        v[1] = x.y;
+        v[2] = x.z;
+        v[3] = x.w;
+      }
+    };
+    float rinv = 1.0f;
+    if (a.pro != PRO_QUANT) {
+      for (int g = wave; g < ngr; g += 4) {
+        const int c = g * 256 + 4 * lane;
+        float v[4];
+        load4(c, v);
+        if (a.pro == PRO_EMBED && write_stage && a.x_out)
+          *reinterpret_cast<float4 *>(a.x_out + static_cast<int64_t>(m) * a.ldx + c) =
+              make_float4(v[0], v[1], v[2], v[3]);
+        float s = __fadd_rn(__fadd_rn(__fmul_rn(v[0], v[0]), __fmul_rn(v[1], v[1])),
+                            __fadd_rn(__fmul_rn(v[2], v[2]), __fmul_rn(v[3], v[3])));
+        s = __fadd_rn(s, __shfl_xor(s, 1));
+        s = __fadd_rn(s, __shfl_xor(s, 2));
+        s = __fadd_rn(s, __shfl_xor(s, 4));
+        if ((lane & 7) == 0) blk[g * 8 + (lane >> 3)] = s;
+      }
+      __syncthreads();
+      float ss = 0.0f;
+      for (int b = 0; b < nblk; ++b) ss = __fadd_rn(ss, blk[b]);
+      rinv = rms_factor(ss, a.inv_pre);
+    }
+    for (int g = wave; g < ngr; g += 4) {
+      const int c = g * 256 + 4 * lane;
+      float v[4];
+      load4(c, v);
+      if (a.pro != PRO_QUANT) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = __fmul_rn(__fmul_rn(v[i], rinv), a.w_pre[c + i]);
+        if (write_stage && a.h_out)
+          *reinterpret_cast<float4 *>(a.h_out + static_cast<int64_t>(m) * K + c) =
+              make_float4(v[0], v[1], v[2], v[3]);
+      }
+      float mx = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+      mx = max64(mx);
+      const float scale = __fmul_rn(mx, inv127());
+      char4 q;
+      q.x = static_cast<signed char>(quant1(v[0], scale));
+      q.y = static_cast<signed char>(quant1(v[1], scale));
+      q.z = static_cast<signed char>(quant1(v[2], scale));
+      q.w = static_cast<signed char>(quant1(v[3], scale));
+      *reinterpret_cast<char4 *>(a_lds + m * K + c) = q;
+      if (lane == 0) as_lds[m * ngr + g] = scale;
+      if (write_stage) {
+        if (a.h8_out) *reinterpret_cast<char4 *>(a.h8_out + static_cast<int64_t>(m) * K + c) = q;
+        if (a.hs_out && lane == 0) a.hs_out[static_cast<int64_t>(m) * ngr + g] = scale;
+      }
+    }
+    __syncthreads();  // blk is reused by the next row
+  }
+}
+
+template <int GPW, int KSTEPS, int NT, int NMAT>
+__global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  constexpr int NB = 16 * NT;       // columns per workgroup
+  constexpr int PP = NB + 1;        // partial-tile pitch
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int lr = lane & 15;
+  const int lg = lane >> 4;
+  const int M = a.M;
+  const int K = a.K;
+  const int G = a.group;
+  const int ngroups = K / G;
+  const int n_blk = blockIdx.x * NB;
+  int si = 0;
+  while (si + 1 < a.nseg && n_blk >= a.seg[si + 1].n0) ++si;
+  const GemvSeg &sg = a.seg[si];
+
+  // LDS: partials [NMAT][ngroups][16][PP] f32, then (prologue) A [M][K] i8
+  // and its scales [M][K/256] f32 and 32 block sums
+  float *part = reinterpret_cast<float *>(smem);
+  const int part_floats = NMAT * ngroups * 16 * PP;
+  int8_t *a_lds = reinterpret_cast<int8_t *>(part + part_floats);
+  float *as_lds = reinterpret_cast<float *>(a_lds + ((M * K + 15) & ~15));
+  float *blk = as_lds + M * (K / 256);
+  __shared__ uint64_t exptab[32];
+
+  // weights first: their HBM latency overlaps the prologue below
+  v4i bv[NMAT][NT][GPW][KSTEPS];
+#pragma unroll
+  for (int gi = 0; gi < GPW; ++gi) {
+    const int g = wave + 4 * gi;
+    const bool ok = g < ngroups;
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      const int k = g * G + ks * 64 + lg * 16;
+#pragma unroll
+      for (int mi = 0; mi < NMAT; ++mi)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const int8_t *b = (mi == 0 ? sg.b : sg.b2) +
+                            static_cast<int64_t>(n_blk - sg.n0 + nt * 16 + lr) * K;
+          bv[mi][nt][gi][ks] = ok ? *reinterpret_cast<const v4i *>(b + k) : zero4();
+        }
+    }
+  }
+  if (NMAT == 2 && threadIdx.x < 32) exptab[threadIdx.x] = kExp2Tab[threadIdx.x];
+
+  const int8_t *arow;
+  const float *as;
+  int64_t ldas;
+  if (a.pro != PRO_NONE) {
+    gemv_prologue(a, a_lds, as_lds, blk);
+    arow = a_lds + (lr < M ? lr : 0) * K + lg * 16;
+    as = as_lds;
+    ldas = K / 256;
+  } else {
+    arow = a.a + static_cast<int64_t>(lr < M ? lr : 0) * a.lda + lg * 16;
+    as = a.as;
+    ldas = a.ldas;
+  }
+  const bool avalid = lr < M;
+  v4i av[GPW][KSTEPS];
+#pragma unroll
+  for (int gi = 0; gi < GPW; ++gi) {
+    const int g = wave + 4 * gi;
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks)
+      av[gi][ks] = (g < ngroups && avalid) ? *reinterpret_cast<const v4i *>(arow + g * G + ks * 64)
+                                           : zero4();
+  }
+#pragma unroll
+  for (int gi = 0; gi < GPW; ++gi) {
+    const int g = wave + 4 * gi;
+    if (g >= ngroups) break;
+    float asv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = lg * 4 + i;
+      asv[i] = (m < M) ? as[static_cast<int64_t>(m) * ldas + g] : 0.0f;
+    }
+#pragma unroll
+    for (int mi = 0; mi < NMAT; ++mi)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        v4i acc = zero4();
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks)
+          acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[gi][ks], bv[mi][nt][gi][ks], acc, 0, 0, 0);
+        const int ncol = n_blk - sg.n0 + nt * 16 + lr;
+        const float bsv = (mi == 0 ? sg.bs : sg.bs2)[ncol];
+        float *pt = part + ((mi * ngroups + g) * 16) * PP + nt * 16 + lr;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          pt[(lg * 4 + i) * PP] = __fmul_rn(__fmul_rn(static_cast<float>(acc[i]), bsv), asv[i]);
+      }
+  }
+  __syncthreads();
+
+  // ordered group sums: item = (row m, column j); 16*NB items over 256 threads
+  for (int it = threadIdx.x; it < 16 * NB; it += 256) {
+    const int m = it / NB;
+    const int j = it % NB;
+    float out = 0.0f, out2 = 0.0f;
+    for (int g = 0; g < ngroups; ++g) {
+      out = __fadd_rn(out, part[(g * 16 + m) * PP + j]);
+      if (NMAT == 2) out2 = __fadd_rn(out2, part[((ngroups + g) * 16 + m) * PP + j]);
+    }
+    const int ncol = n_blk - sg.n0 + j;
+    if (sg.epi == EPI_ARGMAX) {
+      unsigned long long key = 0ull;
+      if (m < M)
+        key = (static_cast<unsigned long long>(ordered_key(out)) << 32) |
+              (0xFFFFFFFFu - static_cast<uint32_t>(ncol));
+      // NB consecutive threads share a row when NB <= 64 (wave-aligned)
+#pragma unroll
+      for (int s = 1; s < NB && s < 64; s <<= 1) {
+        const unsigned long long o = shfl_xor_u64(key, s);
+        key = o > key ? o : key;
+      }
+      if (m < M && j == 0) a.keys[static_cast<int64_t>(m) * a.keys_ld + blockIdx.x] = key;
+      continue;
+    }
+    if (m >= M) continue;
+    float *dst = sg.out + static_cast<int64_t>(m) * sg.ldo + ncol;
+    if (sg.epi == EPI_ADD)
+      *dst = __fadd_rn(*dst, out);
+    else if (sg.epi == EPI_SWIGLU)
+      *dst = swiglu1(out, out2, exptab);
+    else
+      *dst = out;
+  }
+}
+
+// Per (row, head) wave: the head epilogues of the Q/K/V projections
+// (kernels/norm_rope_quant.h:17-86, group_gemm.h:173-193), from f32 rows.
+__global__ void __launch_bounds__(256) qkv_heads_kernel(QkvHeadArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int nh = a.q_heads + 2 * a.kv_heads;
+  if (item >= a.M * nh) return;
+  const int m = item / nh;
+  const int h = item % nh;
+  const float *src;
+  QDest d;
+  int head;
+  bool nrq;
+  const float *nw;
+  const float *cs;
+  const float *sn;
+  if (h < a.q_heads) {
+    src = a.q + static_cast<int64_t>(m) * a.ldq + h * 128;
+    d = a.qd;
+    head = h;
+    nrq = true;
+    nw = a.nq;
+    cs = a.cos_q;
+    sn = a.sin_q;
+  } else if (h < a.q_heads + a.kv_heads) {
+    head = h - a.q_heads;
+    src = a.k + static_cast<int64_t>(m) * a.ldk + head * 128;
+    d = a.kd;
+    nrq = true;
+    nw = a.nk;
+    cs = a.cos_k;
+    sn = a.sin_k;
+  } else {
+    head = h - a.q_heads - a.kv_heads;
+    src = a.v + static_cast<int64_t>(m) * a.ldk + head * 128;
+    d = a.vd;
+    nrq = false;
+    nw = nullptr;
+    cs = sn = nullptr;
+  }
+  float t0 = src[lane], t1 = src[lane + 64];
+  if (nrq)
+    head_norm_rope(t0, t1, lane, nw, 1, cs + static_cast<int64_t>(m) * a.ld_cs,
+                   sn + static_cast<int64_t>(m) * a.ld_cs, a.inv_hd, true);
+  const float mx = max64(fmaxf(fabsf(t0), fabsf(t1)));
+  const float scale = __fmul_rn(mx, inv127());
+  int8_t *row8;
+  float *sp;
+  if (d.table) {
+    const uint32_t t = d.pos0 + static_cast<uint32_t>(m);
+    const uint32_t page = d.table[t / d.page_tokens];
+    const uint32_t slot = t % d.page_tokens;
+    row8 = d.q8 + page * d.page_bytes + slot * d.row_bytes + head * 128;
+    sp = reinterpret_cast<float *>(reinterpret_cast<int8_t *>(d.qs) + page * d.scale_page_bytes +
+                                   slot * d.scale_row_bytes) + head;
+  } else {
+    row8 = d.q8 + static_cast<int64_t>(m) * d.ldq8 + head * 128;
+    sp = d.qs + static_cast<int64_t>(m) * d.ldqs + head * d.qs_col;
+  }
+  row8[lane] = static_cast<int8_t>(quant1(t0, scale));
+  row8[lane + 64] = static_cast<int8_t>(quant1(t1, scale));
+  if (lane == 0) *sp = scale;
+}
+
+template <int GPW, int KSTEPS, int NT, int NMAT>
+hipError_t launch_t(const GemvArgs &a, int ncols, hipStream_t s) {
+  constexpr int NB = 16 * NT;
+  const int ngroups = a.K / a.group;
+  size_t lds = sizeof(float) * NMAT * ngroups * 16 * (NB + 1);
+  if (a.pro != PRO_NONE)
+    lds += ((a.M * a.K + 15) & ~15) + sizeof(float) * (a.M * (a.K / 256) + a.K / 32);
+  if (lds > 65536) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((gemv_kernel<GPW, KSTEPS, NT, NMAT>), dim3(ncols / NB), dim3(256), lds, s, a);
+  return hipGetLastError();
+}
+
+template <int NT, int NMAT>
+hipError_t dispatch_k(const GemvArgs &a, int ncols, hipStream_t s) {
+  if (a.K == 1024 && a.group == 256) return launch_t<1, 4, NT, NMAT>(a, ncols, s);
+  if (a.K == 1024 && a.group == 128) return launch_t<2, 2, NT, NMAT>(a, ncols, s);
+  if (a.K == 2048 && a.group == 128) return launch_t<4, 2, NT, NMAT>(a, ncols, s);
+  if (a.K == 2048 && a.group == 256) return launch_t<2, 4, NT, NMAT>(a, ncols, s);
+  if (a.K == 3072 && a.group == 256) return launch_t<3, 4, NT, NMAT>(a, ncols, s);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+bool gemv_supported(int M, int K, int group) {
+  if (M < 1 || M > 16) return false;
+  return (K == 1024 && (group == 256 || group == 128)) || (K == 2048 && (group == 128 || group == 256)) ||
+         (K == 3072 && group == 256);
+}
+
+int gemv_cols_per_block(const GemvArgs &a) {
+  int ncols = 0;
+  for (int i = 0; i < a.nseg; ++i) ncols = a.seg[i].n1;
+  return ncols >= 65536 ? 64 : 16;
+}
+
+hipError_t launch_gemv(const GemvArgs &a, hipStream_t s) {
+  if (a.M <= 0) return hipSuccess;
+  if (a.pro != PRO_NONE && (a.K % 256 != 0 || a.M > 16)) return hipErrorInvalidValue;
+  int ncols = 0;
+  for (int i = 0; i < a.nseg; ++i) ncols = a.seg[i].n1;
+  const bool two = a.seg[0].epi == EPI_SWIGLU;
+  const int nb = gemv_cols_per_block(a);
+  if (two) return dispatch_k<1, 2>(a, ncols, s);
+  if (nb == 64) return dispatch_k<4, 1>(a, ncols, s);
+  return dispatch_k<1, 1>(a, ncols, s);
+}
+
+hipError_t launch_qkv_heads(const QkvHeadArgs &a, hipStream_t s) {
+  const int items = a.M * (a.q_heads + 2 * a.kv_heads);
+  if (items <= 0) return hipSuccess;
+  hipLaunchKernelGGL(qkv_heads_kernel, dim3((items + 3) / 4), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace q3

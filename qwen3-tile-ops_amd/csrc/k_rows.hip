@@ -111,6 +111,90 @@ __global__ void __launch_bounds__(256) nrq_rows_kernel(NrqArgs a) {
   if (lane == 0) a.qs[static_cast<int64_t>(row) * a.ldqs + head * a.qs_col] = scale;
 }
 
+// Register-resident variant for 1024-wide rows with 256-column groups (the
+// model's hidden size): one 256-thread workgroup per row, thread t owns
+// columns 4t..4t+3.  The 32-column block tree is: pairs inside the thread,
+// then xor-1/2/4 butterflies over the block's 8 threads (the reference's
+// adjacent-pair tree, level by level); the 32 block sums are then added in
+// column order by every thread from LDS.  A 256-column quant group is
+// exactly one wave.
+__global__ void __launch_bounds__(256) rows1024_kernel(RowArgs a) {
+  __shared__ float bsum[32];
+  const int row = blockIdx.x;
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int c0 = 4 * t;
+  float v[4];
+  if (a.mode == 2) {
+    int64_t base = 0;
+    if (a.ids_base_pos) base = *a.ids_base_pos;
+    const int32_t id = a.ids[(base + row) * a.ids_stride];
+    if (id >= 0 && id < a.table_rows) {
+      const char4 e = *reinterpret_cast<const char4 *>(a.table + static_cast<int64_t>(id) * a.ldt + c0);
+      const float sc = a.tscale[static_cast<int64_t>(id) * a.tss];
+      v[0] = __fmul_rn(static_cast<float>(e.x), sc);
+      v[1] = __fmul_rn(static_cast<float>(e.y), sc);
+      v[2] = __fmul_rn(static_cast<float>(e.z), sc);
+      v[3] = __fmul_rn(static_cast<float>(e.w), sc);
+    } else {
+      v[0] = v[1] = v[2] = v[3] = 0.0f;
+    }
+    if (a.x_out)
+      *reinterpret_cast<float4 *>(a.x_out + static_cast<int64_t>(row) * a.ldxo + c0) =
+          make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+    const float4 x = *reinterpret_cast<const float4 *>(a.x + static_cast<int64_t>(row) * a.ldx + c0);
+    v[0] = x.x;
+    v[1] = x.y;
+    v[2] = x.z;
+    v[3] = x.w;
+  }
+  if (a.mode != 0) {
+    float s = __fadd_rn(__fadd_rn(__fmul_rn(v[0], v[0]), __fmul_rn(v[1], v[1])),
+                        __fadd_rn(__fmul_rn(v[2], v[2]), __fmul_rn(v[3], v[3])));
+    s = __fadd_rn(s, __shfl_xor(s, 1));
+    s = __fadd_rn(s, __shfl_xor(s, 2));
+    s = __fadd_rn(s, __shfl_xor(s, 4));
+    if ((t & 7) == 0) bsum[t >> 3] = s;
+    __syncthreads();
+    float ss = 0.0f;
+#pragma unroll
+    for (int b = 0; b < 32; ++b) ss = __fadd_rn(ss, bsum[b]);
+    const float rinv = rms_factor(ss, a.inv);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      v[i] = __fmul_rn(__fmul_rn(v[i], rinv), a.w[static_cast<int64_t>(c0 + i) * a.w_stride]);
+    if (a.h)
+      *reinterpret_cast<float4 *>(a.h + static_cast<int64_t>(row) * a.ldh + c0) =
+          make_float4(v[0], v[1], v[2], v[3]);
+  }
+  if (!a.h8) return;
+  float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  m = max64(m);
+  const float scale = __fmul_rn(m, inv127());
+  char4 q;
+  q.x = static_cast<signed char>(quant1(v[0], scale));
+  q.y = static_cast<signed char>(quant1(v[1], scale));
+  q.z = static_cast<signed char>(quant1(v[2], scale));
+  q.w = static_cast<signed char>(quant1(v[3], scale));
+  *reinterpret_cast<char4 *>(a.h8 + static_cast<int64_t>(row) * a.ldh8 + c0) = q;
+  if (lane == 0) a.hs[static_cast<int64_t>(row) * a.ldhs + (t >> 6)] = scale;
+}
+
+bool rows1024_ok(const RowArgs &a) {
+  auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (a.cols != 1024) return false;
+  if (a.h8 && (a.group != 256 || (a.ldh8 & 3) || !al16(a.h8))) return false;
+  if (a.mode == 2) {
+    if ((a.ldt & 3) || (reinterpret_cast<uintptr_t>(a.table) & 3)) return false;
+    if (a.x_out && ((a.ldxo & 3) || !al16(a.x_out))) return false;
+  } else if ((a.ldx & 3) || !al16(a.x)) {
+    return false;
+  }
+  if (a.h && ((a.ldh & 3) || !al16(a.h))) return false;
+  return true;
+}
+
 }  // namespace
 
 hipError_t launch_nrq_rows(const NrqArgs &a, hipStream_t s) {
@@ -122,6 +206,10 @@ hipError_t launch_nrq_rows(const NrqArgs &a, hipStream_t s) {
 
 hipError_t launch_rows(const RowArgs &a, hipStream_t s) {
   if (a.rows <= 0) return hipSuccess;
+  if (rows1024_ok(a)) {
+    hipLaunchKernelGGL(rows1024_kernel, dim3(a.rows), dim3(256), 0, s, a);
+    return hipGetLastError();
+  }
   const dim3 grid((a.rows + 3) / 4);
   hipLaunchKernelGGL(rows_kernel, grid, dim3(256), 0, s, a);
   return hipGetLastError();

@@ -73,6 +73,39 @@ __device__ __forceinline__ float exp_f32(float x) {
   return exp2f_glibc(__fmul_rn(x, bits_f32(0x3FB8AA3Bu)));
 }
 
+// Same function with the 32-entry table read from `tab` (a copy of kExp2Tab
+// staged in LDS by the caller), so a latency-critical loop does not wait on
+// a global-memory table lookup per call.
+__device__ __forceinline__ float exp2f_glibc_tab(float x, const uint64_t *tab) {
+  const uint32_t ux = f32_bits(x);
+  const uint32_t abstop = (ux >> 20) & 0x7ffu;
+  if (abstop >= (0x43000000u >> 20)) {
+    if (ux == 0xff800000u) return 0.0f;
+    if (abstop >= (0x7f800000u >> 20)) return x + x;
+    if (x > 0.0f) return bits_f32(0x7f800000u);
+    if (x <= -150.0f) return 0.0f;
+  }
+  const double xd = static_cast<double>(x);
+  const double shift = 0x1.8p+52 / 32;
+  double kd = __dadd_rn(xd, shift);
+  const uint64_t ki = static_cast<uint64_t>(__double_as_longlong(kd));
+  kd = __dsub_rn(kd, shift);
+  const double r = __dsub_rn(xd, kd);
+  uint64_t t = tab[ki & 31u];
+  t += ki << 47;
+  const double s = __longlong_as_double(static_cast<long long>(t));
+  const double z = __fma_rn(0x1.c6af84b912394p-5, r, 0x1.ebfce50fac4f3p-3);
+  const double r2 = __dmul_rn(r, r);
+  double y = __fma_rn(0x1.62e42ff0c52d6p-1, r, 1.0);
+  y = __fma_rn(z, r2, y);
+  y = __dmul_rn(y, s);
+  return __double2float_rn(y);
+}
+
+__device__ __forceinline__ float exp_f32_tab(float x, const uint64_t *tab) {
+  return exp2f_glibc_tab(__fmul_rn(x, bits_f32(0x3FB8AA3Bu)), tab);
+}
+
 __device__ __forceinline__ float inv127() { return 1.0f / 127.0f; }
 
 // ref_qwen3.py:69-76: one element of aquant with an external scale.

@@ -47,6 +47,7 @@ enum Epi : int {
   EPI_HEADQ = 2,   // per-128-column int8 quant (V)
   EPI_NRQ = 3,     // per-head RMSNorm + RoPE + int8 quant (Q, K)
   EPI_ARGMAX = 4,  // fold D into per-row (max, first index) keys
+  EPI_SWIGLU = 5,  // gate/up pair -> f32 SwiGLU (decode GEMV only)
 };
 
 // Destination of the HEADQ/NRQ int8 rows: either a dense [M][N] i8 view
@@ -87,16 +88,18 @@ struct GemmArgs {
   int64_t ld_cs;
   const int32_t *cs_row_dev;   // optional: cos/sin row offset (device scalar)
   float inv_hd;
-  // EPI_ARGMAX
-  unsigned long long *keys;  // [M] workspace, zero before the first launch
+  // EPI_ARGMAX: one key per (row, column block of 128) at keys[m * keys_ld + blockIdx.x]
+  unsigned long long *keys;
+  int64_t keys_ld;
 };
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t s);
 
-// Finishes EPI_ARGMAX: merges keys[m] into (best[m], bidx[m]) with the
-// strict `best < value` rule (init != 0: start from -3e38 / 0 instead of the
-// current contents), optionally writes the winning id to
-// ids[*pos] (greedy loop), and clears keys for the next launch.
-hipError_t launch_argmax_finish(unsigned long long *keys, int M, float *best,
+// Finishes EPI_ARGMAX: reduces the nslots per-workgroup keys of each row
+// and merges the winner into (best[m], bidx[m]) with the strict
+// `best < value` rule (init != 0: start from -3e38 / 0 instead of the
+// current contents); optionally writes the winning id to ids[*pos].
+hipError_t launch_argmax_finish(const unsigned long long *keys, int64_t keys_ld, int nslots,
+                                int M, float *best,
                                 int64_t best_stride, int32_t *bidx,
                                 int64_t bidx_stride, int init, int32_t *ids_out,
                                 const int32_t *pos_dev, int pos_add,
@@ -145,6 +148,15 @@ struct AttnArgs {
   int64_t os_col;
   float *attn;   // optional f32 attention output [rows][heads*128]
   int64_t ld_attn;
+  // decode kernel only: when fuse_heads != 0 the kernel first runs the head
+  // epilogues of the new token (row 0 of fq/fk/fv, position kv_len - 1):
+  // K norm+RoPE+quant and V quant into their page slots, Q norm+RoPE+quant
+  // into q8/qs (which must then be writable).
+  int fuse_heads;
+  const float *fq, *fk, *fv;
+  const float *nq, *nk;
+  const float *cos_row, *sin_row;
+  float inv_hd;
 };
 hipError_t launch_attention(const AttnArgs &a, hipStream_t s);
 
@@ -165,6 +177,69 @@ struct NrqArgs {
   int64_t ldqs, qs_col;
 };
 hipError_t launch_nrq_rows(const NrqArgs &a, hipStream_t s);
+
+// ---- decode-shaped group GEMM (M <= 16) ---------------------------------
+// One launch can cover up to three column ranges with their own weights and
+// epilogue (fused Q/K/V).  No grid-wide synchronisation.
+enum Pro : int {
+  PRO_NONE = 0,   // A operand int8 + scales from global memory
+  PRO_NORM = 1,   // A = quant256(rmsnorm(x, w_pre))
+  PRO_QUANT = 2,  // A = quant256(x)
+  PRO_EMBED = 3,  // A = quant256(rmsnorm(emb[ids] * emb_s[ids], w_pre))
+};
+struct GemvSeg {
+  int n0, n1;  // columns [n0, n1) of the launch
+  int epi;     // EPI_STORE / EPI_ADD / EPI_ARGMAX / EPI_SWIGLU
+  const int8_t *b, *b2;    // [n1-n0][K] rows (b2: up rows for EPI_SWIGLU)
+  const float *bs, *bs2;   // per-row scales
+  float *out;
+  int64_t ldo;
+};
+struct GemvArgs {
+  int M, K, group;
+  const int8_t *a;  // PRO_NONE
+  int64_t lda;
+  const float *as;
+  int64_t ldas;
+  int pro;
+  const float *x;   // PRO_NORM / PRO_QUANT rows (ldx); PRO_EMBED: x_out rows
+  int64_t ldx;
+  const float *w_pre;
+  float inv_pre;
+  const int8_t *emb;
+  const float *emb_s;
+  const int32_t *ids;
+  int64_t vocab;
+  float *x_out;     // PRO_EMBED: dequantised rows (written by workgroup 0)
+  float *h_out;     // stage buffers written by workgroup 0 (may be null)
+  int8_t *h8_out;
+  float *hs_out;
+  int nseg;
+  GemvSeg seg[3];
+  unsigned long long *keys;  // EPI_ARGMAX: [M][keys_ld] one key per workgroup
+  int64_t keys_ld;
+};
+bool gemv_supported(int M, int K, int group);
+int gemv_cols_per_block(const GemvArgs &a);
+hipError_t launch_gemv(const GemvArgs &a, hipStream_t s);
+
+// Head epilogues of the Q/K/V projections from f32 rows: per (row, head)
+// RMSNorm + RoPE + quant (Q, K) or quant (V) into dense or paged int8.
+struct QkvHeadArgs {
+  int M, q_heads, kv_heads;
+  const float *q, *k, *v;
+  int64_t ldq, ldk;
+  QDest qd, kd, vd;
+  const float *nq, *nk;
+  const float *cos_q, *sin_q, *cos_k, *sin_k;  // rows at the rows' positions
+  int64_t ld_cs;
+  float inv_hd;
+};
+hipError_t launch_qkv_heads(const QkvHeadArgs &a, hipStream_t s);
+
+// ---- decode attention (one query row per head) ---------------------------
+bool attn_decode_supported(const AttnArgs &a);
+hipError_t launch_attn_decode(const AttnArgs &a, hipStream_t s);
 
 // ---- greedy pick over a logits row (main_big.cpp:300-322) ---------------
 hipError_t launch_argmax_logits(const float *logits, int vocab,

@@ -29,11 +29,15 @@ struct q3_model {
   uint16_t *ptab;              // device, max_seq / 32 entries
   uint32_t n_pages;
   unsigned long long *keys;    // device argmax key (1 row)
+  // argmax workspace: one key per lm_head column block (allocated at open)
+  unsigned long long *keys_ws;
+  int64_t keys_ld;
 };
 
 namespace {
 
 constexpr uint32_t kPageTokens = 32;
+constexpr int kMaxGemvRows = 16;
 
 int hip_status(hipError_t e) { return e == hipSuccess ? Q3_OK : Q3_ERR_HIP; }
 
@@ -157,6 +161,334 @@ q3::GemmArgs gemm_args(int M, int N, int K, int group, const int8_t *a, const fl
   return g;
 }
 
+q3::GemvArgs gemv_args(int M, int K, int group) {
+  q3::GemvArgs v;
+  std::memset(&v, 0, sizeof(v));
+  v.M = M;
+  v.K = K;
+  v.group = group;
+  return v;
+}
+
+q3::GemvSeg gemv_seg(int n0, int n1, int epi, const int8_t *b, const float *bs, float *out,
+                     int64_t ldo) {
+  q3::GemvSeg g;
+  std::memset(&g, 0, sizeof(g));
+  g.n0 = n0;
+  g.n1 = n1;
+  g.epi = epi;
+  g.b = b;
+  g.bs = bs;
+  g.out = out;
+  g.ldo = ldo;
+  return g;
+}
+
+// True when a chunk of `rows` runs on the decode-shaped kernels.
+bool small_path(const q3_layout &y, uint32_t rows) {
+  const int H = static_cast<int>(y.hidden);
+  const int QW = static_cast<int>(y.heads * y.head_dim);
+  return rows <= static_cast<uint32_t>(kMaxGemvRows) && q3::gemv_supported(static_cast<int>(rows), H, 256) &&
+         q3::gemv_supported(static_cast<int>(rows), QW, static_cast<int>(y.head_dim)) &&
+         q3::gemv_supported(static_cast<int>(rows), static_cast<int>(y.inter), 256);
+}
+
+// main_big.cpp:264-295: final RMSNorm of the last row, lm_head, and either
+// full logits (mode 1) or the fused argmax (mode 0).  Its stage buffers are
+// the borrowed rows of main_big.cpp:268-272 (hl = o row 0, h8l = q8 row 0,
+// hsl = qs row 0).
+int lm_head(q3_model *m, uint32_t rows, int lm_out, int32_t *id_dst) {
+  const q3_layout &y = m->lay;
+  const hipStream_t s = m->stream;
+  const int H = static_cast<int>(y.hidden), V = static_cast<int>(y.vocab);
+  if (lm_out == Q3_LM_NONE) return Q3_OK;
+  float *x = at<float>(m, y.kX);
+  q3::GemvArgs g = gemv_args(1, H, 256);
+  g.pro = q3::PRO_NORM;
+  g.x = x + static_cast<int64_t>(rows - 1) * H;
+  g.ldx = H;
+  g.w_pre = at<const float>(m, y.kNF);
+  g.inv_pre = 1.0f / static_cast<float>(H);
+  g.h_out = at<float>(m, y.kO);
+  g.h8_out = at<int8_t>(m, y.kQ8);
+  g.hs_out = at<float>(m, y.kQS);
+  g.nseg = 1;
+  const int8_t *lm = at<const int8_t>(m, y.kLM);
+  const float *lm_s = at<const float>(m, y.kLM + static_cast<int64_t>(V) * H);
+  if (lm_out == Q3_LM_LOGITS) {
+    float *logits = at<float>(m, y.kLOGITS);
+    g.seg[0] = gemv_seg(0, V, q3::EPI_STORE, lm, lm_s, logits, V);
+    Q3_HIP(q3::launch_gemv(g, s));
+    if (id_dst) Q3_HIP(q3::launch_argmax_logits(logits, V, id_dst, nullptr, 0, s));
+  } else {
+    g.seg[0] = gemv_seg(0, V, q3::EPI_ARGMAX, lm, lm_s, nullptr, 0);
+    g.keys = m->keys_ws;
+    g.keys_ld = m->keys_ld;
+    Q3_HIP(q3::launch_gemv(g, s));
+    const int nslots = V / q3::gemv_cols_per_block(g);
+    Q3_HIP(q3::launch_argmax_finish(m->keys_ws, m->keys_ld, nslots, 1, at<float>(m, y.kARGF), 1,
+                                    at<int32_t>(m, y.kARGI), 1, /*init=*/1, id_dst, nullptr, 0, s));
+  }
+  return Q3_OK;
+}
+
+// main_big.cpp:145-296 for chunks of at most 16 rows: every GEMM is a
+// whole-chip GEMV whose prologue builds its int8 operand from the f32 rows
+// (embedding / RMSNorm / quant), and whose epilogue is a plain store, the
+// residual add, SwiGLU or the argmax.
+int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int optimize_tail,
+                  int32_t *id_dst) {
+  const q3_layout &y = m->lay;
+  const hipStream_t s = m->stream;
+  const int H = static_cast<int>(y.hidden), HD = static_cast<int>(y.head_dim);
+  const int QW = static_cast<int>(y.heads) * HD, KW = static_cast<int>(y.kv_heads) * HD;
+  const int I = static_cast<int>(y.inter), V = static_cast<int>(y.vocab);
+  const int HALF = static_cast<int>(y.half);
+  const int R = static_cast<int>(rows);
+  float *x = at<float>(m, y.kX);
+  float *h = at<float>(m, y.kH);
+  int8_t *h8 = at<int8_t>(m, y.kH8);
+  float *hs = at<float>(m, y.kHS);
+  float *q = at<float>(m, y.kQ);
+  float *k = at<float>(m, y.kK);
+  float *v = at<float>(m, y.kV);
+  int8_t *q8 = at<int8_t>(m, y.kQ8);
+  float *qs = at<float>(m, y.kQS);
+  int8_t *o8 = at<int8_t>(m, y.kO8);
+  float *os = at<float>(m, y.kOS);
+  float *sw = at<float>(m, y.kSW);
+  int8_t *s8 = at<int8_t>(m, y.kS8);
+  float *ss = at<float>(m, y.kSS);
+  const float *cos_t = at<const float>(m, y.kCOS);
+  const float *sin_t = at<const float>(m, y.kSIN);
+  const float inv_h = 1.0f / static_cast<float>(H);
+  const float inv_hd = 1.0f / static_cast<float>(HD);
+  const float qk_scale = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(HD)));
+
+  for (uint32_t L = 0; L < y.layers; ++L) {
+    const LayerPtrs lp = layer_ptrs(m, L);
+    const bool is_last = (L + 1 == y.layers);
+    const bool do_tail = !is_last || lm_out != Q3_LM_NONE;
+    const bool tail_last_row = optimize_tail && is_last;
+    const uint32_t tr0 = tail_last_row ? rows - 1 : 0;
+    const uint32_t tr = tail_last_row ? 1 : rows;
+    const int M = static_cast<int>(tr);
+
+    // Q | K | V projections; prologue = (embedding +) RMSNorm n1 + quant
+    {
+      q3::GemvArgs g = gemv_args(R, H, 256);
+      if (L == 0) {
+        g.pro = q3::PRO_EMBED;
+        g.emb = at<const int8_t>(m, y.kEMB);
+        g.emb_s = at<const float>(m, y.kEMB + static_cast<int64_t>(V) * H);
+        g.ids = at<const int32_t>(m, y.kIDS) + pos;
+        g.vocab = V;
+        g.x_out = x;
+      } else {
+        g.pro = q3::PRO_NORM;
+        g.x = x;
+      }
+      g.ldx = H;
+      g.w_pre = lp.n1;
+      g.inv_pre = inv_h;
+      g.h_out = h;
+      g.h8_out = h8;
+      g.hs_out = hs;
+      g.nseg = 3;
+      g.seg[0] = gemv_seg(0, QW, q3::EPI_STORE, lp.wq, lp.wqs, q, QW);
+      g.seg[1] = gemv_seg(QW, QW + KW, q3::EPI_STORE, lp.wk, lp.wks, k, KW);
+      g.seg[2] = gemv_seg(QW + KW, QW + 2 * KW, q3::EPI_STORE, lp.wv, lp.wvs, v, KW);
+      Q3_HIP(q3::launch_gemv(g, s));
+    }
+    // paged GQA attention over kv_len = pos + rows keys
+    q3::AttnArgs t{};
+    t.rows = M;
+    t.heads = static_cast<int>(y.heads);
+    t.kv_heads = static_cast<int>(y.kv_heads);
+    t.kv_len = pos + rows;
+    t.causal = 1;
+    t.qk_scale = qk_scale;
+    t.q8 = q8 + static_cast<int64_t>(tr0) * QW;
+    t.ldq = QW;
+    t.qs = qs + static_cast<int64_t>(tr0) * y.heads;
+    t.ldqs = y.heads;
+    t.qs_col = 1;
+    t.k = lp.kc;
+    t.v = lp.vc;
+    t.ks = lp.kcs;
+    t.vs = lp.vcs;
+    t.table = m->ptab;
+    t.page_tokens = kPageTokens;
+    t.page_bytes = static_cast<int64_t>(kPageTokens) * KW;
+    t.row_bytes = KW;
+    t.scale_page_bytes = static_cast<int64_t>(kPageTokens) * y.kv_heads * 4;
+    t.scale_row_bytes = y.kv_heads * 4;
+    t.o8 = o8 + static_cast<int64_t>(tr0) * QW;
+    t.ldo = QW;
+    t.os = os + static_cast<int64_t>(tr0) * y.heads;
+    t.ldos = y.heads;
+    t.os_col = 1;
+    // one decode token: the head epilogues run in the attention prologue
+    const bool fuse = do_tail && rows == 1 && q3::attn_decode_supported(t);
+    if (fuse) {
+      t.fuse_heads = 1;
+      t.fq = q;
+      t.fk = k;
+      t.fv = v;
+      t.nq = lp.nq;
+      t.nk = lp.nk;
+      t.cos_row = cos_t + static_cast<int64_t>(pos) * HALF;
+      t.sin_row = sin_t + static_cast<int64_t>(pos) * HALF;
+      t.inv_hd = inv_hd;
+    } else {
+      // head epilogues: K (norm+RoPE+quant) and V (quant) of every row into
+      // the page slots; Q (norm+RoPE+quant) of the tail rows
+      q3::QkvHeadArgs e;
+      std::memset(&e, 0, sizeof(e));
+      e.kv_heads = static_cast<int>(y.kv_heads);
+      e.k = k;
+      e.v = v;
+      e.ldq = QW;
+      e.ldk = KW;
+      set_paged(e.kd, m, lp.kc, lp.kcs, pos);
+      set_paged(e.vd, m, lp.vc, lp.vcs, pos);
+      e.nk = lp.nk;
+      e.nq = lp.nq;
+      e.cos_k = cos_t + static_cast<int64_t>(pos) * HALF;
+      e.sin_k = sin_t + static_cast<int64_t>(pos) * HALF;
+      e.ld_cs = HALF;
+      e.inv_hd = inv_hd;
+      e.qd.q8 = q8 + static_cast<int64_t>(tr0) * QW;
+      e.qd.ldq8 = QW;
+      e.qd.qs = qs + static_cast<int64_t>(tr0) * y.heads;
+      e.qd.ldqs = y.heads;
+      e.qd.qs_col = 1;
+      e.cos_q = cos_t + static_cast<int64_t>(pos + tr0) * HALF;
+      e.sin_q = sin_t + static_cast<int64_t>(pos + tr0) * HALF;
+      if (do_tail && tr == rows) {
+        e.M = R;
+        e.q_heads = static_cast<int>(y.heads);
+        e.q = q;
+        Q3_HIP(q3::launch_qkv_heads(e, s));
+      } else {
+        e.M = R;
+        e.q_heads = 0;
+        Q3_HIP(q3::launch_qkv_heads(e, s));
+        if (do_tail) {
+          q3::QkvHeadArgs eq = e;
+          eq.M = M;
+          eq.q_heads = static_cast<int>(y.heads);
+          eq.kv_heads = 0;
+          eq.q = q + static_cast<int64_t>(tr0) * QW;
+          Q3_HIP(q3::launch_qkv_heads(eq, s));
+        }
+      }
+    }
+    if (!do_tail) continue;
+    if (q3::attn_decode_supported(t))
+      Q3_HIP(q3::launch_attn_decode(t, s));
+    else
+      Q3_HIP(q3::launch_attention(t, s));
+    float *xt = x + static_cast<int64_t>(tr0) * H;
+    // O projection (group = head_dim) + residual
+    {
+      q3::GemvArgs g = gemv_args(M, QW, HD);
+      g.a = o8 + static_cast<int64_t>(tr0) * QW;
+      g.lda = QW;
+      g.as = os + static_cast<int64_t>(tr0) * y.heads;
+      g.ldas = y.heads;
+      g.nseg = 1;
+      g.seg[0] = gemv_seg(0, H, q3::EPI_ADD, lp.wo, lp.wos, xt, H);
+      Q3_HIP(q3::launch_gemv(g, s));
+    }
+    // gate/up + SwiGLU; prologue = RMSNorm n2 + quant
+    {
+      q3::GemvArgs g = gemv_args(M, H, 256);
+      g.pro = q3::PRO_NORM;
+      g.x = xt;
+      g.ldx = H;
+      g.w_pre = lp.n2;
+      g.inv_pre = inv_h;
+      g.h_out = h + static_cast<int64_t>(tr0) * H;
+      g.h8_out = h8 + static_cast<int64_t>(tr0) * H;
+      g.hs_out = hs + static_cast<int64_t>(tr0) * (H / 256);
+      g.nseg = 1;
+      g.seg[0] = gemv_seg(0, I, q3::EPI_SWIGLU, lp.wg, lp.wgs, sw + static_cast<int64_t>(tr0) * I, I);
+      g.seg[0].b2 = lp.wu;
+      g.seg[0].bs2 = lp.wus;
+      Q3_HIP(q3::launch_gemv(g, s));
+    }
+    // down projection + residual; prologue = per-256 quant of SwiGLU
+    {
+      q3::GemvArgs g = gemv_args(M, I, 256);
+      g.pro = q3::PRO_QUANT;
+      g.x = sw + static_cast<int64_t>(tr0) * I;
+      g.ldx = I;
+      g.h8_out = s8 + static_cast<int64_t>(tr0) * I;
+      g.hs_out = ss + static_cast<int64_t>(tr0) * (I / 256);
+      g.nseg = 1;
+      g.seg[0] = gemv_seg(0, H, q3::EPI_ADD, lp.wd, lp.wds, xt, H);
+      Q3_HIP(q3::launch_gemv(g, s));
+    }
+  }
+
+  return lm_head(m, rows, lm_out, id_dst);
+}
+
+// V (quant) and K (norm + RoPE + quant) straight into the page slots and Q
+// for the tail rows, with 128-column GEMM tiles (prefill-sized chunks).
+int qkv_projections(q3_model *m, const LayerPtrs &lp, uint32_t pos, uint32_t rows, bool do_tail,
+                    uint32_t tr0, uint32_t tr) {
+  const q3_layout &y = m->lay;
+  const hipStream_t s = m->stream;
+  const int H = static_cast<int>(y.hidden), HD = static_cast<int>(y.head_dim);
+  const int QW = static_cast<int>(y.heads) * HD, KW = static_cast<int>(y.kv_heads) * HD;
+  const int HALF = static_cast<int>(y.half);
+  int8_t *h8 = at<int8_t>(m, y.kH8);
+  float *hs = at<float>(m, y.kHS);
+  int8_t *q8 = at<int8_t>(m, y.kQ8);
+  float *qs = at<float>(m, y.kQS);
+  const float *cos_t = at<const float>(m, y.kCOS);
+  const float *sin_t = at<const float>(m, y.kSIN);
+  const float inv_hd = 1.0f / static_cast<float>(HD);
+  {
+    q3::GemmArgs g = gemm_args(static_cast<int>(rows), KW, H, 256, h8, hs, lp.wv, lp.wvs);
+    g.epi = q3::EPI_HEADQ;
+    set_paged(g.qd, m, lp.vc, lp.vcs, pos);
+    Q3_HIP(q3::launch_gemm(g, s));
+  }
+  {
+    q3::GemmArgs g = gemm_args(static_cast<int>(rows), KW, H, 256, h8, hs, lp.wk, lp.wks);
+    g.epi = q3::EPI_NRQ;
+    set_paged(g.qd, m, lp.kc, lp.kcs, pos);
+    g.nw = lp.nk;
+    g.nw_stride = 1;
+    g.cos_t = cos_t + static_cast<int64_t>(pos) * HALF;
+    g.sin_t = sin_t + static_cast<int64_t>(pos) * HALF;
+    g.ld_cs = HALF;
+    g.inv_hd = inv_hd;
+    Q3_HIP(q3::launch_gemm(g, s));
+  }
+  if (do_tail) {
+    q3::GemmArgs g = gemm_args(static_cast<int>(tr), QW, H, 256, h8 + static_cast<int64_t>(tr0) * H,
+                               hs + static_cast<int64_t>(tr0) * (H / 256), lp.wq, lp.wqs);
+    g.epi = q3::EPI_NRQ;
+    g.qd.q8 = q8 + static_cast<int64_t>(tr0) * QW;
+    g.qd.ldq8 = QW;
+    g.qd.qs = qs + static_cast<int64_t>(tr0) * y.heads;
+    g.qd.ldqs = y.heads;
+    g.qd.qs_col = 1;
+    g.nw = lp.nq;
+    g.nw_stride = 1;
+    g.cos_t = cos_t + static_cast<int64_t>(pos + tr0) * HALF;
+    g.sin_t = sin_t + static_cast<int64_t>(pos + tr0) * HALF;
+    g.ld_cs = HALF;
+    g.inv_hd = inv_hd;
+    Q3_HIP(q3::launch_gemm(g, s));
+  }
+  return Q3_OK;
+}
+
 // main_big.cpp:145-296.  id_dst (device, may be null) receives the greedy id
 // of the last row when lm_out != Q3_LM_NONE.
 int forward_chunk_impl(q3_model *m, uint32_t pos, uint32_t rows, int lm_out,
@@ -164,10 +496,10 @@ int forward_chunk_impl(q3_model *m, uint32_t pos, uint32_t rows, int lm_out,
   const q3_layout &y = m->lay;
   if (rows == 0 || rows > y.seq || pos + rows > y.max_seq) return Q3_ERR_RANGE;
   if (lm_out < Q3_LM_NONE || lm_out > Q3_LM_ARGMAX) return Q3_ERR_ARG;
+  if (small_path(y, rows)) return forward_small(m, pos, rows, lm_out, optimize_tail, id_dst);
   const int H = static_cast<int>(y.hidden), HD = static_cast<int>(y.head_dim);
   const int QW = static_cast<int>(y.heads) * HD, KW = static_cast<int>(y.kv_heads) * HD;
-  const int I = static_cast<int>(y.inter), V = static_cast<int>(y.vocab);
-  const int HALF = static_cast<int>(y.half);
+  const int I = static_cast<int>(y.inter);
   const hipStream_t s = m->stream;
 
   float *x = at<float>(m, y.kX);
@@ -180,9 +512,6 @@ int forward_chunk_impl(q3_model *m, uint32_t pos, uint32_t rows, int lm_out,
   float *os = at<float>(m, y.kOS);
   int8_t *s8 = at<int8_t>(m, y.kS8);
   float *ss = at<float>(m, y.kSS);
-  const float *cos_t = at<const float>(m, y.kCOS);
-  const float *sin_t = at<const float>(m, y.kSIN);
-  const float inv_hd = 1.0f / static_cast<float>(HD);
   const float qk_scale = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(HD)));
 
   // embedding + layer-0 RMSNorm (main_big.cpp:163-166), then its quant
@@ -198,53 +527,20 @@ int forward_chunk_impl(q3_model *m, uint32_t pos, uint32_t rows, int lm_out,
       const int rc = norm_quant_rows(m, 1, pos, 0, rows, lp.n1, x, h, h8, hs);
       if (rc != Q3_OK) return rc;
     }
-    // V: GEMM + per-head quant straight into the page slots
-    {
-      q3::GemmArgs g = gemm_args(static_cast<int>(rows), KW, H, 256, h8, hs, lp.wv, lp.wvs);
-      g.epi = q3::EPI_HEADQ;
-      set_paged(g.qd, m, lp.vc, lp.vcs, pos);
-      Q3_HIP(q3::launch_gemm(g, s));
-    }
-    // K: GEMM + k-norm + RoPE + per-head quant into the page slots
-    {
-      q3::GemmArgs g = gemm_args(static_cast<int>(rows), KW, H, 256, h8, hs, lp.wk, lp.wks);
-      g.epi = q3::EPI_NRQ;
-      set_paged(g.qd, m, lp.kc, lp.kcs, pos);
-      g.nw = lp.nk;
-      g.nw_stride = 1;
-      g.cos_t = cos_t + static_cast<int64_t>(pos) * HALF;
-      g.sin_t = sin_t + static_cast<int64_t>(pos) * HALF;
-      g.ld_cs = HALF;
-      g.inv_hd = inv_hd;
-      Q3_HIP(q3::launch_gemm(g, s));
-    }
     // main_big.cpp:212-223: the last layer only needs the tail rows
     const bool is_last = (L + 1 == y.layers);
     const bool do_tail = !is_last || lm_out != Q3_LM_NONE;
-    if (!do_tail) continue;
     const bool tail_last_row = optimize_tail && is_last;
     const uint32_t tr0 = tail_last_row ? rows - 1 : 0;
     const uint32_t tr = tail_last_row ? 1 : rows;
     const int M = static_cast<int>(tr);
 
-    // Q: GEMM + q-norm + RoPE + per-head quant
-    {
-      q3::GemmArgs g = gemm_args(M, QW, H, 256, h8 + static_cast<int64_t>(tr0) * H,
-                                 hs + static_cast<int64_t>(tr0) * (H / 256), lp.wq, lp.wqs);
-      g.epi = q3::EPI_NRQ;
-      g.qd.q8 = q8 + static_cast<int64_t>(tr0) * QW;
-      g.qd.ldq8 = QW;
-      g.qd.qs = qs + static_cast<int64_t>(tr0) * y.heads;
-      g.qd.ldqs = y.heads;
-      g.qd.qs_col = 1;
-      g.nw = lp.nq;
-      g.nw_stride = 1;
-      g.cos_t = cos_t + static_cast<int64_t>(pos + tr0) * HALF;
-      g.sin_t = sin_t + static_cast<int64_t>(pos + tr0) * HALF;
-      g.ld_cs = HALF;
-      g.inv_hd = inv_hd;
-      Q3_HIP(q3::launch_gemm(g, s));
-    }
+    // K (norm + RoPE + quant) and V (quant) straight into the page slots,
+    // Q (norm + RoPE + quant) for the tail rows
+    const int rc_qkv = qkv_projections(m, lp, pos, rows, do_tail, tr0, tr);
+    if (rc_qkv != Q3_OK) return rc_qkv;
+    if (!do_tail) continue;
+
     // paged GQA attention over kv_len = pos + rows keys
     {
       q3::AttnArgs t{};
@@ -274,7 +570,10 @@ int forward_chunk_impl(q3_model *m, uint32_t pos, uint32_t rows, int lm_out,
       t.os = os + static_cast<int64_t>(tr0) * y.heads;
       t.ldos = y.heads;
       t.os_col = 1;
-      Q3_HIP(q3::launch_attention(t, s));
+      if (q3::attn_decode_supported(t))
+        Q3_HIP(q3::launch_attn_decode(t, s));
+      else
+        Q3_HIP(q3::launch_attention(t, s));
     }
     float *xt = x + static_cast<int64_t>(tr0) * H;
     // O projection (group = head_dim) + residual into x
@@ -326,50 +625,7 @@ int forward_chunk_impl(q3_model *m, uint32_t pos, uint32_t rows, int lm_out,
     }
   }
 
-  if (lm_out == Q3_LM_NONE) return Q3_OK;
-  // final norm of the last row into the borrowed buffers (main_big.cpp:264-274):
-  // hl = o row 0, h8l = q8 row 0 (first H columns), hsl = qs row 0
-  float *hl = at<float>(m, y.kO);
-  int8_t *h8l = q8;
-  float *hsl = qs;
-  {
-    q3::RowArgs r{};
-    r.mode = 1;
-    r.rows = 1;
-    r.cols = H;
-    r.x = x + static_cast<int64_t>(rows - 1) * H;
-    r.ldx = H;
-    r.w = at<const float>(m, y.kNF);
-    r.w_stride = 1;
-    r.inv = 1.0f / static_cast<float>(H);
-    r.h = hl;
-    r.ldh = H;
-    r.h8 = h8l;
-    r.ldh8 = H;
-    r.hs = hsl;
-    r.ldhs = H / 256;
-    r.group = 256;
-    Q3_HIP(q3::launch_rows(r, s));
-  }
-  const int8_t *lm = at<const int8_t>(m, y.kLM);
-  const float *lm_s = at<const float>(m, y.kLM + static_cast<int64_t>(V) * H);
-  if (lm_out == Q3_LM_LOGITS) {
-    float *logits = at<float>(m, y.kLOGITS);
-    q3::GemmArgs g = gemm_args(1, V, H, 256, h8l, hsl, lm, lm_s);
-    g.epi = q3::EPI_STORE;
-    g.out = logits;
-    g.ldo = V;
-    Q3_HIP(q3::launch_gemm(g, s));
-    if (id_dst) Q3_HIP(q3::launch_argmax_logits(logits, V, id_dst, nullptr, 0, s));
-  } else {
-    q3::GemmArgs g = gemm_args(1, V, H, 256, h8l, hsl, lm, lm_s);
-    g.epi = q3::EPI_ARGMAX;
-    g.keys = m->keys;
-    Q3_HIP(q3::launch_gemm(g, s));
-    Q3_HIP(q3::launch_argmax_finish(m->keys, 1, at<float>(m, y.kARGF), 1, at<int32_t>(m, y.kARGI),
-                                    1, /*init=*/1, id_dst, nullptr, 0, s));
-  }
-  return Q3_OK;
+  return lm_head(m, rows, lm_out, id_dst);
 }
 
 }  // namespace
@@ -388,8 +644,10 @@ extern "C" int q3_model_open(void *blob, const q3_layout *lay, void *stream, q3_
   m->lay = *lay;
   m->stream = static_cast<hipStream_t>(stream);
   m->n_pages = lay->max_seq / kPageTokens;
+  m->keys_ld = lay->vocab / 16 + 64;  // one key per lm_head column block
   if (hipMalloc(&m->ptab, sizeof(uint16_t) * m->n_pages) != hipSuccess ||
-      hipMalloc(&m->keys, sizeof(unsigned long long) * 8) != hipSuccess) {
+      hipMalloc(&m->keys, sizeof(unsigned long long) * 8) != hipSuccess ||
+      hipMalloc(&m->keys_ws, sizeof(unsigned long long) * m->keys_ld) != hipSuccess) {
     q3_model_close(m);
     return Q3_ERR_HIP;
   }
@@ -457,6 +715,7 @@ extern "C" int q3_model_close(q3_model *m) {
   }
   if (m->ptab) (void)hipFree(m->ptab);
   if (m->keys) (void)hipFree(m->keys);
+  if (m->keys_ws) (void)hipFree(m->keys_ws);
   delete m;
   return rc;
 }

@@ -91,6 +91,47 @@ int gemm_common(const q3_view *a, const q3_view *a_scale, const q3_view *b,
   return Q3_OK;
 }
 
+// Decode-shaped STORE/ADD/ARGMAX GEMMs go to the whole-chip GEMV kernel.
+bool use_gemv(const q3::GemmArgs &g) {
+  return q3::gemv_supported(g.M, g.K, g.group) && g.ldb == g.K && g.bs_stride == 1 &&
+         (g.epi == q3::EPI_STORE || g.epi == q3::EPI_ADD || g.epi == q3::EPI_ARGMAX);
+}
+
+q3::GemvArgs to_gemv(const q3::GemmArgs &g) {
+  q3::GemvArgs v;
+  std::memset(&v, 0, sizeof(v));
+  v.M = g.M;
+  v.K = g.K;
+  v.group = g.group;
+  v.a = g.a;
+  v.lda = g.lda;
+  v.as = g.as;
+  v.ldas = g.ldas;
+  v.pro = q3::PRO_NONE;
+  v.nseg = 1;
+  v.seg[0].n0 = 0;
+  v.seg[0].n1 = g.N;
+  v.seg[0].epi = g.epi;
+  v.seg[0].b = g.b;
+  v.seg[0].bs = g.bs;
+  v.seg[0].out = g.out;
+  v.seg[0].ldo = g.ldo;
+  v.keys = g.keys;
+  v.keys_ld = g.keys_ld;
+  return v;
+}
+
+hipError_t launch_gemm_or_gemv(const q3::GemmArgs &g, hipStream_t s) {
+  if (!use_gemv(g)) return q3::launch_gemm(g, s);
+  return q3::launch_gemv(to_gemv(g), s);
+}
+
+// Per-workgroup argmax slots needed by launch_gemm_or_gemv for g.
+int argmax_slots(const q3::GemmArgs &g) {
+  if (use_gemv(g)) return g.N / q3::gemv_cols_per_block(to_gemv(g));
+  return g.N / 128;
+}
+
 int nrq_common(const q3_view *nw, const q3_view *cos, const q3_view *sin,
                uint32_t rows, float inv_hd, q3::GemmArgs &g) {
   int64_t nws = 1;
@@ -261,7 +302,7 @@ int q3_gemm_nt_group_store(const q3_view *a, const q3_view *a_scale,
     g.out = static_cast<float *>(out->data);
     g.ldo = ld(out);
   }
-  return hip_status(q3::launch_gemm(g, static_cast<hipStream_t>(stream)));
+  return hip_status(launch_gemm_or_gemv(g, static_cast<hipStream_t>(stream)));
 }
 
 int q3_gemm_nt_group_kv_paged(const q3_view *a, const q3_view *a_scale,
@@ -389,6 +430,8 @@ int q3_attention_heads_gqa_tokscale_paged(const q3_view *q8,
   t.os = static_cast<float *>(os->data);
   t.ldos = os->row_bytes / 4;
   t.os_col = os->col_bytes / 4;
+  if (q3::attn_decode_supported(t))
+    return hip_status(q3::launch_attn_decode(t, static_cast<hipStream_t>(stream)));
   return hip_status(q3::launch_attention(t, static_cast<hipStream_t>(stream)));
 }
 
@@ -441,8 +484,11 @@ int q3_gemm_gate_up_swiglu_quant(const q3_view *a, const q3_view *a_scale,
 
 // ---- lm_head + argmax: per-device key workspace ---------------------------
 namespace {
+// One key per (row, column block): 4 MiB of slots (e.g. 256 rows x 1187
+// lm_head blocks of 128 columns).
 constexpr int kMaxArgmaxRows = 256;
-__device__ unsigned long long g_argmax_keys[kMaxArgmaxRows];
+constexpr int64_t kArgmaxSlots = int64_t(1) << 19;
+__device__ unsigned long long g_argmax_keys[kArgmaxSlots];
 }  // namespace
 
 namespace q3 {
@@ -486,11 +532,15 @@ extern "C" int q3_gemm_nt_group_argmax(const q3_view *a, const q3_view *a_scale,
   if (!keys) return Q3_ERR_HIP;
   g.epi = q3::EPI_ARGMAX;
   g.keys = keys;
+  const int nslots = argmax_slots(g);
+  if (static_cast<int64_t>(g.M) * nslots > kArgmaxSlots) return Q3_ERR_UNSUPPORTED;
+  g.keys_ld = nslots;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  Q3_TRY(hip_status(q3::launch_gemm(g, s)));
-  return hip_status(q3::launch_argmax_finish(keys, g.M, static_cast<float *>(best->data), bst,
-                                             static_cast<int32_t *>(bidx->data), ist, 0,
-                                             nullptr, nullptr, 0, s));
+  Q3_TRY(hip_status(launch_gemm_or_gemv(g, s)));
+  return hip_status(q3::launch_argmax_finish(keys, nslots, nslots, g.M,
+                                             static_cast<float *>(best->data), bst,
+                                             static_cast<int32_t *>(bidx->data), ist, 0, nullptr,
+                                             nullptr, 0, s));
 }
 
 extern "C" int q3_argmax_logits(const q3_view *logits, int32_t *out_id, void *stream) {

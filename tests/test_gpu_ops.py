@@ -185,6 +185,28 @@ def test_attention_paged(cuda, rows, kv_len):
     assert bits_equal(host(os_), ros), describe_diff(host(os_), ros)
 
 
+@pytest.mark.parametrize("heads,kvh,kv_len", [(16, 8, 1023), (16, 8, 1025), (16, 8, 2500),
+                                              (8, 8, 77), (8, 8, 1100)])
+def test_attention_decode_chunks(cuda, heads, kvh, kv_len):
+    """One query row (the decode kernel): key counts around and beyond the
+    1024-key chunk of the parallel form, GQA groups 2 and 1."""
+    note(f"attention decode heads={heads}/{kvh} kv_len={kv_len}")
+    rng = np.random.default_rng(kv_len + heads)
+    n_pages = (kv_len + 31) // 32 + 2
+    (k8, v8, ks, vs), (kp, vp, ksp, vsp, table) = make_pages(rng, kv_len, kvh * 128, kvh, n_pages)
+    q8 = rng.integers(-127, 128, (1, heads * 128)).astype(np.int8)
+    qs = rng.uniform(1e-3, 5e-2, (1, heads)).astype(F)
+    kv = ops.paged_kv(dev(kp), dev(vp), dev(ksp), dev(vsp), dev(table.view(np.int16)))
+    o8 = torch.zeros((1, heads * 128), dtype=torch.int8, device=cuda)
+    os_ = torch.zeros((1, heads), dtype=torch.float32, device=cuda)
+    ops.attention_heads_gqa_tokscale_paged(dev(q8), dev(qs), kv, kv_len, o8, os_, heads, kvh, 128,
+                                           True, QK)
+    attn = oracle.attention_heads_gqa_tokscale(q8, qs, k8, ks, v8, vs, heads, kvh, 128, True, QK)
+    ro8, ros = oracle.quant_rows_heads(attn, 128)
+    assert bits_equal(host(o8), ro8), describe_diff(host(o8), ro8)
+    assert bits_equal(host(os_), ros), describe_diff(host(os_), ros)
+
+
 @pytest.mark.parametrize("case,rows,kv_len", [("pa", 4, 80), ("pm1", 8, 48)])
 def test_attention_guest_fixture(cuda, case, rows, kv_len):
     """The reference's paged-attention guest inputs (4 heads / 2 kv heads,
