@@ -46,7 +46,7 @@ __global__ void __launch_bounds__(256) attention_kernel(AttnArgs a) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = wave_id();
   const int lr = lane & 15;
   const int lg = lane >> 4;
   const int h = blockIdx.x;

@@ -6,7 +6,7 @@
 // Only the carried den/res updates are inherently sequential; everything
 // else depends on the blocks plus the running maximum, and the running
 // maximum is a prefix max of the per-block maxima.  So per chunk of up to
-// 24 blocks (768 keys):
+// CB = NW * BPW blocks:
 //   phase 1 (parallel over blocks)  S_j = q8.k8^T (v_dot4_i32_i8, exact),
 //                                   s = ((f32 S * ks) * qs) * qk, block max
 //   phase 2 (sequential, tiny)      nmm_j = max(nmm_{j-1}, max_j)
@@ -18,19 +18,20 @@
 // with the same rounding points as the reference, so the result is bit-equal
 // to the sequential walk.  Chunks carry (maximum, den, res) like blocks do.
 //
-// One workgroup per KV head handles its GRP (1 or 2) query heads (GQA), so
-// K and V are read once per token per KV head.  8 waves own blocks
-// round-robin (at most 3 per chunk each).  The kernel is latency-bound, so
-// every global load of a chunk (page-table entries, K and V rows, their
-// scales) is issued before any of it is used, V stays in registers from
-// phase 1 to phase 3, and the exp table lives in LDS.
+// A workgroup handles QPW query heads of one KV head (the kernel supports
+// QPW = 1 and 2; with QPW = 1 the workgroups of a GQA pair each read the
+// pair's K/V).  NW waves own blocks round-robin, BPW per chunk each.  The
+// kernel is latency-bound, so its global loads are issued in the order they
+// are needed (vector loads return in order): first the prologue's operands,
+// then every K/V row and scale of the chunk; V stays in registers from
+// phase 1 to phase 3 and the exp table lives in LDS.
 //
 // Optional prologue (decode fusion): the head epilogues of the new token's
 // Q/K/V projection rows (kernels/norm_rope_quant.h:17-86 for Q and K,
 // group_gemm.h:173-193 for V) run here, one wave per head.  They write the
-// K/V page slot of position kv_len - 1 and the Q int8 row for the record,
-// and keep copies in LDS that the attention uses in place of re-reading
-// global memory (the first chunk's loads are already in flight by then).
+// K/V page slot of position kv_len - 1 (one workgroup per KV head) and the Q
+// int8 row for the record, and keep copies in LDS that the attention uses in
+// place of the global K/V of that position.
 #include "q3_device.h"
 #include "q3_kernels.h"
 
@@ -38,94 +39,145 @@ namespace q3 {
 namespace {
 
 constexpr int HD = 128;
-constexpr int CB = 24;         // blocks per chunk (768 keys)
-constexpr int NW = 8;          // waves per workgroup
-constexpr int BPW = CB / NW;   // blocks per wave per chunk
 
 __device__ __forceinline__ int sdot4(int a, int b, int c) {
   return __builtin_amdgcn_sdot4(a, b, c, false);
 }
 
-template <int GRP>
+// P8.V of one 32-key block for the lanes' layout of phase 3: lane l holds
+// vw[cc] = the 4 int8 values of dims d0..d0+3 (d0 = 4 (l % 32)) of key
+// kh + cc (kh = 16 (l / 32)), and p8 of key c for head h sits in lane
+// 32 h + c.  acc[h][e] += sum over the 16 keys of p8[h][key] * v[key][d0+e],
+// exact in int32.  4x4 byte tiles (4 keys x 4 dims) are transposed with
+// v_perm_b32 so that v_dot4_i32_i8 multiplies 4 keys at once; the P8 bytes of
+// 4 consecutive keys are packed with DPP quad broadcasts.
+template <int QPW>
+__device__ __forceinline__ void pv_dot(const int (&vw)[16], int p8, int lane, int (&acc)[QPW][4]) {
+  const int b = p8 & 0xff;
+  const int q0 = __builtin_amdgcn_mov_dpp(b, 0x00, 0xf, 0xf, false);  // quad lane 0
+  const int q1 = __builtin_amdgcn_mov_dpp(b, 0x55, 0xf, 0xf, false);  // quad lane 1
+  const int q2 = __builtin_amdgcn_mov_dpp(b, 0xaa, 0xf, 0xf, false);
+  const int q3 = __builtin_amdgcn_mov_dpp(b, 0xff, 0xf, 0xf, false);
+  const int packed = q0 | (q1 << 8) | (q2 << 16) | (q3 << 24);  // keys 4q..4q+3
+  const bool upper = lane >= 32;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const uint32_t w0 = vw[4 * g], w1 = vw[4 * g + 1], w2 = vw[4 * g + 2], w3 = vw[4 * g + 3];
+    const uint32_t x01l = __builtin_amdgcn_perm(w1, w0, 0x06020400u);
+    const uint32_t x01h = __builtin_amdgcn_perm(w1, w0, 0x07030501u);
+    const uint32_t x23l = __builtin_amdgcn_perm(w3, w2, 0x06020400u);
+    const uint32_t x23h = __builtin_amdgcn_perm(w3, w2, 0x07030501u);
+    const int r[4] = {static_cast<int>(__builtin_amdgcn_perm(x23l, x01l, 0x05040100u)),
+                      static_cast<int>(__builtin_amdgcn_perm(x23h, x01h, 0x05040100u)),
+                      static_cast<int>(__builtin_amdgcn_perm(x23l, x01l, 0x07060302u)),
+                      static_cast<int>(__builtin_amdgcn_perm(x23h, x01h, 0x07060302u))};
+#pragma unroll
+    for (int h = 0; h < QPW; ++h) {
+      const int pa = __builtin_amdgcn_readlane(packed, 32 * h + 4 * g);
+      const int pb = __builtin_amdgcn_readlane(packed, 32 * h + 16 + 4 * g);
+      const int pk = upper ? pb : pa;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[h][e] = sdot4(pk, r[e], acc[h][e]);
+    }
+  }
+}
+
+template <int QPW, int CB>
 struct Smem {
   uint64_t tab[32];
-  int8_t q8[GRP][HD];
-  float qs[GRP];
+  int8_t q8[QPW][HD];
+  float qs[QPW];
   int8_t knew[HD], vnew[HD];
   float ksnew, vsnew;
-  float s[GRP][CB * 32];  // scores of the chunk
-  float bmax[GRP][CB];
-  float prev[GRP][CB], nmm[GRP][CB];
-  float corr[GRP][CB], psum[GRP][CB];
-  float pv[GRP][CB][HD];  // f32(P8.V) * pmax per block
-  float run[GRP];
-  float absmax[GRP][2];
+  float s[QPW][CB * 32];  // scores of the chunk
+  float bmax[QPW][CB];
+  float prev[QPW][CB], nmm[QPW][CB];
+  float corr[QPW][CB], psum[QPW][CB];
+  float pv[QPW][CB][HD];  // f32(P8.V) * pmax per block
+  float run[QPW];
+  float absmax[QPW][2];
 };
 
-template <int GRP>
-__device__ void fused_heads(const AttnArgs &a, Smem<GRP> &sm, int kvh, int wave, int lane) {
-  // wave 0: K head kvh, wave 1: V head kvh, waves 2..: Q heads kvh*GRP + h
-  if (wave >= 2 + GRP) return;
+// Operands of the fused head epilogue of one wave (see fused_load).
+struct FusedRegs {
+  float t0, t1, w0, w1, c, s;
+};
+
+// wave 0: K head kvh, wave 1: V head kvh, waves 2..: query heads qh0 + h
+template <int QPW>
+__device__ __forceinline__ void fused_load(const AttnArgs &a, int kvh, int qh0, int wave, int lane,
+                                           FusedRegs &r) {
+  if (wave >= 2 + QPW) return;
+  const float *src = wave == 0 ? a.fk + kvh * HD : wave == 1 ? a.fv + kvh * HD : a.fq + (qh0 + wave - 2) * HD;
+  r.t0 = src[lane];
+  r.t1 = src[lane + 64];
+  if (wave != 1) {
+    const float *nw = wave == 0 ? a.nk : a.nq;
+    r.w0 = nw[lane];
+    r.w1 = nw[lane + 64];
+    r.c = a.cos_row[lane];
+    r.s = a.sin_row[lane];
+  }
+}
+
+template <int QPW, class SM>
+__device__ void fused_compute(const AttnArgs &a, SM &sm, FusedRegs r, int kvh, int qh0,
+                              bool kv_writer, int wave, int lane) {
+  if (wave >= 2 + QPW) return;
   const uint32_t t = a.kv_len - 1;  // the new token
-  const float *src;
-  if (wave == 0)
-    src = a.fk + kvh * HD;
-  else if (wave == 1)
-    src = a.fv + kvh * HD;
-  else
-    src = a.fq + (kvh * GRP + wave - 2) * HD;
-  float t0 = src[lane], t1 = src[lane + 64];
-  if (wave != 1)
-    head_norm_rope(t0, t1, lane, wave == 0 ? a.nk : a.nq, 1, a.cos_row, a.sin_row, a.inv_hd, true);
+  float t0 = r.t0, t1 = r.t1;
+  if (wave != 1) head_norm_rope_regs(t0, t1, r.w0, r.w1, r.c, r.s, a.inv_hd, true);
   const float mx = max64(fmaxf(fabsf(t0), fabsf(t1)));
   const float scale = __fmul_rn(mx, inv127());
   const int8_t q0 = static_cast<int8_t>(quant1(t0, scale));
   const int8_t q1 = static_cast<int8_t>(quant1(t1, scale));
-  int8_t *row8;
-  float *sp;
   int8_t *lrow;
   float *lsp;
   if (wave < 2) {
-    const uint32_t page = a.table[t / a.page_tokens];
-    const uint32_t slot = t % a.page_tokens;
-    row8 = const_cast<int8_t *>(wave == 0 ? a.k : a.v) + page * a.page_bytes + slot * a.row_bytes +
-           kvh * HD;
-    sp = reinterpret_cast<float *>(reinterpret_cast<int8_t *>(const_cast<float *>(wave == 0 ? a.ks : a.vs)) +
-                                   page * a.scale_page_bytes + slot * a.scale_row_bytes) + kvh;
     lrow = wave == 0 ? sm.knew : sm.vnew;
     lsp = wave == 0 ? &sm.ksnew : &sm.vsnew;
+    if (kv_writer) {
+      const uint32_t page = a.table[t / a.page_tokens];
+      const uint32_t slot = t % a.page_tokens;
+      int8_t *row8 = const_cast<int8_t *>(wave == 0 ? a.k : a.v) + page * a.page_bytes +
+                     slot * a.row_bytes + kvh * HD;
+      float *sp = reinterpret_cast<float *>(reinterpret_cast<int8_t *>(const_cast<float *>(wave == 0 ? a.ks : a.vs)) +
+                                            page * a.scale_page_bytes + slot * a.scale_row_bytes) + kvh;
+      row8[lane] = q0;
+      row8[lane + 64] = q1;
+      if (lane == 0) *sp = scale;
+    }
   } else {
-    const int h = wave - 2;
-    const int qh = kvh * GRP + h;
-    row8 = const_cast<int8_t *>(a.q8) + qh * HD;
-    sp = const_cast<float *>(a.qs) + qh * a.qs_col;
-    lrow = sm.q8[h];
-    lsp = &sm.qs[h];
+    const int qh = qh0 + wave - 2;
+    int8_t *row8 = const_cast<int8_t *>(a.q8) + qh * HD;
+    row8[lane] = q0;
+    row8[lane + 64] = q1;
+    if (lane == 0) const_cast<float *>(a.qs)[qh * a.qs_col] = scale;
+    lrow = sm.q8[wave - 2];
+    lsp = &sm.qs[wave - 2];
   }
-  row8[lane] = q0;
-  row8[lane + 64] = q1;
   lrow[lane] = q0;
   lrow[lane + 64] = q1;
-  if (lane == 0) {
-    *sp = scale;
-    *lsp = scale;
-  }
+  if (lane == 0) *lsp = scale;
 }
 
-template <int GRP>
+template <int QPW, int NW, int BPW>
 __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
-  __shared__ __align__(16) Smem<GRP> sm;
+  constexpr int CB = NW * BPW;
+  __shared__ __align__(16) Smem<QPW, CB> sm;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int kvh = blockIdx.x;
+  const int wave = wave_id();
+  const int grp = a.heads / a.kv_heads;
+  const int qh0 = blockIdx.x * QPW;
+  const int kvh = qh0 / grp;
+  const bool kv_writer = (qh0 % grp) == 0;
   const uint32_t kv_len = a.kv_len;
   // one query row: pos0 = kv_len - 1, so kv_end = kv_len and the causal mask
   // only removes keys >= kv_len (attention_gqa.h:454-458)
   const int pos0 = static_cast<int>(kv_len) - 1;
   const int kv_end = static_cast<int>(kv_len);
   const int nblocks = (kv_end + 31) / 32;
-  const int sr = static_cast<int>(a.scale_row_bytes / 4);
   const int half = lane & 1;   // phase 1: lane pair (2c, 2c+1) on key c,
   const int kc = lane >> 1;    //   lane parity picks dims [0,64) / [64,128)
   const int d0 = 4 * (lane & 31);   // phase 3: 4 dims per lane,
@@ -134,8 +186,21 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
   const int ph = tid / HD;  // phase-4 ownership: (head, dim)
   const int pd = tid % HD;
   float res = 0.0f, den = 0.0f;
-  int qv[GRP][16];
-  float qscale[GRP];
+  int qv[QPW][16];
+  float qscale[QPW];
+
+  // prologue operands first
+  FusedRegs fr{};
+  int8_t q8a = 0, q8b = 0;
+  float qsa = 0.0f;
+  if (a.fuse_heads) {
+    fused_load<QPW>(a, kvh, qh0, wave, lane, fr);
+  } else if (wave < QPW) {
+    const int qh = qh0 + wave;
+    q8a = a.q8[qh * HD + lane];
+    q8b = a.q8[qh * HD + lane + 64];
+    qsa = a.qs[qh * a.qs_col];
+  }
 
   for (int b0 = 0; b0 < nblocks; b0 += CB) {
     const int nb = min(CB, nblocks - b0);
@@ -181,18 +246,17 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
     if (b0 == 0) {
       // ---- prologue (overlaps the loads above) ----
       if (tid < 32) sm.tab[tid] = kExp2Tab[tid];
-      if (tid < GRP) sm.run[tid] = -3.402823466e38f;
+      if (tid < QPW) sm.run[tid] = -3.402823466e38f;
       if (a.fuse_heads) {
-        fused_heads<GRP>(a, sm, kvh, wave, lane);
-      } else if (wave < GRP) {
-        const int qh = kvh * GRP + wave;
-        sm.q8[wave][lane] = a.q8[qh * HD + lane];
-        sm.q8[wave][lane + 64] = a.q8[qh * HD + lane + 64];
-        if (lane == 0) sm.qs[wave] = a.qs[qh * a.qs_col];
+        fused_compute<QPW>(a, sm, fr, kvh, qh0, kv_writer, wave, lane);
+      } else if (wave < QPW) {
+        sm.q8[wave][lane] = q8a;
+        sm.q8[wave][lane + 64] = q8b;
+        if (lane == 0) sm.qs[wave] = qsa;
       }
       __syncthreads();
 #pragma unroll
-      for (int h = 0; h < GRP; ++h) {
+      for (int h = 0; h < QPW; ++h) {
         const int *qp = reinterpret_cast<const int *>(sm.q8[h] + half * 64);
 #pragma unroll
         for (int e = 0; e < 16; ++e) qv[h][e] = qp[e];
@@ -225,7 +289,7 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
       const int j = (b0 + jb) * 32;
       const bool valid = j + kc < kv_end;
 #pragma unroll
-      for (int h = 0; h < GRP; ++h) {
+      for (int h = 0; h < QPW; ++h) {
         int acc = 0;
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc = sdot4(qv[h][e], kw[i][e], acc);
@@ -244,7 +308,7 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
     }
     __syncthreads();
     // ---- phase 2: prefix max (attention_gqa.h:476-477) ----
-    if (tid < GRP) {
+    if (tid < QPW) {
       float run = sm.run[tid];
       for (int jb = 0; jb < nb; ++jb) {
         const float bm = sm.bmax[tid][jb];
@@ -265,9 +329,9 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
       const int c = lane & 31;
       const bool valid = j + c < kv_end;
 #pragma unroll
-      for (int hp = 0; hp < GRP; hp += 2) {
+      for (int hp = 0; hp < QPW; hp += 2) {
         const int h = hp + (lane >> 5);
-        const bool hok = h < GRP;
+        const bool hok = h < QPW;
         float p = 0.0f, pv = 0.0f;
         if (hok && valid) {
           p = exp_f32_tab(__fsub_rn(sm.s[h][jb * 32 + c], sm.nmm[h][jb]), sm.tab);
@@ -281,18 +345,7 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
           sm.corr[h][jb] = exp_f32_tab(__fsub_rn(sm.prev[h][jb], sm.nmm[h][jb]), sm.tab);
         }
         int acc[2][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
-#pragma unroll
-        for (int cc = 0; cc < 16; ++cc) {
-          const int key = kh + cc;
-          const int pa = __shfl(p8, key);       // head hp, key `key`
-          const int pb = __shfl(p8, 32 + key);  // head hp+1, key `key`
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int ve = static_cast<int>(static_cast<int8_t>(vw[i][cc] >> (8 * e)));
-            acc[0][e] += pa * ve;
-            acc[1][e] += pb * ve;
-          }
-        }
+        pv_dot<(QPW > 1 ? 2 : 1)>(vw[i], p8, lane, reinterpret_cast<int(&)[(QPW > 1 ? 2 : 1)][4]>(acc));
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
@@ -303,7 +356,7 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
 #pragma unroll
           for (int s2 = 0; s2 < 2; ++s2) {
             const int hh = hp + s2;
-            if (hh < GRP) {
+            if (hh < QPW) {
               const float pmh = s2 ? pm1 : pm0;
               float4 o;
               o.x = __fmul_rn(static_cast<float>(acc[s2][0]), pmh);
@@ -318,7 +371,7 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
     }
     __syncthreads();
     // ---- phase 4: the sequential den/res chain (attention_gqa.h:476-519) ----
-    if (tid < GRP * HD) {
+    if (tid < QPW * HD) {
       for (int jb = 0; jb < nb; ++jb) {
         const float corr = sm.corr[ph][jb];
         den = __fadd_rn(__fmul_rn(den, corr), sm.psum[ph][jb]);
@@ -330,19 +383,30 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
 
   // ---- epilogue: out = res * (1/den); per-head int8 quant (522-546) ----
   float out = 0.0f;
-  if (tid < GRP * HD) {
+  if (tid < QPW * HD) {
     out = __fmul_rn(res, __fdiv_rn(1.0f, den));
     const float m = max64(fabsf(out));
     if (lane == 0) sm.absmax[ph][(tid % HD) / 64] = m;
   }
   __syncthreads();
-  if (tid < GRP * HD) {
-    const int qh = kvh * GRP + ph;
+  if (tid < QPW * HD) {
+    const int qh = qh0 + ph;
     const float scale = __fmul_rn(fmaxf(sm.absmax[ph][0], sm.absmax[ph][1]), inv127());
     if (a.attn) a.attn[qh * HD + pd] = out;
     a.o8[qh * HD + pd] = static_cast<int8_t>(quant1(out, scale));
     if (pd == 0) a.os[qh * a.os_col] = scale;
   }
+}
+
+// One workgroup per query head (QPW = 1): 16 workgroups for the 16/8-head
+// model instead of 8 halves the per-workgroup work, which matters more here
+// than reading each KV head's rows twice.  8 waves x 3 blocks (768 keys per
+// chunk) keep K and V of the chunk in registers without spilling.
+hipError_t launch_decode(const AttnArgs &a, hipStream_t s) {
+  constexpr int QPW = 1, NW = 8, BPW = 3;
+  static_assert(QPW * HD <= NW * 64, "phase 4 needs a thread per (head, dim)");
+  hipLaunchKernelGGL((attn_decode_kernel<QPW, NW, BPW>), dim3(a.heads / QPW), dim3(NW * 64), 0, s, a);
+  return hipGetLastError();
 }
 
 }  // namespace
@@ -355,14 +419,6 @@ bool attn_decode_supported(const AttnArgs &a) {
          al16(a.q8) && (a.scale_row_bytes % 4) == 0 && a.kv_len >= 1 && !a.kv_len_dev;
 }
 
-hipError_t launch_attn_decode(const AttnArgs &a, hipStream_t s) {
-  const int grp = a.heads / a.kv_heads;
-  const dim3 grid(a.kv_heads, 1);
-  if (grp == 1)
-    hipLaunchKernelGGL(attn_decode_kernel<1>, grid, dim3(NW * 64), 0, s, a);
-  else
-    hipLaunchKernelGGL(attn_decode_kernel<2>, grid, dim3(NW * 64), 0, s, a);
-  return hipGetLastError();
-}
+hipError_t launch_attn_decode(const AttnArgs &a, hipStream_t s) { return launch_decode(a, s); }
 
 }  // namespace q3

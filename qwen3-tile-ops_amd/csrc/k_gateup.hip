@@ -42,7 +42,7 @@ __global__ void __launch_bounds__(256) gate_up_kernel(GateUpArgs a) {
   __shared__ float tile[BM * LDT];
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = wave_id();
   const int lr = lane & 15;
   const int lg = lane >> 4;
   const int m0 = blockIdx.y * BM;

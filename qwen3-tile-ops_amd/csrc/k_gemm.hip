@@ -80,7 +80,7 @@ __global__ void __launch_bounds__(256) gemm_group_kernel(GemmArgs a) {
   __shared__ float tile[(EPI >= EPI_HEADQ) ? BM * LDT : 1];
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = wave_id();
   const int lr = lane & 15;
   const int lg = lane >> 4;
   const int m0 = blockIdx.y * BM;

@@ -57,94 +57,124 @@ __device__ __forceinline__ float swiglu1(float g, float u, const uint64_t *tab) 
   return __fmul_rn(__fmul_rn(g, e), u);
 }
 
-// Builds the int8 A operand of M rows (K columns, 256-column groups) in LDS.
-// Thread layout: wave w walks groups w, w+4, ...; lane l owns columns
-// 4l..4l+3 of the group, so a 32-column RMSNorm block is 8 lanes (the
-// reference's pairwise tree: in-thread pairs, then xor 1/2/4), and a
-// quantisation group is one wave.
-__device__ void gemv_prologue(const GemvArgs &a, int8_t *a_lds, float *as_lds, float *blk) {
+// The prologue builds the int8 A operand of M rows (K = 1024*QW columns,
+// 256-column groups) in LDS.  Thread layout: wave w owns groups w, w+4, ...
+// (QW of them); lane l owns columns 4l..4l+3 of a group, so a 32-column
+// RMSNorm block is 8 lanes (the reference's pairwise tree: in-thread pairs,
+// then xor 1/2/4), and a quantisation group is one wave.
+//
+// A row's global operands are loaded into registers in one go
+// (pro_load_row) before any of them is used.  The kernel loads row 0 before
+// it issues the weight stream: vector loads return in order, so operands
+// requested after the weights would wait for all of them.
+template <int QW>
+struct ProRow {
+  float4 x[QW];     // f32 row (PRO_NORM / PRO_QUANT)
+  float4 w[QW];     // RMSNorm gain (PRO_NORM / PRO_EMBED)
+  uint32_t e[QW];   // four int8 embedding values (PRO_EMBED)
+  float esc;        // embedding row scale
+};
+
+template <int QW>
+__device__ __forceinline__ void pro_load_row(const GemvArgs &a, int m, ProRow<QW> &r) {
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = wave_id();
   const int K = a.K;
-  const int ngr = K / 256;
-  const int nblk = K / 32;
-  const bool write_stage = blockIdx.x == 0;
-  for (int m = 0; m < a.M; ++m) {
-    int32_t id = 0;
-    bool id_ok = false;
-    if (a.pro == PRO_EMBED) {
-      id = a.ids[m];
-      id_ok = id >= 0 && id < a.vocab;
-    }
-    auto load4 = [&](int c, float v[4]) {
-      if (a.pro == PRO_EMBED) {
-        if (id_ok) {
-          const char4 e = *reinterpret_cast<const char4 *>(a.emb + static_cast<int64_t>(id) * K + c);
-          const float sc = a.emb_s[id];
-          v[0] = __fmul_rn(static_cast<float>(e.x), sc);
-          v[1] = __fmul_rn(static_cast<float>(e.y), sc);
-          v[2] = __fmul_rn(static_cast<float>(e.z), sc);
-          v[3] = __fmul_rn(static_cast<float>(e.w), sc);
-        } else {
-          v[0] = v[1] = v[2] = v[3] = 0.0f;
-        }
-      } else {
-        const float4 x = *reinterpret_cast<const float4 *>(a.x + static_cast<int64_t>(m) * a.ldx + c);
-        v[0] = x.x;
-        v[1] = x.y;
-        v[2] = x.z;
-        v[3] = x.w;
-      }
-    };
-    float rinv = 1.0f;
-    if (a.pro != PRO_QUANT) {
-      for (int g = wave; g < ngr; g += 4) {
-        const int c = g * 256 + 4 * lane;
-        float v[4];
-        load4(c, v);
-        if (a.pro == PRO_EMBED && write_stage && a.x_out)
-          *reinterpret_cast<float4 *>(a.x_out + static_cast<int64_t>(m) * a.ldx + c) =
-              make_float4(v[0], v[1], v[2], v[3]);
-        float s = __fadd_rn(__fadd_rn(__fmul_rn(v[0], v[0]), __fmul_rn(v[1], v[1])),
-                            __fadd_rn(__fmul_rn(v[2], v[2]), __fmul_rn(v[3], v[3])));
-        s = __fadd_rn(s, __shfl_xor(s, 1));
-        s = __fadd_rn(s, __shfl_xor(s, 2));
-        s = __fadd_rn(s, __shfl_xor(s, 4));
-        if ((lane & 7) == 0) blk[g * 8 + (lane >> 3)] = s;
-      }
-      __syncthreads();
-      float ss = 0.0f;
-      for (int b = 0; b < nblk; ++b) ss = __fadd_rn(ss, blk[b]);
-      rinv = rms_factor(ss, a.inv_pre);
-    }
-    for (int g = wave; g < ngr; g += 4) {
-      const int c = g * 256 + 4 * lane;
-      float v[4];
-      load4(c, v);
-      if (a.pro != PRO_QUANT) {
+  if (a.pro == PRO_EMBED) {
+    const int32_t id = a.ids[m];
+    const bool ok = id >= 0 && id < a.vocab;  // out-of-range ids embed to zero
+    r.esc = ok ? a.emb_s[id] : 0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = __fmul_rn(__fmul_rn(v[i], rinv), a.w_pre[c + i]);
-        if (write_stage && a.h_out)
-          *reinterpret_cast<float4 *>(a.h_out + static_cast<int64_t>(m) * K + c) =
-              make_float4(v[0], v[1], v[2], v[3]);
-      }
-      float mx = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-      mx = max64(mx);
-      const float scale = __fmul_rn(mx, inv127());
-      char4 q;
-      q.x = static_cast<signed char>(quant1(v[0], scale));
-      q.y = static_cast<signed char>(quant1(v[1], scale));
-      q.z = static_cast<signed char>(quant1(v[2], scale));
-      q.w = static_cast<signed char>(quant1(v[3], scale));
-      *reinterpret_cast<char4 *>(a_lds + m * K + c) = q;
-      if (lane == 0) as_lds[m * ngr + g] = scale;
-      if (write_stage) {
-        if (a.h8_out) *reinterpret_cast<char4 *>(a.h8_out + static_cast<int64_t>(m) * K + c) = q;
-        if (a.hs_out && lane == 0) a.hs_out[static_cast<int64_t>(m) * ngr + g] = scale;
-      }
+    for (int q = 0; q < QW; ++q) {
+      const int c = (wave + 4 * q) * 256 + 4 * lane;
+      r.e[q] = ok ? *reinterpret_cast<const uint32_t *>(a.emb + static_cast<int64_t>(id) * K + c) : 0u;
     }
-    __syncthreads();  // blk is reused by the next row
+  } else {
+#pragma unroll
+    for (int q = 0; q < QW; ++q) {
+      const int c = (wave + 4 * q) * 256 + 4 * lane;
+      r.x[q] = *reinterpret_cast<const float4 *>(a.x + static_cast<int64_t>(m) * a.ldx + c);
+    }
   }
+  if (a.pro != PRO_QUANT) {
+#pragma unroll
+    for (int q = 0; q < QW; ++q)
+      r.w[q] = *reinterpret_cast<const float4 *>(a.w_pre + (wave + 4 * q) * 256 + 4 * lane);
+  }
+}
+
+template <int QW>
+__device__ void pro_compute_row(const GemvArgs &a, int m, const ProRow<QW> &r, int8_t *a_lds,
+                                float *as_lds, float *blk) {
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_id();
+  const int K = a.K;
+  constexpr int ngr = 4 * QW;
+  const bool write_stage = blockIdx.x == 0;
+  float v[QW][4];
+#pragma unroll
+  for (int q = 0; q < QW; ++q) {
+    const int c = (wave + 4 * q) * 256 + 4 * lane;
+    if (a.pro == PRO_EMBED) {
+      const uint32_t e = r.e[q];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        v[q][i] = __fmul_rn(static_cast<float>(static_cast<int8_t>(e >> (8 * i))), r.esc);
+      if (write_stage && a.x_out)
+        *reinterpret_cast<float4 *>(a.x_out + static_cast<int64_t>(m) * a.ldx + c) =
+            make_float4(v[q][0], v[q][1], v[q][2], v[q][3]);
+    } else {
+      v[q][0] = r.x[q].x;
+      v[q][1] = r.x[q].y;
+      v[q][2] = r.x[q].z;
+      v[q][3] = r.x[q].w;
+    }
+  }
+  if (a.pro != PRO_QUANT) {
+#pragma unroll
+    for (int q = 0; q < QW; ++q) {
+      float s = __fadd_rn(__fadd_rn(__fmul_rn(v[q][0], v[q][0]), __fmul_rn(v[q][1], v[q][1])),
+                          __fadd_rn(__fmul_rn(v[q][2], v[q][2]), __fmul_rn(v[q][3], v[q][3])));
+      s = __fadd_rn(s, __shfl_xor(s, 1));
+      s = __fadd_rn(s, __shfl_xor(s, 2));
+      s = __fadd_rn(s, __shfl_xor(s, 4));
+      if ((lane & 7) == 0) blk[(wave + 4 * q) * 8 + (lane >> 3)] = s;
+    }
+    __syncthreads();
+    float ss = 0.0f;
+#pragma unroll
+    for (int b = 0; b < 8 * ngr; ++b) ss = __fadd_rn(ss, blk[b]);
+    const float rinv = rms_factor(ss, a.inv_pre);
+#pragma unroll
+    for (int q = 0; q < QW; ++q) {
+      const float w4[4] = {r.w[q].x, r.w[q].y, r.w[q].z, r.w[q].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[q][i] = __fmul_rn(__fmul_rn(v[q][i], rinv), w4[i]);
+      if (write_stage && a.h_out)
+        *reinterpret_cast<float4 *>(a.h_out + static_cast<int64_t>(m) * K + (wave + 4 * q) * 256 + 4 * lane) =
+            make_float4(v[q][0], v[q][1], v[q][2], v[q][3]);
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < QW; ++q) {
+    const int g = wave + 4 * q;
+    const int c = g * 256 + 4 * lane;
+    float mx = fmaxf(fmaxf(fabsf(v[q][0]), fabsf(v[q][1])), fmaxf(fabsf(v[q][2]), fabsf(v[q][3])));
+    mx = max64(mx);
+    const float scale = __fmul_rn(mx, inv127());
+    char4 qv;
+    qv.x = static_cast<signed char>(quant1(v[q][0], scale));
+    qv.y = static_cast<signed char>(quant1(v[q][1], scale));
+    qv.z = static_cast<signed char>(quant1(v[q][2], scale));
+    qv.w = static_cast<signed char>(quant1(v[q][3], scale));
+    *reinterpret_cast<char4 *>(a_lds + m * K + c) = qv;
+    if (lane == 0) as_lds[m * ngr + g] = scale;
+    if (write_stage) {
+      if (a.h8_out) *reinterpret_cast<char4 *>(a.h8_out + static_cast<int64_t>(m) * K + c) = qv;
+      if (a.hs_out && lane == 0) a.hs_out[static_cast<int64_t>(m) * ngr + g] = scale;
+    }
+  }
+  __syncthreads();  // blk is reused by the next row; A is complete
 }
 
 template <int GPW, int KSTEPS, int NT, int NMAT>
@@ -153,7 +183,7 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
   constexpr int NB = 16 * NT;       // columns per workgroup
   constexpr int PP = NB + 1;        // partial-tile pitch
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = wave_id();
   const int lr = lane & 15;
   const int lg = lane >> 4;
   const int M = a.M;
@@ -173,8 +203,11 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
   float *as_lds = reinterpret_cast<float *>(a_lds + ((M * K + 15) & ~15));
   float *blk = as_lds + M * (K / 256);
   __shared__ uint64_t exptab[32];
+  constexpr int QW = GPW * KSTEPS / 4;  // 256-column groups per wave
 
-  // weights first: their HBM latency overlaps the prologue below
+  // row 0's prologue operands, then the weight stream (see ProRow)
+  ProRow<QW> r0;
+  if (a.pro != PRO_NONE) pro_load_row<QW>(a, 0, r0);
   v4i bv[NMAT][NT][GPW][KSTEPS];
 #pragma unroll
   for (int gi = 0; gi < GPW; ++gi) {
@@ -199,7 +232,12 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
   const float *as;
   int64_t ldas;
   if (a.pro != PRO_NONE) {
-    gemv_prologue(a, a_lds, as_lds, blk);
+    pro_compute_row<QW>(a, 0, r0, a_lds, as_lds, blk);
+    for (int m = 1; m < M; ++m) {
+      ProRow<QW> r;
+      pro_load_row<QW>(a, m, r);
+      pro_compute_row<QW>(a, m, r, a_lds, as_lds, blk);
+    }
     arow = a_lds + (lr < M ? lr : 0) * K + lg * 16;
     as = as_lds;
     ldas = K / 256;
@@ -285,7 +323,7 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
 // (kernels/norm_rope_quant.h:17-86, group_gemm.h:173-193), from f32 rows.
 __global__ void __launch_bounds__(256) qkv_heads_kernel(QkvHeadArgs a) {
   const int lane = threadIdx.x & 63;
-  const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int item = blockIdx.x * 4 + wave_id();
   const int nh = a.q_heads + 2 * a.kv_heads;
   if (item >= a.M * nh) return;
   const int m = item / nh;
@@ -348,6 +386,8 @@ __global__ void __launch_bounds__(256) qkv_heads_kernel(QkvHeadArgs a) {
 template <int GPW, int KSTEPS, int NT, int NMAT>
 hipError_t launch_t(const GemvArgs &a, int ncols, hipStream_t s) {
   constexpr int NB = 16 * NT;
+  // the prologue gives each wave GPW * KSTEPS / 4 groups of 256 columns
+  if (a.pro != PRO_NONE && a.K != 256 * GPW * KSTEPS) return hipErrorInvalidValue;
   const int ngroups = a.K / a.group;
   size_t lds = sizeof(float) * NMAT * ngroups * 16 * (NB + 1);
   if (a.pro != PRO_NONE)
@@ -383,7 +423,7 @@ int gemv_cols_per_block(const GemvArgs &a) {
 
 hipError_t launch_gemv(const GemvArgs &a, hipStream_t s) {
   if (a.M <= 0) return hipSuccess;
-  if (a.pro != PRO_NONE && (a.K % 256 != 0 || a.M > 16)) return hipErrorInvalidValue;
+  if (a.pro != PRO_NONE && (a.K % 1024 != 0 || a.M > 16)) return hipErrorInvalidValue;
   int ncols = 0;
   for (int i = 0; i < a.nseg; ++i) ncols = a.seg[i].n1;
   const bool two = a.seg[0].epi == EPI_SWIGLU;

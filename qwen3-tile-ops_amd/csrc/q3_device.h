@@ -25,6 +25,14 @@ namespace q3 {
 
 constexpr int kWave = 64;
 
+// Index of the calling wave within its workgroup as a wave-uniform (scalar)
+// value.  The compiler cannot prove threadIdx.x / 64 uniform by itself; it
+// would then keep per-lane copies of anything selected by the wave index
+// (argument pointers included) instead of scalar registers.
+__device__ __forceinline__ int wave_id() {
+  return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+}
+
 __device__ __forceinline__ float bits_f32(uint32_t u) { return __uint_as_float(u); }
 __device__ __forceinline__ uint32_t f32_bits(float f) { return __float_as_uint(f); }
 
@@ -164,10 +172,10 @@ __device__ __forceinline__ float rms_factor(float ss, float inv) {
 // followed by rotate-half RoPE (norm_rope_quant.h:42-65,
 // ref_qwen3.py:180-191).  Block sums: lanes 0-31 of t0 are columns 0-31,
 // lanes 32-63 columns 32-63, t1 likewise for 64-127, added in column order.
-__device__ __forceinline__ void head_norm_rope(float &t0, float &t1, int lane,
-                                               const float *nw, int64_t nw_stride,
-                                               const float *cos_row, const float *sin_row,
-                                               float inv_hd, bool do_rope) {
+// Operands in registers: gains w0 = nw[lane], w1 = nw[lane + 64], and the
+// RoPE row's c = cos[lane], s = sin[lane].
+__device__ __forceinline__ void head_norm_rope_regs(float &t0, float &t1, float w0, float w1,
+                                                    float c, float s, float inv_hd, bool do_rope) {
   const float sa = tree_sum32(__fmul_rn(t0, t0));
   const float sb = tree_sum32(__fmul_rn(t1, t1));
   float ss = 0.0f;
@@ -176,16 +184,26 @@ __device__ __forceinline__ void head_norm_rope(float &t0, float &t1, int lane,
   ss = __fadd_rn(ss, __shfl(sb, 0));
   ss = __fadd_rn(ss, __shfl(sb, 32));
   const float rinv = rms_factor(ss, inv_hd);
-  const float y0 = __fmul_rn(__fmul_rn(t0, rinv), nw[static_cast<int64_t>(lane) * nw_stride]);
-  const float y1 = __fmul_rn(__fmul_rn(t1, rinv), nw[static_cast<int64_t>(lane + 64) * nw_stride]);
+  const float y0 = __fmul_rn(__fmul_rn(t0, rinv), w0);
+  const float y1 = __fmul_rn(__fmul_rn(t1, rinv), w1);
   if (do_rope) {
-    const float c = cos_row[lane], s = sin_row[lane];
     t0 = __fsub_rn(__fmul_rn(y0, c), __fmul_rn(y1, s));
     t1 = __fadd_rn(__fmul_rn(y0, s), __fmul_rn(y1, c));
   } else {
     t0 = y0;
     t1 = y1;
   }
+}
+
+__device__ __forceinline__ void head_norm_rope(float &t0, float &t1, int lane,
+                                               const float *nw, int64_t nw_stride,
+                                               const float *cos_row, const float *sin_row,
+                                               float inv_hd, bool do_rope) {
+  const float w0 = nw[static_cast<int64_t>(lane) * nw_stride];
+  const float w1 = nw[static_cast<int64_t>(lane + 64) * nw_stride];
+  const float c = do_rope ? cos_row[lane] : 0.0f;
+  const float s = do_rope ? sin_row[lane] : 0.0f;
+  head_norm_rope_regs(t0, t1, w0, w1, c, s, inv_hd, do_rope);
 }
 
 }  // namespace q3
