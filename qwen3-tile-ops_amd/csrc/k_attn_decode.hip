@@ -161,10 +161,38 @@ __device__ void fused_compute(const AttnArgs &a, SM &sm, FusedRegs r, int kvh, i
   if (lane == 0) *lsp = scale;
 }
 
+// Workgroup w of the pf_wgs prefetch workgroups reads 16 B per thread from
+// every (nthreads * 16)-byte chunk w, w + pf_wgs, ... of each range.  Four
+// loads are in flight per thread; the values only feed an empty asm
+// statement so that the loads are kept.
+__device__ void prefetch_ranges(const AttnArgs &a, int w) {
+  for (int r = 0; r < a.pf_n; ++r) {
+    const int8_t *base = a.pf[r];
+    const int64_t n16 = a.pf_bytes[r] / 16;
+    int64_t i = static_cast<int64_t>(w) * blockDim.x + threadIdx.x;
+    const int64_t stride = static_cast<int64_t>(a.pf_wgs) * blockDim.x;
+    for (; i + 3 * stride < n16; i += 4 * stride) {
+      const int4 v0 = reinterpret_cast<const int4 *>(base)[i];
+      const int4 v1 = reinterpret_cast<const int4 *>(base)[i + stride];
+      const int4 v2 = reinterpret_cast<const int4 *>(base)[i + 2 * stride];
+      const int4 v3 = reinterpret_cast<const int4 *>(base)[i + 3 * stride];
+      asm volatile("" ::"v"(v0.x), "v"(v1.x), "v"(v2.x), "v"(v3.x));
+    }
+    for (; i < n16; i += stride) {
+      const int4 v0 = reinterpret_cast<const int4 *>(base)[i];
+      asm volatile("" ::"v"(v0.x));
+    }
+  }
+}
+
 template <int QPW, int NW, int BPW>
 __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
   constexpr int CB = NW * BPW;
   __shared__ __align__(16) Smem<QPW, CB> sm;
+  if (static_cast<int>(blockIdx.x) >= a.heads / QPW) {  // prefetch workgroups
+    prefetch_ranges(a, static_cast<int>(blockIdx.x) - a.heads / QPW);
+    return;
+  }
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = wave_id();
@@ -405,7 +433,8 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
 hipError_t launch_decode(const AttnArgs &a, hipStream_t s) {
   constexpr int QPW = 1, NW = 8, BPW = 3;
   static_assert(QPW * HD <= NW * 64, "phase 4 needs a thread per (head, dim)");
-  hipLaunchKernelGGL((attn_decode_kernel<QPW, NW, BPW>), dim3(a.heads / QPW), dim3(NW * 64), 0, s, a);
+  const int extra = a.pf_n > 0 ? a.pf_wgs : 0;
+  hipLaunchKernelGGL((attn_decode_kernel<QPW, NW, BPW>), dim3(a.heads / QPW + extra), dim3(NW * 64), 0, s, a);
   return hipGetLastError();
 }
 
@@ -414,7 +443,10 @@ hipError_t launch_decode(const AttnArgs &a, hipStream_t s) {
 bool attn_decode_supported(const AttnArgs &a) {
   const int grp = a.kv_heads > 0 ? a.heads / a.kv_heads : 0;
   auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  for (int r = 0; r < a.pf_n; ++r)
+    if ((reinterpret_cast<uintptr_t>(a.pf[r]) & 15) != 0 || a.pf_bytes[r] < 0) return false;
   return a.rows == 1 && a.causal && (grp == 1 || grp == 2) && a.kv_heads * grp == a.heads &&
+         a.pf_n >= 0 && a.pf_n <= 8 && (a.pf_n == 0 || a.pf_wgs > 0) &&
          (a.row_bytes % 16) == 0 && (a.page_tokens % 32) == 0 && al16(a.k) && al16(a.v) &&
          al16(a.q8) && (a.scale_row_bytes % 4) == 0 && a.kv_len >= 1 && !a.kv_len_dev;
 }

@@ -23,6 +23,8 @@
 // rows of the same columns, swiglu_quant.h:195-231, stored as f32 for the
 // next prologue) and ARGMAX (lm_argmax.h:55-67: one (max, first index) key
 // per workgroup and row into a slot array, reduced by argmax_finish).
+#include <algorithm>
+
 #include "q3_device.h"
 #include "q3_kernels.h"
 
@@ -319,6 +321,153 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
   }
 }
 
+// Column-streaming variant for very wide single-segment launches (the
+// lm_head): a fixed grid walks 16*NT-column tiles t = blockIdx.x,
+// t + gridDim.x, ...  The A operand is built once per workgroup, the next
+// tile's weights are loaded (unconditionally, clamped to the last tile, so
+// that the loads stay in flight with a static count) while the current tile
+// is reduced, and EPI_ARGMAX keeps one running key per row, written to slot
+// blockIdx.x at the end.  Items (row m, column j) map to threads so that a
+// row's NB = 64 columns are one wave.
+template <int GPW, int KSTEPS, int NT>
+__global__ void __launch_bounds__(256) gemv_stream_kernel(GemvArgs a, int ntiles) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  constexpr int NB = 16 * NT;
+  constexpr int PP = NB + 1;
+  constexpr int QW = GPW * KSTEPS / 4;
+  static_assert(NB == 64, "argmax reduction assumes one wave per row");
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_id();
+  const int lr = lane & 15;
+  const int lg = lane >> 4;
+  const int M = a.M;
+  const int K = a.K;
+  const int G = a.group;
+  const int ngroups = K / G;
+  const GemvSeg &sg = a.seg[0];
+  float *part = reinterpret_cast<float *>(smem);
+  int8_t *a_lds = reinterpret_cast<int8_t *>(part + ngroups * 16 * PP);
+  float *as_lds = reinterpret_cast<float *>(a_lds + ((M * K + 15) & ~15));
+  float *blk = as_lds + M * (K / 256);
+
+  ProRow<QW> r0;
+  if (a.pro != PRO_NONE) pro_load_row<QW>(a, 0, r0);
+
+  auto load_tile = [&](v4i (&bv)[NT][GPW][KSTEPS], int t) {
+#pragma unroll
+    for (int gi = 0; gi < GPW; ++gi) {
+      const int g = min(wave + 4 * gi, ngroups - 1);
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks) {
+        const int k = g * G + ks * 64 + lg * 16;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const int8_t *b = sg.b + static_cast<int64_t>(t * NB + nt * 16 + lr) * K;
+          bv[nt][gi][ks] = *reinterpret_cast<const v4i *>(b + k);
+        }
+      }
+    }
+  };
+  int t = blockIdx.x;
+  v4i bv[NT][GPW][KSTEPS];
+  load_tile(bv, t);
+
+  const int8_t *arow;
+  const float *as;
+  int64_t ldas;
+  if (a.pro != PRO_NONE) {
+    pro_compute_row<QW>(a, 0, r0, a_lds, as_lds, blk);
+    for (int m = 1; m < M; ++m) {
+      ProRow<QW> r;
+      pro_load_row<QW>(a, m, r);
+      pro_compute_row<QW>(a, m, r, a_lds, as_lds, blk);
+    }
+    arow = a_lds + (lr < M ? lr : 0) * K + lg * 16;
+    as = as_lds;
+    ldas = K / 256;
+  } else {
+    arow = a.a + static_cast<int64_t>(lr < M ? lr : 0) * a.lda + lg * 16;
+    as = a.as;
+    ldas = a.ldas;
+  }
+  v4i av[GPW][KSTEPS];
+  float asv[GPW][4];
+#pragma unroll
+  for (int gi = 0; gi < GPW; ++gi) {
+    const int g = wave + 4 * gi;
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks)
+      av[gi][ks] = (g < ngroups && lr < M) ? *reinterpret_cast<const v4i *>(arow + g * G + ks * 64) : zero4();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = lg * 4 + i;
+      asv[gi][i] = (g < ngroups && m < M) ? as[static_cast<int64_t>(m) * ldas + g] : 0.0f;
+    }
+  }
+
+  unsigned long long best[4] = {0ull, 0ull, 0ull, 0ull};  // items tid + 256 k
+  for (; t < ntiles; t += gridDim.x) {
+    v4i bn[NT][GPW][KSTEPS];
+    load_tile(bn, min(t + static_cast<int>(gridDim.x), ntiles - 1));
+#pragma unroll
+    for (int gi = 0; gi < GPW; ++gi) {
+      const int g = wave + 4 * gi;
+      if (g >= ngroups) break;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        v4i acc = zero4();
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks)
+          acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[gi][ks], bv[nt][gi][ks], acc, 0, 0, 0);
+        const float bsv = sg.bs[t * NB + nt * 16 + lr];
+        float *pt = part + (g * 16) * PP + nt * 16 + lr;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          pt[(lg * 4 + i) * PP] = __fmul_rn(__fmul_rn(static_cast<float>(acc[i]), bsv), asv[gi][i]);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int it = threadIdx.x + 256 * kk;
+      if (it >= M * NB) break;
+      const int m = it / NB;
+      const int j = it % NB;
+      float out = 0.0f;
+      for (int g = 0; g < ngroups; ++g) out = __fadd_rn(out, part[(g * 16 + m) * PP + j]);
+      const int ncol = t * NB + j;
+      if (sg.epi == EPI_ARGMAX) {
+        const unsigned long long key = (static_cast<unsigned long long>(ordered_key(out)) << 32) |
+                                       (0xFFFFFFFFu - static_cast<uint32_t>(ncol));
+        best[kk] = key > best[kk] ? key : best[kk];
+      } else {
+        sg.out[static_cast<int64_t>(m) * sg.ldo + ncol] = out;
+      }
+    }
+    __syncthreads();  // part is rewritten by the next tile
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int gi = 0; gi < GPW; ++gi)
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) bv[nt][gi][ks] = bn[nt][gi][ks];
+  }
+  if (sg.epi == EPI_ARGMAX) {
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int it = threadIdx.x + 256 * kk;
+      if (it >= M * NB) break;  // wave-uniform: M * NB is a multiple of 64
+      unsigned long long key = best[kk];
+#pragma unroll
+      for (int sft = 1; sft < 64; sft <<= 1) {
+        const unsigned long long o = shfl_xor_u64(key, sft);
+        key = o > key ? o : key;
+      }
+      if (lane == 0) a.keys[static_cast<int64_t>(it / NB) * a.keys_ld + blockIdx.x] = key;
+    }
+  }
+}
+
 // Per (row, head) wave: the head epilogues of the Q/K/V projections
 // (kernels/norm_rope_quant.h:17-86, group_gemm.h:173-193), from f32 rows.
 __global__ void __launch_bounds__(256) qkv_heads_kernel(QkvHeadArgs a) {
@@ -415,21 +564,57 @@ bool gemv_supported(int M, int K, int group) {
          (K == 3072 && group == 256);
 }
 
-int gemv_cols_per_block(const GemvArgs &a) {
+namespace {
+
+int ncols_of(const GemvArgs &a) {
   int ncols = 0;
   for (int i = 0; i < a.nseg; ++i) ncols = a.seg[i].n1;
-  return ncols >= 65536 ? 64 : 16;
+  return ncols;
+}
+
+// Launches that take the column-streaming kernel: one wide segment
+// (lm_head: 151936 columns) of STORE or ARGMAX over K = 1024, group 256.
+bool use_stream(const GemvArgs &a) {
+  const int epi = a.seg[0].epi;
+  return a.nseg == 1 && ncols_of(a) >= 65536 && ncols_of(a) % 64 == 0 && a.K == 1024 && a.group == 256 &&
+         (epi == EPI_ARGMAX || epi == EPI_STORE);
+}
+
+int stream_grid(int ntiles) {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+      cus = n;
+    else
+      cus = 256;
+  }
+  return std::min(ntiles, 2 * cus);
+}
+
+}  // namespace
+
+int gemv_argmax_slots(const GemvArgs &a) {
+  const int ncols = ncols_of(a);
+  if (use_stream(a)) return stream_grid(ncols / 64);
+  return ncols / (ncols >= 65536 ? 64 : 16);
 }
 
 hipError_t launch_gemv(const GemvArgs &a, hipStream_t s) {
   if (a.M <= 0) return hipSuccess;
   if (a.pro != PRO_NONE && (a.K % 1024 != 0 || a.M > 16)) return hipErrorInvalidValue;
-  int ncols = 0;
-  for (int i = 0; i < a.nseg; ++i) ncols = a.seg[i].n1;
+  const int ncols = ncols_of(a);
+  if (use_stream(a)) {
+    const int ntiles = ncols / 64;
+    const size_t lds = sizeof(float) * 4 * 16 * 65 +
+                       (a.pro != PRO_NONE ? ((a.M * a.K + 15) & ~15) + sizeof(float) * (a.M * 4 + 32) : 0);
+    hipLaunchKernelGGL((gemv_stream_kernel<1, 4, 4>), dim3(stream_grid(ntiles)), dim3(256), lds, s, a, ntiles);
+    return hipGetLastError();
+  }
   const bool two = a.seg[0].epi == EPI_SWIGLU;
-  const int nb = gemv_cols_per_block(a);
   if (two) return dispatch_k<1, 2>(a, ncols, s);
-  if (nb == 64) return dispatch_k<4, 1>(a, ncols, s);
+  if (ncols >= 65536) return dispatch_k<4, 1>(a, ncols, s);
   return dispatch_k<1, 1>(a, ncols, s);
 }
 

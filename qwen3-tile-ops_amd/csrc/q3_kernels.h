@@ -157,6 +157,12 @@ struct AttnArgs {
   const float *nq, *nk;
   const float *cos_row, *sin_row;
   float inv_hd;
+  // decode kernel only: pf_wgs extra workgroups read these byte ranges once
+  // (values discarded) while the attention workgroups run, so that the
+  // kernels after it find their weights in the last-level cache
+  int pf_n, pf_wgs;
+  const int8_t *pf[8];
+  int64_t pf_bytes[8];
 };
 hipError_t launch_attention(const AttnArgs &a, hipStream_t s);
 
@@ -220,7 +226,8 @@ struct GemvArgs {
   int64_t keys_ld;
 };
 bool gemv_supported(int M, int K, int group);
-int gemv_cols_per_block(const GemvArgs &a);
+// key slots per row that an EPI_ARGMAX launch writes (keys_ld must cover it)
+int gemv_argmax_slots(const GemvArgs &a);
 hipError_t launch_gemv(const GemvArgs &a, hipStream_t s);
 
 // Head epilogues of the Q/K/V projections from f32 rows: per (row, head)

@@ -14,7 +14,9 @@
 // may start anywhere and span pages.  All work is enqueued on the model's
 // stream; the generated ids are written on the device (no host round trip
 // per token).
+#include <algorithm>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <vector>
@@ -32,6 +34,9 @@ struct q3_model {
   // argmax workspace: one key per lm_head column block (allocated at open)
   unsigned long long *keys_ws;
   int64_t keys_ld;
+  // decode: workgroups that prefetch the next kernels' weights during the
+  // attention kernel (Q3_DECODE_PREFETCH_WGS, default 64; 0 disables)
+  int pf_wgs;
 };
 
 namespace {
@@ -225,7 +230,7 @@ int lm_head(q3_model *m, uint32_t rows, int lm_out, int32_t *id_dst) {
     g.keys = m->keys_ws;
     g.keys_ld = m->keys_ld;
     Q3_HIP(q3::launch_gemv(g, s));
-    const int nslots = V / q3::gemv_cols_per_block(g);
+    const int nslots = q3::gemv_argmax_slots(g);
     Q3_HIP(q3::launch_argmax_finish(m->keys_ws, m->keys_ld, nslots, 1, at<float>(m, y.kARGF), 1,
                                     at<int32_t>(m, y.kARGI), 1, /*init=*/1, id_dst, nullptr, 0, s));
   }
@@ -340,6 +345,27 @@ int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int opti
       t.cos_row = cos_t + static_cast<int64_t>(pos) * HALF;
       t.sin_row = sin_t + static_cast<int64_t>(pos) * HALF;
       t.inv_hd = inv_hd;
+      // while the 16 attention workgroups run, idle CUs pull this layer's
+      // O / gate / up / down weights and the next layer's Q / K / V weights
+      // into the last-level cache
+      const int64_t HH = static_cast<int64_t>(H);
+      auto add_pf = [&t](const int8_t *p, int64_t bytes) {
+        t.pf[t.pf_n] = p;
+        t.pf_bytes[t.pf_n] = bytes;
+        ++t.pf_n;
+      };
+      add_pf(lp.wo, HH * QW);
+      add_pf(lp.wg, static_cast<int64_t>(I) * H);
+      add_pf(lp.wu, static_cast<int64_t>(I) * H);
+      add_pf(lp.wd, HH * I);
+      if (!is_last) {
+        const LayerPtrs nx = layer_ptrs(m, L + 1);
+        add_pf(nx.wq, static_cast<int64_t>(QW) * H);
+        add_pf(nx.wk, static_cast<int64_t>(KW) * H);
+        add_pf(nx.wv, static_cast<int64_t>(KW) * H);
+      }
+      t.pf_wgs = m->pf_wgs;
+      if (m->pf_wgs == 0) t.pf_n = 0;
     } else {
       // head epilogues: K (norm+RoPE+quant) and V (quant) of every row into
       // the page slots; Q (norm+RoPE+quant) of the tail rows
@@ -645,6 +671,8 @@ extern "C" int q3_model_open(void *blob, const q3_layout *lay, void *stream, q3_
   m->stream = static_cast<hipStream_t>(stream);
   m->n_pages = lay->max_seq / kPageTokens;
   m->keys_ld = lay->vocab / 16 + 64;  // one key per lm_head column block
+  m->pf_wgs = 64;
+  if (const char *e = std::getenv("Q3_DECODE_PREFETCH_WGS")) m->pf_wgs = std::max(0, std::atoi(e));
   if (hipMalloc(&m->ptab, sizeof(uint16_t) * m->n_pages) != hipSuccess ||
       hipMalloc(&m->keys, sizeof(unsigned long long) * 8) != hipSuccess ||
       hipMalloc(&m->keys_ws, sizeof(unsigned long long) * m->keys_ld) != hipSuccess) {

@@ -128,7 +128,7 @@ hipError_t launch_gemm_or_gemv(const q3::GemmArgs &g, hipStream_t s) {
 
 // Per-workgroup argmax slots needed by launch_gemm_or_gemv for g.
 int argmax_slots(const q3::GemmArgs &g) {
-  if (use_gemv(g)) return g.N / q3::gemv_cols_per_block(to_gemv(g));
+  if (use_gemv(g)) return q3::gemv_argmax_slots(to_gemv(g));
   return g.N / 128;
 }
 

@@ -307,6 +307,52 @@ def test_lm_argmax(cuda, N):
     assert int(host(bidx2)[0]) == -5 and host(best2)[0] == np.float32(1e30)
 
 
+@pytest.mark.parametrize("M", [2, 5, 16])
+def test_lm_argmax_wide_multirow(cuda, M):
+    """lm_head width with several rows: one running key per row and
+    workgroup across the column tiles each workgroup walks."""
+    note(f"lm argmax M={M} N=151936")
+    rng = np.random.default_rng(40 + M)
+    a, as_, b, bs = rand_gemm(rng, M, 1024, 151936, 256)
+    best = torch.full((M,), -3.0e38, dtype=torch.float32, device=cuda)
+    bidx = torch.zeros(M, dtype=torch.int32, device=cuda)
+    ops.gemm_nt_group_argmax(dev(a), dev(as_), dev(b), dev(bs), best, bidx, 256)
+    logits = oracle.gemm_nt_group(a, as_, b, bs, 256)
+    assert host(bidx).tolist() == [int(i) for i in np.argmax(logits, axis=1)]
+    assert bits_equal(host(best), logits.max(axis=1))
+
+
+def test_lm_argmax_wide_ties_across_tiles(cuda):
+    """Copies of the winning row in tiles owned by other workgroups (and in
+    the same tile): the earliest index wins."""
+    rng = np.random.default_rng(77)
+    a, as_, b, bs = rand_gemm(rng, 1, 1024, 151936, 256)
+    logits = oracle.gemm_nt_group(a, as_, b, bs, 256)[0]
+    w = int(np.argmax(logits))
+    copies = [151935, 70001, min(w + 1, 151935), 64 * 513 + 3]
+    for c in copies:
+        b[c] = b[w]
+        bs[c] = bs[w]
+    first = min([w] + copies)
+    best = torch.tensor([-3.0e38], dtype=torch.float32, device=cuda)
+    bidx = torch.zeros(1, dtype=torch.int32, device=cuda)
+    ops.gemm_nt_group_argmax(dev(a), dev(as_), dev(b), dev(bs), best, bidx, 256)
+    assert int(host(bidx)[0]) == first
+
+
+@pytest.mark.parametrize("M", [1, 3])
+def test_gemm_store_lm_width(cuda, M):
+    """Logits mode: the full 151936-wide f32 row(s)."""
+    note(f"gemm store M={M} N=151936")
+    rng = np.random.default_rng(90 + M)
+    a, as_, b, bs = rand_gemm(rng, M, 1024, 151936, 256)
+    out = torch.zeros((M, 151936), dtype=torch.float32, device=cuda)
+    ops.gemm_nt_group_store(dev(a), dev(as_), dev(b), dev(bs), out, 256)
+    ref = oracle.gemm_nt_group(a, as_, b, bs, 256)
+    got = host(out)
+    assert bits_equal(got, ref), describe_diff(got, ref)
+
+
 def test_lm_argmax_ties_first_index(cuda):
     """Duplicate the winning weight row at a later index and an earlier one:
     the earliest index of the maximum wins."""
