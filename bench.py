@@ -125,6 +125,54 @@ def kernel_rooflines(stream) -> dict:
     return res
 
 
+# Algorithmic HBM bytes of one launch of each decode kernel class (model
+# shape of the workload): every operand read once, every result written once.
+def decode_class_bytes(name: str, kv_len: int) -> int:
+    H, QW, KW, KVH, NH, I, V = 1024, 2048, 1024, 8, 16, 3072, 151936
+    if name == "attn_decode":
+        kv_rows = kv_len * (2 * KW + 2 * KVH * 4)       # K, V rows + per-head scales
+        ins = (QW + 2 * KW) * 4 + 2 * 128 * 4 + 2 * 64 * 4  # f32 q|k|v rows, q/k gains, cos/sin
+        outs = (QW + NH * 4) * 2 + 2 * (KW + KVH * 4)  # q8/qs + o8/os, new K/V rows + scales
+        return kv_rows + ins + outs
+    if name == "gemv_qkv":     # RMSNorm prologue (x, gain) + Q|K|V weights, f32 outputs
+        N = QW + 2 * KW
+        return N * H + 4 * N + 2 * 4 * H + 4 * N + (H + 4 * H + 16)
+    if name == "gemv_o":       # o8/os + Wo + residual read/write
+        return H * QW + 4 * H + QW + 4 * NH + 2 * 4 * H
+    if name == "gemv_gate_up":  # prologue (x, gain) + Wg, Wu + f32 SwiGLU row
+        return 2 * I * H + 8 * I + 2 * 4 * H + 4 * I + (H + 4 * H + 16)
+    if name == "gemv_down":    # f32 SwiGLU row + Wd + residual read/write (+ s8/ss stage)
+        return 4 * I + H * I + 4 * H + 2 * 4 * H + I + 4 * (I // 256)
+    if name == "lm_head":      # prologue + lm weights and scales (+ keys)
+        return V * H + 4 * V + 2 * 4 * H + 8 * 1024
+    raise KeyError(name)
+
+
+def attn_prefetch_bytes(kv_len: int, last_layer: bool) -> int:
+    """Bytes the attention kernel's prefetch workgroups read per launch
+    (q3_model.hip): this layer's O, gate, up, down weights, the next layer's
+    Q, K, V weights (not after the last layer), and the K/V pages and scales
+    of the next attention."""
+    H, QW, KW, KVH, I = 1024, 2048, 1024, 8, 3072
+    b = H * QW + 2 * I * H + H * I
+    if not last_layer:
+        b += (QW + 2 * KW) * H
+    pages = (kv_len + (1 if last_layer else 0) + 31) // 32
+    return b + pages * (2 * 32 * KW + 2 * 32 * KVH * 4)
+
+
+def load_pmc_traffic() -> dict:
+    """Per-kernel HBM bytes per dispatch from the committed rocprofv3 PMC
+    summary (profiles/pmc_traffic.json), if present."""
+    p = REPO / "profiles" / "pmc_traffic.json"
+    if not p.exists():
+        return {}
+    try:
+        return json.loads(p.read_text()).get("kernels", {})
+    except (OSError, ValueError):
+        return {}
+
+
 def cpu_baseline(threads: int) -> dict:
     import numpy as np
     import oracle
@@ -154,6 +202,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-roofline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
+                    help="finish with 3 device-to-device copies of MIB MiB (PMC calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (this build has no multi-GPU path); "
@@ -218,19 +268,55 @@ def main() -> int:
         "decode_tok_s": 1e3 / decode_ms,
         "generated_head": [int(v) for v in gen_ids[:8]],
     }
+    # in-situ kernel timing: one more (untimed) generation with every decode
+    # launch bracketed by HIP events on the model's stream
+    if not args.no_roofline:
+        log("decode kernel timing pass ...")
+        m.set_kernel_timing(True)
+        m.generate()
+        kt = m.kernel_times()
+        m.set_kernel_timing(False)
+        layers = shape.layers
+        # decode step i (0-based) attends over kv_len = N_PROMPT + 1 + i keys
+        n_steps = max(1, kt["attn_decode"][1] // layers)
+        kv_lens = [N_PROMPT + 1 + i for i in range(n_steps)]
+        classes = {}
+        for name, (tot_ms, n) in kt.items():
+            if n == 0:
+                continue
+            if name == "lm_head":
+                byts = decode_class_bytes(name, 0)
+            else:
+                byts = sum(decode_class_bytes(name, kv) for kv in kv_lens) / len(kv_lens)
+            avg = tot_ms / n
+            classes[name] = {"launches": n, "avg_us": avg * 1e3, "total_ms": tot_ms,
+                             "bytes_per_launch": int(byts), "GBs": byts / avg / 1e6}
+        dec_total = sum(c["total_ms"] for c in classes.values())
+        for c in classes.values():
+            c["share_of_timed"] = c["total_ms"] / dec_total if dec_total else 0.0
+        out["decode_kernels"] = classes
+        dom_name = max(classes, key=lambda k: classes[k]["total_ms"])
+        dom = classes[dom_name]
+        pmc = load_pmc_traffic().get(dom_name)
+        pf = None
+        if dom_name == "attn_decode":
+            pf = sum(attn_prefetch_bytes(kv, l == layers - 1)
+                     for kv in kv_lens for l in range(layers)) / (len(kv_lens) * layers)
+        out["roofline"] = {"kernel": dom_name, "bound": "hbm", "achieved": dom["GBs"],
+                           "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": dom["GBs"] / HBM_PEAK_GBS,
+                           "traffic": (pmc or {}).get("bytes_per_dispatch"),
+                           "avg_us": dom["avg_us"], "bytes_per_launch": dom["bytes_per_launch"],
+                           "launches": dom["launches"], "layers": layers}
+        if pf is not None:
+            # traffic counts the prefetch workgroups' reads too (next kernels' weights and KV)
+            out["roofline"]["traffic_prefetch"] = int(pf)
     m.close()
     del m
     torch.cuda.synchronize()
 
     if not args.no_roofline:
         log("kernel rooflines ...")
-        kr = kernel_rooflines(stream)
-        out["kernels"] = kr
-        dom = kr["lm_argmax_gemv"]
-        out["roofline"] = {"kernel": "lm_argmax_gemv (M=1, N=151936, K=1024)", "bound": "hbm",
-                           "achieved": dom["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                           "frac": dom["GBs"] / HBM_PEAK_GBS, "traffic": None,
-                           "avg_ms": dom["ms"], "bytes_per_launch": dom["bytes"]}
+        out["kernels"] = kernel_rooflines(stream)
     if not args.no_cpu:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
         log(f"cpu baseline ({threads} threads) ...")
@@ -238,6 +324,15 @@ def main() -> int:
         cb_ok = cb.pop("generated_head") == out["generated_head"]
         cb["matches_gpu_ids"] = bool(cb_ok)
         out["cpu_baseline"] = cb
+    if args.calib_copy > 0:
+        n = args.calib_copy << 20
+        src = torch.empty(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        with torch.cuda.stream(stream):
+            for _ in range(3):
+                dst.copy_(src)
+        torch.cuda.synchronize()
+        out["calib_copy_bytes"] = n
     print(json.dumps(out), flush=True)
     return 0
 

@@ -297,6 +297,28 @@ int q3_generate(q3_model *m);
  * (not the blob). */
 int q3_model_close(q3_model *m);
 
+/* ---- measurement (no counterpart in the reference) ------------------------
+ * Decode kernel classes whose launches the model can time with HIP events on
+ * its own stream (hipExtLaunchKernel start/stop events: the kernel's own
+ * dispatch timestamps). */
+enum {
+  Q3_KT_ATTN_DECODE = 0, /* decode attention (+ fused head epilogues)     */
+  Q3_KT_GEMV_QKV = 1,    /* Q|K|V projection, RMSNorm prologue            */
+  Q3_KT_GEMV_O = 2,      /* O projection + residual                       */
+  Q3_KT_GEMV_GATE_UP = 3,/* gate/up + SwiGLU, RMSNorm prologue            */
+  Q3_KT_GEMV_DOWN = 4,   /* down projection + residual, quant prologue    */
+  Q3_KT_LM_HEAD = 5,     /* lm_head GEMV (argmax mode)                    */
+  Q3_KT_COUNT = 6
+};
+
+/* Enables event timing for the classes whose bit (1 << class) is set in
+ * mask (0 disables).  Clears the accumulated times. */
+int q3_model_set_kernel_timing(q3_model *m, uint32_t mask);
+
+/* Synchronises the stream and returns the summed milliseconds and the
+ * number of timed launches of one class since timing was enabled. */
+int q3_model_kernel_time(q3_model *m, int kclass, double *total_ms, uint32_t *launches);
+
 #ifdef __cplusplus
 }
 #endif

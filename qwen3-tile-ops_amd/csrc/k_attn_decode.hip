@@ -434,7 +434,7 @@ hipError_t launch_decode(const AttnArgs &a, hipStream_t s) {
   constexpr int QPW = 1, NW = 8, BPW = 3;
   static_assert(QPW * HD <= NW * 64, "phase 4 needs a thread per (head, dim)");
   const int extra = a.pf_n > 0 ? a.pf_wgs : 0;
-  hipLaunchKernelGGL((attn_decode_kernel<QPW, NW, BPW>), dim3(a.heads / QPW + extra), dim3(NW * 64), 0, s, a);
+  Q3_LAUNCH((attn_decode_kernel<QPW, NW, BPW>), dim3(a.heads / QPW + extra), dim3(NW * 64), 0, s, a);
   return hipGetLastError();
 }
 
@@ -446,7 +446,7 @@ bool attn_decode_supported(const AttnArgs &a) {
   for (int r = 0; r < a.pf_n; ++r)
     if ((reinterpret_cast<uintptr_t>(a.pf[r]) & 15) != 0 || a.pf_bytes[r] < 0) return false;
   return a.rows == 1 && a.causal && (grp == 1 || grp == 2) && a.kv_heads * grp == a.heads &&
-         a.pf_n >= 0 && a.pf_n <= 8 && (a.pf_n == 0 || a.pf_wgs > 0) &&
+         a.pf_n >= 0 && a.pf_n <= 12 && (a.pf_n == 0 || a.pf_wgs > 0) &&
          (a.row_bytes % 16) == 0 && (a.page_tokens % 32) == 0 && al16(a.k) && al16(a.v) &&
          al16(a.q8) && (a.scale_row_bytes % 4) == 0 && a.kv_len >= 1 && !a.kv_len_dev;
 }

@@ -542,7 +542,7 @@ hipError_t launch_t(const GemvArgs &a, int ncols, hipStream_t s) {
   if (a.pro != PRO_NONE)
     lds += ((a.M * a.K + 15) & ~15) + sizeof(float) * (a.M * (a.K / 256) + a.K / 32);
   if (lds > 65536) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((gemv_kernel<GPW, KSTEPS, NT, NMAT>), dim3(ncols / NB), dim3(256), lds, s, a);
+  Q3_LAUNCH((gemv_kernel<GPW, KSTEPS, NT, NMAT>), dim3(ncols / NB), dim3(256), lds, s, a);
   return hipGetLastError();
 }
 
@@ -609,7 +609,7 @@ hipError_t launch_gemv(const GemvArgs &a, hipStream_t s) {
     const int ntiles = ncols / 64;
     const size_t lds = sizeof(float) * 4 * 16 * 65 +
                        (a.pro != PRO_NONE ? ((a.M * a.K + 15) & ~15) + sizeof(float) * (a.M * 4 + 32) : 0);
-    hipLaunchKernelGGL((gemv_stream_kernel<1, 4, 4>), dim3(stream_grid(ntiles)), dim3(256), lds, s, a, ntiles);
+    Q3_LAUNCH((gemv_stream_kernel<1, 4, 4>), dim3(stream_grid(ntiles)), dim3(256), lds, s, a, ntiles);
     return hipGetLastError();
   }
   const bool two = a.seg[0].epi == EPI_SWIGLU;

@@ -3,10 +3,29 @@
 // strides are in elements.  Launchers only enqueue work on `stream`.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 namespace q3 {
+
+// ---- measurement hook ------------------------------------------------------
+// When set (by the model's kernel timing), the decode launchers time their
+// kernel with hipExtLaunchKernel start/stop events: the dispatch packet's own
+// timestamps, no extra queue packets.
+struct LaunchEvents {
+  hipEvent_t start, stop;
+};
+extern thread_local const LaunchEvents *g_launch_events;
+
+#define Q3_LAUNCH(kern, grid, block, shmem, stream, ...)                                      \
+  do {                                                                                       \
+    if (::q3::g_launch_events)                                                               \
+      hipExtLaunchKernelGGL(kern, grid, block, shmem, stream, ::q3::g_launch_events->start,  \
+                            ::q3::g_launch_events->stop, 0, __VA_ARGS__);                    \
+    else                                                                                     \
+      hipLaunchKernelGGL(kern, grid, block, shmem, stream, __VA_ARGS__);                     \
+  } while (0)
 
 // ---- row kernels: embedding gather, RMSNorm, per-group quantisation ----
 struct RowArgs {
@@ -161,8 +180,8 @@ struct AttnArgs {
   // (values discarded) while the attention workgroups run, so that the
   // kernels after it find their weights in the last-level cache
   int pf_n, pf_wgs;
-  const int8_t *pf[8];
-  int64_t pf_bytes[8];
+  const int8_t *pf[12];
+  int64_t pf_bytes[12];
 };
 hipError_t launch_attention(const AttnArgs &a, hipStream_t s);
 

@@ -29,15 +29,26 @@ struct q3_model {
   q3_layout lay;
   hipStream_t stream;
   uint16_t *ptab;              // device, max_seq / 32 entries
+  std::vector<uint16_t> htab;  // host copy of the page table
   uint32_t n_pages;
   unsigned long long *keys;    // device argmax key (1 row)
   // argmax workspace: one key per lm_head column block (allocated at open)
   unsigned long long *keys_ws;
   int64_t keys_ld;
+  // event timing of decode kernel classes (q3_model_set_kernel_timing)
+  uint32_t kt_mask = 0;
+  std::vector<hipEvent_t> kt_ev[Q3_KT_COUNT];  // start, end pairs
+  uint32_t kt_used[Q3_KT_COUNT] = {};          // pairs recorded
+  double kt_ms[Q3_KT_COUNT] = {};              // folded totals
+  uint32_t kt_n[Q3_KT_COUNT] = {};
   // decode: workgroups that prefetch the next kernels' weights during the
   // attention kernel (Q3_DECODE_PREFETCH_WGS, default 64; 0 disables)
   int pf_wgs;
 };
+
+namespace q3 {
+thread_local const LaunchEvents *g_launch_events = nullptr;
+}  // namespace q3
 
 namespace {
 
@@ -95,6 +106,69 @@ LayerPtrs layer_ptrs(const q3_model *m, uint32_t L) {
   p.vc = at<int8_t>(m, kv + y.kKV_VOFF);
   p.vcs = at<float>(m, kv + y.kKV_VOFF + y.kKV_SOFF);
   return p;
+}
+
+// Sums the recorded event pairs of class c into kt_ms and recycles them
+// (synchronises the stream).
+int kt_fold(q3_model *m, int c) {
+  if (m->kt_used[c] == 0) return Q3_OK;
+  Q3_HIP(hipStreamSynchronize(m->stream));
+  for (uint32_t i = 0; i < m->kt_used[c]; ++i) {
+    float ms = 0.0f;
+    Q3_HIP(hipEventElapsedTime(&ms, m->kt_ev[c][2 * i], m->kt_ev[c][2 * i + 1]));
+    m->kt_ms[c] += ms;
+  }
+  m->kt_n[c] += m->kt_used[c];
+  m->kt_used[c] = 0;
+  return Q3_OK;
+}
+
+// Times the one launch issued during its lifetime, when class c is being
+// timed, through the launchers' hipExtLaunchKernel events.
+class KTimer {
+ public:
+  KTimer(q3_model *m, int c) : m_(m), c_(c) {
+    if (!(m->kt_mask & (1u << c))) return;
+    constexpr uint32_t kMaxPairs = 2048;
+    if (m->kt_used[c] == kMaxPairs && kt_fold(m, c) != Q3_OK) return;
+    std::vector<hipEvent_t> &ev = m->kt_ev[c];
+    while (ev.size() < 2 * (m->kt_used[c] + 1)) {
+      hipEvent_t e;
+      if (hipEventCreate(&e) != hipSuccess) return;
+      ev.push_back(e);
+    }
+    pair_.start = ev[2 * m->kt_used[c]];
+    pair_.stop = ev[2 * m->kt_used[c] + 1];
+    q3::g_launch_events = &pair_;
+    active_ = true;
+  }
+  ~KTimer() {
+    if (!active_) return;
+    q3::g_launch_events = nullptr;
+    ++m_->kt_used[c_];
+  }
+  KTimer(const KTimer &) = delete;
+  KTimer &operator=(const KTimer &) = delete;
+
+ private:
+  q3_model *m_;
+  int c_;
+  q3::LaunchEvents pair_{};
+  bool active_ = false;
+};
+
+// Physical page span [lo, hi] holding tokens [0, len) under the page table.
+bool kv_page_span(const q3_model *m, uint32_t len, uint32_t *lo, uint32_t *hi) {
+  const uint32_t used = (len + kPageTokens - 1) / kPageTokens;
+  if (used == 0 || used > m->htab.size()) return false;
+  uint32_t a = m->htab[0], b = m->htab[0];
+  for (uint32_t i = 1; i < used; ++i) {
+    a = std::min<uint32_t>(a, m->htab[i]);
+    b = std::max<uint32_t>(b, m->htab[i]);
+  }
+  *lo = a;
+  *hi = b;
+  return true;
 }
 
 void set_paged(q3::QDest &d, const q3_model *m, int8_t *pool, float *spool, uint32_t pos0) {
@@ -229,7 +303,10 @@ int lm_head(q3_model *m, uint32_t rows, int lm_out, int32_t *id_dst) {
     g.seg[0] = gemv_seg(0, V, q3::EPI_ARGMAX, lm, lm_s, nullptr, 0);
     g.keys = m->keys_ws;
     g.keys_ld = m->keys_ld;
-    Q3_HIP(q3::launch_gemv(g, s));
+    {
+      KTimer kt(m, Q3_KT_LM_HEAD);
+      Q3_HIP(q3::launch_gemv(g, s));
+    }
     const int nslots = q3::gemv_argmax_slots(g);
     Q3_HIP(q3::launch_argmax_finish(m->keys_ws, m->keys_ld, nslots, 1, at<float>(m, y.kARGF), 1,
                                     at<int32_t>(m, y.kARGI), 1, /*init=*/1, id_dst, nullptr, 0, s));
@@ -303,6 +380,7 @@ int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int opti
       g.seg[0] = gemv_seg(0, QW, q3::EPI_STORE, lp.wq, lp.wqs, q, QW);
       g.seg[1] = gemv_seg(QW, QW + KW, q3::EPI_STORE, lp.wk, lp.wks, k, KW);
       g.seg[2] = gemv_seg(QW + KW, QW + 2 * KW, q3::EPI_STORE, lp.wv, lp.wvs, v, KW);
+      KTimer kt(m, Q3_KT_GEMV_QKV);
       Q3_HIP(q3::launch_gemv(g, s));
     }
     // paged GQA attention over kv_len = pos + rows keys
@@ -364,6 +442,22 @@ int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int opti
         add_pf(nx.wk, static_cast<int64_t>(KW) * H);
         add_pf(nx.wv, static_cast<int64_t>(KW) * H);
       }
+      // the K/V pages (and scales) the next attention reads: the next
+      // layer's, or layer 0's for the next token after the last layer
+      {
+        const LayerPtrs nx = layer_ptrs(m, is_last ? 0 : L + 1);
+        const uint32_t span_len = std::min<uint32_t>(pos + rows + (is_last ? 1 : 0), y.max_seq);
+        uint32_t lo = 0, hi = 0;
+        if (kv_page_span(m, span_len, &lo, &hi)) {
+          const int64_t pgb = static_cast<int64_t>(kPageTokens) * KW;
+          const int64_t spb = static_cast<int64_t>(kPageTokens) * y.kv_heads * 4;
+          const int64_t np = hi - lo + 1;
+          add_pf(nx.kc + lo * pgb, np * pgb);
+          add_pf(nx.vc + lo * pgb, np * pgb);
+          add_pf(reinterpret_cast<const int8_t *>(nx.kcs) + lo * spb, np * spb);
+          add_pf(reinterpret_cast<const int8_t *>(nx.vcs) + lo * spb, np * spb);
+        }
+      }
       t.pf_wgs = m->pf_wgs;
       if (m->pf_wgs == 0) t.pf_n = 0;
     } else {
@@ -411,10 +505,12 @@ int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int opti
       }
     }
     if (!do_tail) continue;
-    if (q3::attn_decode_supported(t))
+    if (q3::attn_decode_supported(t)) {
+      KTimer kt(m, Q3_KT_ATTN_DECODE);
       Q3_HIP(q3::launch_attn_decode(t, s));
-    else
+    } else {
       Q3_HIP(q3::launch_attention(t, s));
+    }
     float *xt = x + static_cast<int64_t>(tr0) * H;
     // O projection (group = head_dim) + residual
     {
@@ -425,6 +521,7 @@ int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int opti
       g.ldas = y.heads;
       g.nseg = 1;
       g.seg[0] = gemv_seg(0, H, q3::EPI_ADD, lp.wo, lp.wos, xt, H);
+      KTimer kt(m, Q3_KT_GEMV_O);
       Q3_HIP(q3::launch_gemv(g, s));
     }
     // gate/up + SwiGLU; prologue = RMSNorm n2 + quant
@@ -442,6 +539,7 @@ int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int opti
       g.seg[0] = gemv_seg(0, I, q3::EPI_SWIGLU, lp.wg, lp.wgs, sw + static_cast<int64_t>(tr0) * I, I);
       g.seg[0].b2 = lp.wu;
       g.seg[0].bs2 = lp.wus;
+      KTimer kt(m, Q3_KT_GEMV_GATE_UP);
       Q3_HIP(q3::launch_gemv(g, s));
     }
     // down projection + residual; prologue = per-256 quant of SwiGLU
@@ -454,6 +552,7 @@ int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int opti
       g.hs_out = ss + static_cast<int64_t>(tr0) * (I / 256);
       g.nseg = 1;
       g.seg[0] = gemv_seg(0, H, q3::EPI_ADD, lp.wd, lp.wds, xt, H);
+      KTimer kt(m, Q3_KT_GEMV_DOWN);
       Q3_HIP(q3::launch_gemv(g, s));
     }
   }
@@ -679,7 +778,8 @@ extern "C" int q3_model_open(void *blob, const q3_layout *lay, void *stream, q3_
     q3_model_close(m);
     return Q3_ERR_HIP;
   }
-  std::vector<uint16_t> tab(m->n_pages);
+  std::vector<uint16_t> &tab = m->htab;
+  tab.resize(m->n_pages);
   for (uint32_t p = 0; p < m->n_pages; ++p) tab[p] = static_cast<uint16_t>(m->n_pages - 1 - p);
   if (hipMemcpy(m->ptab, tab.data(), sizeof(uint16_t) * m->n_pages, hipMemcpyHostToDevice) !=
           hipSuccess ||
@@ -691,12 +791,35 @@ extern "C" int q3_model_open(void *blob, const q3_layout *lay, void *stream, q3_
   return Q3_OK;
 }
 
+extern "C" int q3_model_set_kernel_timing(q3_model *m, uint32_t mask) {
+  if (!m) return Q3_ERR_ARG;
+  if (mask >> Q3_KT_COUNT) return Q3_ERR_ARG;
+  Q3_HIP(hipStreamSynchronize(m->stream));
+  m->kt_mask = mask;
+  for (int c = 0; c < Q3_KT_COUNT; ++c) {
+    m->kt_used[c] = 0;
+    m->kt_ms[c] = 0.0;
+    m->kt_n[c] = 0;
+  }
+  return Q3_OK;
+}
+
+extern "C" int q3_model_kernel_time(q3_model *m, int kclass, double *total_ms, uint32_t *launches) {
+  if (!m || kclass < 0 || kclass >= Q3_KT_COUNT || !total_ms || !launches) return Q3_ERR_ARG;
+  const int rc = kt_fold(m, kclass);
+  if (rc != Q3_OK) return rc;
+  *total_ms = m->kt_ms[kclass];
+  *launches = m->kt_n[kclass];
+  return Q3_OK;
+}
+
 extern "C" int q3_model_set_page_table(q3_model *m, const uint16_t *table, uint32_t n) {
   if (!m || !table || n != m->n_pages) return Q3_ERR_ARG;
   for (uint32_t i = 0; i < n; ++i)
     if (table[i] >= m->n_pages) return Q3_ERR_RANGE;
   Q3_HIP(hipMemcpyAsync(m->ptab, table, sizeof(uint16_t) * n, hipMemcpyHostToDevice, m->stream));
   Q3_HIP(hipStreamSynchronize(m->stream));
+  m->htab.assign(table, table + n);
   return Q3_OK;
 }
 
@@ -744,6 +867,8 @@ extern "C" int q3_model_close(q3_model *m) {
   if (m->ptab) (void)hipFree(m->ptab);
   if (m->keys) (void)hipFree(m->keys);
   if (m->keys_ws) (void)hipFree(m->keys_ws);
+  for (int c = 0; c < Q3_KT_COUNT; ++c)
+    for (hipEvent_t e : m->kt_ev[c]) (void)hipEventDestroy(e);
   delete m;
   return rc;
 }

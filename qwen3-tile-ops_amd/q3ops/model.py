@@ -55,6 +55,25 @@ class Model:
     def synchronize(self) -> None:
         self.stream.synchronize()
 
+    # decode kernel classes of q3_model_set_kernel_timing (include/q3ops.h)
+    KERNEL_CLASSES = ("attn_decode", "gemv_qkv", "gemv_o", "gemv_gate_up", "gemv_down", "lm_head")
+
+    def set_kernel_timing(self, enable: bool = True) -> None:
+        """Brackets every launch of each decode kernel class with HIP events
+        on the model's stream (a measurement aid; off by default)."""
+        mask = (1 << len(self.KERNEL_CLASSES)) - 1 if enable else 0
+        check(lib().q3_model_set_kernel_timing(self.handle, mask), "q3_model_set_kernel_timing")
+
+    def kernel_times(self) -> dict:
+        """{class: (total_ms, launches)} since set_kernel_timing(True)."""
+        out = {}
+        for i, name in enumerate(self.KERNEL_CLASSES):
+            ms, n = C.c_double(0.0), C.c_uint32(0)
+            check(lib().q3_model_kernel_time(self.handle, i, C.byref(ms), C.byref(n)),
+                  "q3_model_kernel_time")
+            out[name] = (ms.value, n.value)
+        return out
+
     def close(self) -> None:
         if self.handle:
             check(lib().q3_model_close(self.handle), "q3_model_close")

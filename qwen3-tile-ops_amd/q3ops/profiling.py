@@ -1,0 +1,133 @@
+"""Summaries of rocprofv3 CSV output for the measurement record.
+
+    python -m q3ops.profiling stats <kernel_stats.csv> --cmd "<command>" [--top N]
+        -> markdown table of the per-kernel statistics (stdout)
+
+    python -m q3ops.profiling pmc --fetch <counter_collection.csv>
+        --write <counter_collection.csv> --calib-bytes N --cmd "<command>"
+        -> JSON: per decode kernel class, FETCH_SIZE / WRITE_SIZE per dispatch
+           (KiB, as read) and HBM-side bytes per dispatch after calibration
+
+Calibration: the profiled command ends with device-to-device copies of
+N bytes (bench.py --calib-copy); each reads and writes exactly N bytes, so
+factor = N / (counter KiB * 1024) for the copy dispatches of that size, and
+every kernel's counter is scaled by it.  FETCH_SIZE and WRITE_SIZE count
+L2 <-> fabric traffic, i.e. bytes that left the L2 (last-level-cache hits
+included).
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import json
+import re
+import statistics
+import sys
+
+# decode kernel symbol -> kernel class of q3_model_set_kernel_timing
+CLASS_OF = [
+    (r"attn_decode_kernel<", "attn_decode"),
+    (r"gemv_kernel<1, 4, 1, 1>", "gemv_qkv"),
+    (r"gemv_kernel<4, 2, 1, 1>", "gemv_o"),
+    (r"gemv_kernel<1, 4, 1, 2>", "gemv_gate_up"),
+    (r"gemv_kernel<3, 4, 1, 1>", "gemv_down"),
+    (r"gemv_stream_kernel<", "lm_head"),
+]
+
+
+def short_name(name: str) -> str:
+    """Kernel symbol without return type, anonymous namespace and argument list."""
+    n = name.replace("(anonymous namespace)::", "").replace("void ", "")
+    depth = 0
+    for i, ch in enumerate(n):
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0:
+            return n[:i]
+    return n
+
+
+def class_of(name: str) -> str | None:
+    for pat, cls in CLASS_OF:
+        if re.search(re.escape(pat), name):
+            return cls
+    return None
+
+
+def stats_md(path: str, cmd: str, top: int) -> str:
+    rows = list(csv.DictReader(open(path)))
+    rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
+    out = [f"Command: `{cmd}`", "", f"Source: rocprofv3 `--kernel-trace --stats` ({path.split('/')[-1]})", "",
+           "| kernel | class | calls | avg us | min us | max us | % time |", "|---|---|---:|---:|---:|---:|---:|"]
+    for r in rows[:top]:
+        out.append(f"| `{short_name(r['Name'])}` | {class_of(r['Name']) or ''} | {r['Calls']} | "
+                   f"{float(r['AverageNs']) / 1e3:.2f} | {float(r['MinNs']) / 1e3:.2f} | "
+                   f"{float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.2f} |")
+    return "\n".join(out) + "\n"
+
+
+def _per_kernel(path: str, counter: str) -> dict[str, list[float]]:
+    agg: dict[str, list[float]] = {}
+    for r in csv.DictReader(open(path)):
+        if r["Counter_Name"] != counter:
+            continue
+        agg.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+    return agg
+
+
+def _calibration(agg: dict[str, list[float]], calib_bytes: int) -> float:
+    kib = calib_bytes / 1024.0
+    vals = [v for v in agg.get("__amd_rocclr_copyBuffer", []) if v > 0.25 * kib]
+    if not vals:
+        raise SystemExit("no calibration copy dispatches found")
+    return kib / statistics.median(vals)
+
+
+def pmc_json(fetch: str, write: str, calib_bytes: int, cmd: str) -> dict:
+    f = _per_kernel(fetch, "FETCH_SIZE")
+    w = _per_kernel(write, "WRITE_SIZE")
+    cf, cw = _calibration(f, calib_bytes), _calibration(w, calib_bytes)
+    kernels = {}
+    for name in sorted(set(f) | set(w)):
+        cls = class_of(name)
+        if cls is None:
+            continue
+        fk = statistics.mean(f.get(name, [0.0]))
+        wk = statistics.mean(w.get(name, [0.0]))
+        kernels[cls] = {
+            "kernel": short_name(name),
+            "dispatches": len(f.get(name, [])),
+            "fetch_kib_raw": fk, "write_kib_raw": wk,
+            "fetch_bytes": fk * 1024 * cf, "write_bytes": wk * 1024 * cw,
+            "bytes_per_dispatch": fk * 1024 * cf + wk * 1024 * cw,
+        }
+    return {"command": cmd, "calibration": {"copy_bytes": calib_bytes, "fetch_factor": cf,
+                                            "write_factor": cw},
+            "kernels": kernels}
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(prog="python -m q3ops.profiling")
+    sub = ap.add_subparsers(dest="cmd_name", required=True)
+    s = sub.add_parser("stats")
+    s.add_argument("csv")
+    s.add_argument("--cmd", required=True)
+    s.add_argument("--top", type=int, default=20)
+    p = sub.add_parser("pmc")
+    p.add_argument("--fetch", required=True)
+    p.add_argument("--write", required=True)
+    p.add_argument("--calib-bytes", type=int, required=True)
+    p.add_argument("--cmd", required=True)
+    a = ap.parse_args(argv)
+    if a.cmd_name == "stats":
+        sys.stdout.write(stats_md(a.csv, a.cmd, a.top))
+    else:
+        json.dump(pmc_json(a.fetch, a.write, a.calib_bytes, a.cmd), sys.stdout, indent=1)
+        sys.stdout.write("\n")
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())
