@@ -157,6 +157,29 @@ __global__ void __launch_bounds__(256) gate_up_kernel(GateUpArgs a) {
 
 hipError_t launch_gate_up(const GateUpArgs &a, hipStream_t s) {
   if (a.M <= 0) return hipSuccess;
+  if (a.M > 16) {  // prefill shapes: the LDS-staged tile kernel
+    TileArgs t{};
+    t.M = a.M;
+    t.N = a.N;
+    t.K = a.K;
+    t.group = a.group;
+    t.a = a.a;
+    t.lda = a.lda;
+    t.as = a.as;
+    t.ldas = a.ldas;
+    t.b0 = a.wg;
+    t.b1 = a.wu;
+    t.ldb = a.ldw;
+    t.bs0 = a.wgs;
+    t.bs1 = a.wus;
+    t.bs_stride = a.ws_stride;
+    t.s8 = a.s8;
+    t.lds8 = a.lds8;
+    t.ss = a.ss;
+    t.ldss = a.ldss;
+    t.ss_col = a.ss_col;
+    if (gemm_tile_supported(t, EPI_SWIGLUQ)) return launch_gemm_tile(t, EPI_SWIGLUQ, s);
+  }
   const int nblk = a.N / BN;
   if (a.M <= 16) {
     hipLaunchKernelGGL(gate_up_kernel<1>, dim3(nblk, 1), dim3(256), 0, s, a);

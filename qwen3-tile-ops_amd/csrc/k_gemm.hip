@@ -327,6 +327,32 @@ __global__ void __launch_bounds__(64) argmax_logits_kernel(const float *logits, 
 
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t s) {
   if (a.M <= 0) return hipSuccess;
+  if (a.M > 16 && a.epi != EPI_ARGMAX) {  // prefill shapes: the LDS-staged tile kernel
+    TileArgs t{};
+    t.M = a.M;
+    t.N = a.N;
+    t.K = a.K;
+    t.group = a.group;
+    t.a = a.a;
+    t.lda = a.lda;
+    t.as = a.as;
+    t.ldas = a.ldas;
+    t.b0 = a.b;
+    t.ldb = a.ldb;
+    t.bs0 = a.bs;
+    t.bs_stride = a.bs_stride;
+    t.out = a.out;
+    t.ldo = a.ldo;
+    t.qd = a.qd;
+    t.nw = a.nw;
+    t.nw_stride = a.nw_stride;
+    t.cos_t = a.cos_t;
+    t.sin_t = a.sin_t;
+    t.ld_cs = a.ld_cs;
+    t.cs_row_dev = a.cs_row_dev;
+    t.inv_hd = a.inv_hd;
+    if (gemm_tile_supported(t, a.epi)) return launch_gemm_tile(t, a.epi, s);
+  }
   switch (a.epi) {
     case EPI_STORE: return launch_epi<EPI_STORE>(a, s);
     case EPI_ADD: return launch_epi<EPI_ADD>(a, s);

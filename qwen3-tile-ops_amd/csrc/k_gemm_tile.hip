@@ -1,0 +1,375 @@
+// Prefill-shaped per-group int8 GEMM (M >= 64): LDS-staged MFMA tiles.
+//
+// Arithmetic of kernels/group_gemm.h:27-222 / ref_qwen3.py:145-158, with the
+// epilogues of group_gemm.h:173-214 (V quant, residual add),
+// norm_rope_quant.h:17-86 (Q/K) and swiglu_quant.h:164-255 (gate/up):
+//   D[m,n] = sum over K-groups g, in order from +0.0f, of
+//            RN(RN(f32(I_g[m,n]) * bs[n]) * as[m,g])
+// where I_g is the exact int32 dot product of group g
+// (v_mfma_i32_16x16x64_i8).
+//
+// Decomposition: a workgroup of NW waves (8: two per SIMD, so that one
+// wave's dequantisation and address work overlaps the other's MFMAs) owns a
+// BM x BN output tile (for the gate/up kernel: BN output columns of both
+// matrices).  Waves are arranged WGM (rows) x NW/WGM (columns).  Operand tiles of each KS-byte k-step are
+// copied global -> LDS with global_load_lds_dwordx4 (the copy needs no
+// registers), STAGES steps in flight, and each wave reads its MFMA fragments
+// (KS / 64 slices per step) from LDS with ds_read_b128.  The copy of one
+// k-step is (BM + NMAT*BN) * KS / 1024 instructions of 1 KiB; lane i of an
+// instruction writes LDS bytes [16 i, 16 i + 16), so the layout is chosen
+// through the global address each lane reads: LDS row r keeps its 16-byte
+// chunk c in slot c ^ ((r / RPC) % CH) (CH chunks per row, RPC rows per
+// 256-byte bank cycle), which spreads the 16 rows of a fragment read over
+// all banks.  Steps are coarse (KS = 256 B: one barrier pair per 4 MFMA
+// k-slices) because a k-step's fixed cost (barriers, LDS latency) is
+// comparable to a 64-byte step's MFMA work.  The per-group dequantisation
+// runs when a group's last slice is done, one thread per output element, in
+// group order.
+#include <algorithm>
+
+#include "q3_device.h"
+#include "q3_kernels.h"
+
+namespace q3 {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void *lds_void_ptr;
+
+__device__ __forceinline__ lds_void_ptr to_lds(const void *p) {
+  return reinterpret_cast<lds_void_ptr>(reinterpret_cast<uintptr_t>(p));
+}
+
+__device__ __forceinline__ v4i zero4() {
+  v4i z = {0, 0, 0, 0};
+  return z;
+}
+
+// s_waitcnt vmcnt(N), the other counters untouched (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Workgroup barrier for the k-loop: LDS operations of this wave complete
+// (lgkmcnt), then s_barrier.  __syncthreads() would also wait for every
+// outstanding vector load (vmcnt(0)), i.e. for the copies of the next
+// k-steps that are meant to stay in flight; each wave instead waits for its
+// own copies of the current step with wait_vmcnt before this barrier.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+
+// ref_qwen3.py:194-200: e = exp(-g); e = e + 1; e = 1/e; out = (g * e) * u.
+__device__ __forceinline__ float swiglu1(float g, float u, const uint64_t *tab) {
+  float e = __fmul_rn(g, -1.0f);
+  e = exp_f32_tab(e, tab);
+  e = __fadd_rn(e, 1.0f);
+  e = __fdiv_rn(1.0f, e);
+  return __fmul_rn(__fmul_rn(g, e), u);
+}
+
+// Row destination of the int8 head output (dense view or paged KV slot).
+__device__ __forceinline__ void qdest_row(const QDest &d, int m, int head, int8_t **row8, float **scale) {
+  if (d.table) {
+    uint32_t t = d.pos0 + static_cast<uint32_t>(m);
+    if (d.pos_dev) t += static_cast<uint32_t>(*d.pos_dev);
+    const uint32_t page = d.table[t / d.page_tokens];
+    const uint32_t slot = t % d.page_tokens;
+    *row8 = d.q8 + page * d.page_bytes + slot * d.row_bytes + head * 128;
+    *scale = reinterpret_cast<float *>(reinterpret_cast<int8_t *>(d.qs) + page * d.scale_page_bytes +
+                                       slot * d.scale_row_bytes) + head;
+  } else {
+    *row8 = d.q8 + static_cast<int64_t>(m) * d.ldq8 + head * 128;
+    *scale = d.qs + static_cast<int64_t>(m) * d.ldqs + head * d.qs_col;
+  }
+}
+
+template <int BM, int BN, int WGM, int NMAT, int STAGES, int KS>
+struct TileShape {
+  static constexpr int NW = 8;                         // waves per workgroup
+  static constexpr int NTHR = 64 * NW;
+  static constexpr int WGN = NW / WGM;
+  static constexpr int WM = BM / WGM, WN = BN / WGN;  // wave tile (output columns)
+  static constexpr int MT = WM / 16, NT = WN / 16;
+  static constexpr int BROWS = NMAT * BN;              // B rows per k-step
+  static constexpr int STAGE = (BM + BROWS) * KS;      // bytes per k-step
+  static constexpr int INSTR = STAGE / 1024;           // 1 KiB copies per k-step
+  static constexpr int IPW_HI = (INSTR + NW - 1) / NW; // copies per wave: waves below
+  static constexpr int IPW_LO = INSTR / NW;            //   INSTR % NW issue one more
+  static constexpr int CH = KS / 16;                   // 16-byte chunks per LDS row
+  static constexpr int RPI = 1024 / KS;                // rows per copy instruction
+  static constexpr int RPC = KS >= 256 ? 1 : 256 / KS; // rows per 256-byte bank cycle
+  static constexpr int SLICES = KS / 64;               // MFMA k-slices per step
+  static constexpr int LDT = BN + 4;                   // f32 epilogue tile pitch
+  static_assert(WGM * WGN == NW, "wave grid");
+  static_assert(WM % 16 == 0 && WN % 16 == 0, "16x16 MFMA tiles");
+  static_assert(KS == 64 || KS == 128 || KS == 256, "k-step bytes");
+  static_assert(BM % RPI == 0, "copies do not straddle A and B");
+  static_assert(IPW_HI * (STAGES - 1) < 64, "vmcnt range");
+  __device__ static int swz(int r, int c) { return c ^ ((r / RPC) & (CH - 1)); }
+};
+
+template <int BM, int BN, int WGM, int NMAT, int STAGES, int KS, int EPI>
+__global__ void __launch_bounds__(512) gemm_tile_kernel(TileArgs a) {
+  using S = TileShape<BM, BN, WGM, NMAT, STAGES, KS>;
+  constexpr int MT = S::MT, NT = S::NT;
+  extern __shared__ __align__(16) int8_t smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_id();
+  const int wm = wave % WGM;
+  const int wn = wave / WGM;
+  const int lr = lane & 15;
+  const int lg = lane >> 4;
+  const int m0 = blockIdx.y * BM;
+  const int n0 = blockIdx.x * BN;
+  const int M = a.M;
+  const int T = a.K / KS;            // k-steps
+  const int SPG = a.group / 64;      // k-slices per group
+  const int ngroups = a.K / a.group;
+  float *as_lds = reinterpret_cast<float *>(smem + STAGES * S::STAGE);  // [BM][ngroups]
+  uint64_t *tab = reinterpret_cast<uint64_t *>(as_lds + BM * ngroups);  // exp table (SwiGLU)
+
+  // k-step t -> stage s; instruction j copies LDS rows [RPI j, RPI (j + 1))
+  auto issue = [&](int t, int s) {
+    int8_t *st = smem + s * S::STAGE;
+#pragma unroll
+    for (int q = 0; q < S::IPW_HI; ++q) {
+      const int j = wave + S::NW * q;
+      if (j >= S::INSTR) break;  // wave-uniform
+      const int r = S::RPI * j + lane / S::CH;
+      const int c = S::swz(r, lane % S::CH);
+      const int8_t *src;
+      if (S::RPI * j < BM) {
+        const int row = min(m0 + r, M - 1);
+        src = a.a + static_cast<int64_t>(row) * a.lda + t * KS + 16 * c;
+      } else {
+        const int rb = r - BM;
+        const int8_t *bm = (NMAT == 2 && rb >= BN) ? a.b1 : a.b0;
+        src = bm + static_cast<int64_t>(n0 + rb % BN) * a.ldb + t * KS + 16 * c;
+      }
+      __builtin_amdgcn_global_load_lds(const_cast<int8_t *>(src), to_lds(st + 1024 * j), 16, 0, 0);
+    }
+  };
+
+  // A scales of the tile's rows (all groups) and the per-column B scales
+  for (int i = threadIdx.x; i < BM * ngroups; i += S::NTHR) {
+    const int r = i / ngroups, g = i % ngroups;
+    as_lds[i] = (m0 + r < M) ? a.as[static_cast<int64_t>(m0 + r) * a.ldas + g] : 0.0f;
+  }
+  if (EPI == EPI_SWIGLUQ && threadIdx.x < 32) tab[threadIdx.x] = kExp2Tab[threadIdx.x];
+  float bsv[NMAT][NT];
+#pragma unroll
+  for (int mi = 0; mi < NMAT; ++mi)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const float *bs = mi == 0 ? a.bs0 : a.bs1;
+      bsv[mi][nt] = bs[static_cast<int64_t>(n0 + wn * S::WN + nt * 16 + lr) * a.bs_stride];
+    }
+
+  // scales first, then the first STAGES-1 copies: vector loads complete in
+  // order, so waiting for the scales does not wait for the copies
+#pragma unroll
+  for (int p = 0; p < STAGES - 1; ++p)
+    if (p < T) issue(p, p);
+
+  float acc[NMAT][MT][NT][4];
+  v4i c[NMAT][MT][NT];
+#pragma unroll
+  for (int mi = 0; mi < NMAT; ++mi)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[mi][mt][nt][i] = 0.0f;
+        c[mi][mt][nt] = zero4();
+      }
+
+  for (int t = 0; t < T; ++t) {
+    const int tn = t + STAGES - 1;
+    if (tn < T) {
+      issue(tn, tn % STAGES);
+      // steps t+1 .. t+STAGES-1 of this wave may stay in flight
+      if (wave < S::INSTR % S::NW || S::INSTR % S::NW == 0)
+        wait_vmcnt<S::IPW_HI * (STAGES - 1)>();
+      else
+        wait_vmcnt<S::IPW_LO * (STAGES - 1)>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    lds_barrier();
+    const int8_t *st = smem + (t % STAGES) * S::STAGE;
+#pragma unroll
+    for (int kk = 0; kk < S::SLICES; ++kk) {
+    v4i af[MT], bf[NMAT][NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int r = wm * S::WM + mt * 16 + lr;
+      af[mt] = *reinterpret_cast<const v4i *>(st + r * KS + 16 * S::swz(r, 4 * kk + lg));
+    }
+#pragma unroll
+    for (int mi = 0; mi < NMAT; ++mi)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int r = BM + mi * BN + wn * S::WN + nt * 16 + lr;
+        bf[mi][nt] = *reinterpret_cast<const v4i *>(st + r * KS + 16 * S::swz(r, 4 * kk + lg));
+      }
+#pragma unroll
+    for (int mi = 0; mi < NMAT; ++mi)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          c[mi][mt][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[mt], bf[mi][nt], c[mi][mt][nt], 0, 0, 0);
+    const int slice = t * S::SLICES + kk;
+    if ((slice + 1) % SPG == 0) {  // group g done: dequant and accumulate in order
+      const int g = slice / SPG;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float asv = as_lds[(wm * S::WM + mt * 16 + lg * 4 + i) * ngroups + g];
+#pragma unroll
+          for (int mi = 0; mi < NMAT; ++mi)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+              const float p = __fmul_rn(__fmul_rn(static_cast<float>(c[mi][mt][nt][i]), bsv[mi][nt]), asv);
+              acc[mi][mt][nt][i] = __fadd_rn(acc[mi][mt][nt][i], p);
+            }
+        }
+#pragma unroll
+      for (int mi = 0; mi < NMAT; ++mi)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) c[mi][mt][nt] = zero4();
+    }
+    }  // k-slices
+    lds_barrier();  // stage t % STAGES is refilled by the next iteration
+  }
+  __syncthreads();
+
+  if constexpr (EPI == EPI_STORE || EPI == EPI_ADD) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = m0 + wm * S::WM + mt * 16 + lg * 4 + i;
+        if (m >= M) continue;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          float *dst = a.out + static_cast<int64_t>(m) * a.ldo + n0 + wn * S::WN + nt * 16 + lr;
+          if constexpr (EPI == EPI_ADD)
+            *dst = __fadd_rn(*dst, acc[0][mt][nt][i]);
+          else
+            *dst = acc[0][mt][nt][i];
+        }
+      }
+  } else {
+    // f32 tile through LDS (the stages are free now) so a wave can walk rows
+    float *tile = reinterpret_cast<float *>(smem);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          float v = acc[0][mt][nt][i];
+          if constexpr (EPI == EPI_SWIGLUQ) v = swiglu1(acc[0][mt][nt][i], acc[NMAT - 1][mt][nt][i], tab);
+          tile[(wm * S::WM + mt * 16 + lg * 4 + i) * S::LDT + wn * S::WN + nt * 16 + lr] = v;
+        }
+    __syncthreads();
+    for (int rr = wave; rr < BM; rr += S::NW) {
+      const int m = m0 + rr;
+      if (m >= M) break;
+      if constexpr (EPI == EPI_SWIGLUQ) {
+        // swiglu_quant.h:195-231: per 256-column group absmax * (1/127)
+        static_assert(EPI != EPI_SWIGLUQ || BN % 256 == 0, "whole quantisation groups");
+#pragma unroll
+        for (int q = 0; q < BN / 256; ++q) {
+          float v[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) v[j] = tile[rr * S::LDT + q * 256 + lane + 64 * j];
+          float mx = 0.0f;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) mx = fmaxf(mx, fabsf(v[j]));
+          mx = max64(mx);
+          const float scale = __fmul_rn(mx, inv127());
+          int8_t *dst = a.s8 + static_cast<int64_t>(m) * a.lds8 + n0 + q * 256;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) dst[lane + 64 * j] = static_cast<int8_t>(quant1(v[j], scale));
+          if (lane == 0) a.ss[static_cast<int64_t>(m) * a.ldss + ((n0 + q * 256) / 256) * a.ss_col] = scale;
+        }
+      } else {
+        static_assert(EPI == EPI_SWIGLUQ || BN == 128, "one head (128 columns) per tile");
+        float t0 = tile[rr * S::LDT + lane];
+        float t1 = tile[rr * S::LDT + lane + 64];
+        if constexpr (EPI == EPI_NRQ) {
+          int64_t crow = m;
+          if (a.cs_row_dev) crow += *a.cs_row_dev;
+          head_norm_rope(t0, t1, lane, a.nw, a.nw_stride, a.cos_t + crow * a.ld_cs, a.sin_t + crow * a.ld_cs,
+                         a.inv_hd, true);
+        }
+        const float mx = max64(fmaxf(fabsf(t0), fabsf(t1)));
+        const float scale = __fmul_rn(mx, inv127());
+        int8_t *row8;
+        float *sp;
+        qdest_row(a.qd, m, n0 / 128, &row8, &sp);
+        row8[lane] = static_cast<int8_t>(quant1(t0, scale));
+        row8[lane + 64] = static_cast<int8_t>(quant1(t1, scale));
+        if (lane == 0) *sp = scale;
+      }
+    }
+  }
+}
+
+template <int BM, int BN, int WGM, int NMAT, int STAGES, int KS, int EPI>
+hipError_t launch_shape(const TileArgs &a, hipStream_t s) {
+  using S = TileShape<BM, BN, WGM, NMAT, STAGES, KS>;
+  if (a.K % KS) return hipErrorInvalidValue;
+  const int ngroups = a.K / a.group;
+  size_t lds = static_cast<size_t>(STAGES) * S::STAGE + sizeof(float) * BM * ngroups + 32 * sizeof(uint64_t);
+  if (EPI != EPI_STORE && EPI != EPI_ADD)
+    lds = std::max(lds, sizeof(float) * BM * S::LDT);
+  if (lds > 160 * 1024) return hipErrorInvalidValue;
+  static bool attr_set = false;  // more than 64 KiB of dynamic LDS must be allowed once
+  if (!attr_set) {
+    const hipError_t e =
+        hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_tile_kernel<BM, BN, WGM, NMAT, STAGES, KS, EPI>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  const dim3 grid(a.N / BN, (a.M + BM - 1) / BM);
+  Q3_LAUNCH((gemm_tile_kernel<BM, BN, WGM, NMAT, STAGES, KS, EPI>), grid, dim3(S::NTHR), lds, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool gemm_tile_supported(const TileArgs &a, int epi) {
+  if (a.M < 1 || a.K % 256 || a.group % 64 || a.K % a.group || a.N <= 0) return false;
+  if (a.K / a.group > 64) return false;
+  auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (!al16(a.a) || !al16(a.b0) || (a.lda % 16) || (a.ldb % 16)) return false;
+  if (epi == EPI_SWIGLUQ) return a.N % 256 == 0 && a.b1 && al16(a.b1);
+  return a.N % 128 == 0;
+}
+
+hipError_t launch_gemm_tile(const TileArgs &a, int epi, hipStream_t s) {
+  if (a.M <= 0) return hipSuccess;
+  if (!gemm_tile_supported(a, epi)) return hipErrorInvalidValue;
+  switch (epi) {
+    case EPI_STORE: return launch_shape<64, 128, 2, 1, 3, 256, EPI_STORE>(a, s);
+    case EPI_ADD: return launch_shape<32, 128, 2, 1, 3, 256, EPI_ADD>(a, s);
+    case EPI_HEADQ: return launch_shape<64, 128, 2, 1, 3, 256, EPI_HEADQ>(a, s);
+    case EPI_NRQ: return launch_shape<64, 128, 2, 1, 3, 256, EPI_NRQ>(a, s);
+    case EPI_SWIGLUQ: return launch_shape<32, 256, 2, 2, 2, 128, EPI_SWIGLUQ>(a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace q3

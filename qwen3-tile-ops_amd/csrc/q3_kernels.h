@@ -67,6 +67,7 @@ enum Epi : int {
   EPI_NRQ = 3,     // per-head RMSNorm + RoPE + int8 quant (Q, K)
   EPI_ARGMAX = 4,  // fold D into per-row (max, first index) keys
   EPI_SWIGLU = 5,  // gate/up pair -> f32 SwiGLU (decode GEMV only)
+  EPI_SWIGLUQ = 6, // gate/up pair -> SwiGLU -> per-256-column int8 quant (tiled)
 };
 
 // Destination of the HEADQ/NRQ int8 rows: either a dense [M][N] i8 view
@@ -123,6 +124,36 @@ hipError_t launch_argmax_finish(const unsigned long long *keys, int64_t keys_ld,
                                 int64_t bidx_stride, int init, int32_t *ids_out,
                                 const int32_t *pos_dev, int pos_add,
                                 hipStream_t s);
+
+// ---- LDS-staged tiled group GEMM (prefill, M >= 64) ----------------------
+// b1/bs1: the up matrix of EPI_SWIGLUQ (b0/bs0 gate).  Epilogues: STORE, ADD
+// (out), HEADQ / NRQ (qd and the NRQ fields), SWIGLUQ (s8 / ss).
+struct TileArgs {
+  int M, N, K, group;
+  const int8_t *a;
+  int64_t lda;
+  const float *as;
+  int64_t ldas;
+  const int8_t *b0, *b1;
+  int64_t ldb;
+  const float *bs0, *bs1;
+  int64_t bs_stride;
+  float *out;
+  int64_t ldo;
+  QDest qd;
+  const float *nw;
+  int64_t nw_stride;
+  const float *cos_t, *sin_t;
+  int64_t ld_cs;
+  const int32_t *cs_row_dev;
+  float inv_hd;
+  int8_t *s8;
+  int64_t lds8;
+  float *ss;
+  int64_t ldss, ss_col;
+};
+bool gemm_tile_supported(const TileArgs &a, int epi);
+hipError_t launch_gemm_tile(const TileArgs &a, int epi, hipStream_t s);
 
 // ---- fused gate/up GEMM + SwiGLU + per-256-column quant -----------------
 struct GateUpArgs {

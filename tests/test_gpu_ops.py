@@ -80,7 +80,7 @@ def test_gemm_golden_guest_fixture(cuda):
         assert bits_equal(got, g[key]), describe_diff(got, g[key])
 
 
-@pytest.mark.parametrize("M", [1, 7, 64])
+@pytest.mark.parametrize("M", [1, 7, 64, 300])
 def test_gemm_residual_add(cuda, M):
     rng = np.random.default_rng(M)
     a, as_, b, bs = rand_gemm(rng, M, 2048, 1024, 128)
@@ -92,7 +92,7 @@ def test_gemm_residual_add(cuda, M):
     assert bits_equal(got, ref), describe_diff(got, ref)
 
 
-@pytest.mark.parametrize("M", [1, 9, 40])
+@pytest.mark.parametrize("M", [1, 9, 40, 130])
 def test_gemm_head_quant(cuda, M):
     """V epilogue: per-head int8 quant (group_gemm.h:173-193)."""
     rng = np.random.default_rng(10 + M)
@@ -113,7 +113,7 @@ def nrq_ref(x, nw, cos, sin, heads):
     return oracle.quant_rows_heads(out, 128)
 
 
-@pytest.mark.parametrize("M", [1, 13, 32])
+@pytest.mark.parametrize("M", [1, 13, 32, 77, 512])
 def test_gemm_norm_rope_quant(cuda, M):
     """Q/K epilogue: head RMSNorm + RoPE + quant (norm_rope_quant.h:17-86)."""
     rng = np.random.default_rng(20 + M)
@@ -265,7 +265,7 @@ def test_kv_paged_epilogues(cuda):
     assert not host(kp)[mask].any() and not host(vsp)[mask].any()
 
 
-@pytest.mark.parametrize("M", [1, 11, 64])
+@pytest.mark.parametrize("M", [1, 11, 64, 100, 512])
 def test_gate_up_swiglu_quant(cuda, M):
     rng = np.random.default_rng(50 + M)
     a, as_, wg, wgs = rand_gemm(rng, M, 1024, 3072, 256)
