@@ -161,6 +161,186 @@ def attn_prefetch_bytes(kv_len: int, last_layer: bool) -> int:
     return b + pages * (2 * 32 * KW + 2 * 32 * KVH * 4)
 
 
+CFG4_SEQS, CFG4_CTX, CFG4_STEPS = 64, 2048, 32
+CFG4_PAGES_PER_SEQ = (CFG4_CTX + CFG4_STEPS + 31) // 32   # 65: contexts + the 32 new rows
+KV_BYTES_PER_TOKEN = 2 * 1024 + 2 * 8 * 4               # K and V rows + per-head scales
+
+
+def cfg4_attn_bytes(kv_lens) -> int:
+    """Batched attention launch: every row's K/V pages and scales, its q8/qs
+    row in and o8/os row out."""
+    QW, NH = 2048, 16
+    return sum(int(k) * KV_BYTES_PER_TOKEN for k in kv_lens) + len(kv_lens) * 2 * (QW + 4 * NH)
+
+
+def cfg4_fill_kv(m, lay, seed: int) -> None:
+    """Every K/V row of the pool: N(0,1) values quantised per 128-wide head
+    (scale = max|x| * (1/127), round half to even), written straight into the
+    device blob (torch is only the generator here)."""
+    import torch
+    o = lay.offsets
+    MS, KW, NKV, HD = lay.max_seq, lay.kv_width, lay.kv_heads, lay.head_dim
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    inv127 = torch.tensor(1.0 / 127.0, dtype=torch.float32, device="cuda")
+    chunk = 8192
+    for li in range(lay.layers):
+        base = o["kKV_BASE"] + li * o["kKV_STRIDE"]
+        for off in (0, o["kKV_VOFF"]):
+            q_dst = m.blob[base + off:base + off + MS * KW].view(torch.int8).view(MS, KW)
+            so = base + off + o["kKV_SOFF"]
+            s_dst = m.blob[so:so + 4 * MS * NKV].view(torch.float32).view(MS, NKV)
+            for t0 in range(0, MS, chunk):
+                t1 = min(MS, t0 + chunk)
+                x = torch.randn(t1 - t0, NKV, HD, device="cuda", generator=gen)
+                sc = x.abs().amax(-1) * inv127
+                q = torch.round(x / sc[..., None]).clamp_(-127, 127).to(torch.int8)
+                q_dst[t0:t1] = q.view(t1 - t0, KW)
+                s_dst[t0:t1] = sc
+    torch.cuda.synchronize()
+
+
+def cfg4_cpu_check(blob, lay, m, tables, ids0, gpu_ids, sample: int, steps: int,
+                   threads: int) -> dict:
+    """Oracle on a bounded sample of the batch: `sample` sequences, `steps`
+    greedy steps each from their 2048-token contexts (read back from the
+    device pool through their tables).  Timed (the forwards only) as the CPU
+    baseline and compared with the GPU's ids for the same rows and steps."""
+    import numpy as np
+    import oracle
+    o = lay.offsets
+    MS, KW, NKV = lay.max_seq, lay.kv_width, lay.kv_heads
+    dims = dict(lay.shape.__dict__)
+    dims["max_seq"] = (CFG4_CTX + steps + 31) // 32 * 32
+    oracle.set_threads(threads)
+    om = oracle.OracleModel(blob, o, dims)
+    import torch
+    got, dt = [], 0.0
+    for r in range(sample):
+        om.reset_cache()
+        pages = torch.from_numpy(tables[r, :CFG4_CTX // 32].astype(np.int64)).cuda()
+        for li in range(lay.layers):
+            base = o["kKV_BASE"] + li * o["kKV_STRIDE"]
+            for dst_q, dst_s, off in ((om.k8, om.k_s, 0), (om.v8, om.v_s, o["kKV_VOFF"])):
+                pool_q = m.blob[base + off:base + off + MS * KW].view(torch.int8).view(MS // 32, 32, KW)
+                so = base + off + o["kKV_SOFF"]
+                pool_s = m.blob[so:so + 4 * MS * NKV].view(torch.float32).view(MS // 32, 32, NKV)
+                dst_q[li, :CFG4_CTX] = pool_q[pages].reshape(CFG4_CTX, KW).cpu().numpy()
+                dst_s[li, :CFG4_CTX] = pool_s[pages].reshape(CFG4_CTX, NKV).cpu().numpy()
+        tok = int(ids0[r])
+        seq = []
+        for st in range(steps):
+            t0 = time.perf_counter()
+            logits, _ = om.forward_chunk(np.array([tok], np.int32), CFG4_CTX + st, 1, True)
+            dt += time.perf_counter() - t0
+            tok = oracle.argmax_logits(logits)
+            seq.append(tok)
+        got.append(seq)
+    exp = [[int(gpu_ids[st][r]) for st in range(steps)] for r in range(sample)]
+    mism = [r for r in range(sample) if got[r] != exp[r]]
+    return {"value": steps * sample / dt, "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": (f"{sample} of the {CFG4_SEQS} sequences x {steps} greedy steps from their "
+                       f"{CFG4_CTX}-token contexts, one row at a time: oracle/ C port of "
+                       f"tools/ref_qwen3.py, {dt:.1f} s, {threads} OpenMP threads"),
+            "matches_gpu_ids": not mism, "mismatched_rows": mism}
+
+
+def run_cfg4(args) -> dict:
+    """Batched paged decode: 64 independent sequences, each with a random
+    2048-token context in its own 64 pages (plus one page for the new rows),
+    32 greedy steps of all 64 rows through q3_decode_batch.  One bench step =
+    those 32 decode steps from the same contexts and first ids (each step
+    rewrites the rows at positions 2048..2079)."""
+    import numpy as np
+    import torch
+    from q3ops.layout import InitConfig, Layout, ModelShape, init_random_blob
+    from q3ops.model import Model
+
+    n_pages = CFG4_SEQS * CFG4_PAGES_PER_SEQ
+    shape = ModelShape(seq=CFG4_SEQS, max_seq=n_pages * 32)
+    lay = Layout(shape)
+    log(f"cfg4: writing random-init blob ({lay.size / 1e9:.2f} GB) ...")
+    blob = init_random_blob(lay, InitConfig(n_prompt=1, n_gen=0, mode=0))
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        m = Model(lay, blob, stream=stream)
+    log("cfg4: filling the K/V pools ...")
+    cfg4_fill_kv(m, lay, seed=0x5EED0004)
+    rng = np.random.default_rng(0x5EED0004)
+    tables = rng.permutation(n_pages).astype(np.uint16).reshape(CFG4_SEQS, CFG4_PAGES_PER_SEQ)
+    ids0 = rng.integers(0, lay.vocab, size=CFG4_SEQS).astype(np.int32)
+    ids_a = torch.empty(CFG4_SEQS, dtype=torch.int32, device="cuda")
+    ids_b = torch.empty_like(ids_a)
+    ids_init = torch.from_numpy(ids0).cuda()
+    hist = [torch.empty_like(ids_a) for _ in range(CFG4_STEPS)]
+    pos = [np.full(CFG4_SEQS, CFG4_CTX + s, np.int32) for s in range(CFG4_STEPS)]
+
+    def one_step():
+        with torch.cuda.stream(stream):
+            ids_a.copy_(ids_init)
+        cur, nxt = ids_a, ids_b
+        for s in range(CFG4_STEPS):
+            m.decode_batch(cur, pos[s], tables, nxt)
+            with torch.cuda.stream(stream):
+                hist[s].copy_(nxt)
+            cur, nxt = nxt, cur
+
+    torch.cuda.synchronize()
+    log("cfg4: warmup ...")
+    for _ in range(args.warmup):
+        one_step()
+    torch.cuda.synchronize()
+    log(f"cfg4: timing {args.steps} steps ...")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        one_step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    gpu_ids = [h.cpu().numpy() for h in hist[:4]]
+    tokens = CFG4_SEQS * CFG4_STEPS
+    weight_bytes = 441_778_176 + 156_190_208
+    kv_step = sum(CFG4_CTX + 1 + s for s in range(CFG4_STEPS)) / CFG4_STEPS
+    step_bytes = weight_bytes + shape.layers * CFG4_SEQS * kv_step * KV_BYTES_PER_TOKEN
+    out = {
+        "metric": "tok/s batched paged decode (64 seq x 2048 ctx, 32 steps), Qwen3-0.6B W8A8, 1 MI355X",
+        "value": tokens / dt, "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": dt * 1e3, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": ("synthetic (random-init weights N(0,0.02) int8 per-row; K/V N(0,1) int8 per head; "
+                 "random page tables; uniform first ids)"),
+        "config": {"workload": "cfg4: 28-layer Qwen3-0.6B shape, 64 independent sequences x "
+                               "2048-token contexts, 32 batched greedy decode steps (M=64)",
+                   "sequences": CFG4_SEQS, "context": CFG4_CTX, "decode_steps": CFG4_STEPS,
+                   "pages": n_pages, "max_seq": shape.max_seq},
+        "ms_per_decode_step": dt * 1e3 / CFG4_STEPS,
+        "hbm_bound_ms_per_decode_step": step_bytes / (HBM_PEAK_GBS * 1e6),
+        "step_frac_of_hbm_bound": (step_bytes / (HBM_PEAK_GBS * 1e6)) / (dt * 1e3 / CFG4_STEPS),
+        "first_ids": [int(v) for v in gpu_ids[0][:8]],
+    }
+    if not args.no_roofline:
+        log("cfg4: attention timing pass ...")
+        m.set_kernel_timing(True)
+        one_step()
+        kt = m.kernel_times()
+        m.set_kernel_timing(False)
+        tot_ms, n = kt["attn_decode"]
+        byts = sum(cfg4_attn_bytes([CFG4_CTX + 1 + s] * CFG4_SEQS)
+                   for s in range(CFG4_STEPS)) / CFG4_STEPS
+        avg = tot_ms / max(n, 1)
+        gbs = byts / avg / 1e6
+        out["roofline"] = {"kernel": "attn_decode (batched)", "bound": "hbm", "achieved": gbs,
+                           "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
+                           "traffic": None, "avg_us": avg * 1e3, "bytes_per_launch": int(byts),
+                           "launches": n, "share_of_step": tot_ms / (dt * 1e3)}
+    if not args.no_cpu:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        log(f"cfg4: cpu baseline ({threads} threads) ...")
+        out["cpu_baseline"] = cfg4_cpu_check(blob, lay, m, tables, ids0, gpu_ids, CFG4_SEQS, 4,
+                                             threads)
+    m.close()
+    return out
+
+
 def load_pmc_traffic() -> dict:
     """Per-kernel HBM bytes per dispatch from the committed rocprofv3 PMC
     summary (profiles/pmc_traffic.json), if present."""
@@ -204,11 +384,20 @@ def main() -> int:
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="finish with 3 device-to-device copies of MIB MiB (PMC calibration)")
+    ap.add_argument("--workload", choices=("cfg3", "cfg4"), default="cfg3",
+                    help="cfg3: 512-token prefill + 64 b=1 decode steps (the headline line); "
+                         "cfg4: 64-sequence batched paged decode")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (this build has no multi-GPU path); "
               f"got --gpus {args.gpus}", file=sys.stderr)
         return 2
+    if args.workload == "cfg4":
+        import torch
+        assert torch.cuda.is_available(), "bench.py needs a ROCm device"
+        torch.cuda.set_device(0)
+        print(json.dumps(run_cfg4(args)), flush=True)
+        return 0
 
     import numpy as np
     import torch

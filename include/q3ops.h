@@ -293,6 +293,19 @@ int q3_forward_chunk(q3_model *m, uint32_t pos, uint32_t rows, int lm_out,
  * for mode > 1 (the reference returns 2). */
 int q3_generate(q3_model *m);
 
+/* Batched decode of n <= seq independent sequences: one
+ * token each.  Replaces the reference's op-level batch path, per request:
+ * paged_kv_scatter_batch (kernels/kv_pages.h) writes row r's K/V through its
+ * own page table, paged attention (attention_gqa.h:549-572) runs per request
+ * (tests/guest/paged_attn_multi.cpp), and every GEMM is row-independent.
+ * Row r: token ids[r] (device) at position pos[r] (host), page table
+ * tables + r * ld_table (host, logical -> physical page of the model's
+ * pool); it attends over pos[r] + 1 keys, its K/V are written at pos[r],
+ * and out_ids[r] (device) receives its greedy id.  Q3_ERR_RANGE if a
+ * position or a page entry is out of range. */
+int q3_decode_batch(q3_model *m, uint32_t n, const int32_t *ids, const int32_t *pos,
+                    const uint16_t *tables, uint32_t ld_table, int32_t *out_ids);
+
 /* Synchronises the model's stream and frees the handle's own allocations
  * (not the blob). */
 int q3_model_close(q3_model *m);

@@ -193,6 +193,14 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
     prefetch_ranges(a, static_cast<int>(blockIdx.x) - a.heads / QPW);
     return;
   }
+  // a batch of independent sequences: sequence blockIdx.y's length, pages
+  // and rows of q8/qs/o8/os
+  const int brow = a.row_pos ? static_cast<int>(blockIdx.y) : 0;
+  const uint16_t *table = a.row_pos ? a.row_tables + brow * a.ld_table : a.table;
+  const int8_t *q8_row = a.q8 + brow * a.ldq;
+  const float *qs_row = a.qs + brow * a.ldqs;
+  int8_t *o8_row = a.o8 + brow * a.ldo;
+  float *os_row = a.os + brow * a.ldos;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = wave_id();
@@ -200,7 +208,7 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
   const int qh0 = blockIdx.x * QPW;
   const int kvh = qh0 / grp;
   const bool kv_writer = (qh0 % grp) == 0;
-  const uint32_t kv_len = a.kv_len;
+  const uint32_t kv_len = a.row_pos ? static_cast<uint32_t>(a.row_pos[brow]) + 1 : a.kv_len;
   // one query row: pos0 = kv_len - 1, so kv_end = kv_len and the causal mask
   // only removes keys >= kv_len (attention_gqa.h:454-458)
   const int pos0 = static_cast<int>(kv_len) - 1;
@@ -225,9 +233,9 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
     fused_load<QPW>(a, kvh, qh0, wave, lane, fr);
   } else if (wave < QPW) {
     const int qh = qh0 + wave;
-    q8a = a.q8[qh * HD + lane];
-    q8b = a.q8[qh * HD + lane + 64];
-    qsa = a.qs[qh * a.qs_col];
+    q8a = q8_row[qh * HD + lane];
+    q8b = q8_row[qh * HD + lane + 64];
+    qsa = qs_row[qh * a.qs_col];
   }
 
   for (int b0 = 0; b0 < nblocks; b0 += CB) {
@@ -244,7 +252,7 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
       for (int e = 0; e < 16; ++e) kw[i][e] = vw[i][e] = 0;
       if (jb >= nb) continue;
       const int j = (b0 + jb) * 32;
-      const uint32_t page = a.table[static_cast<uint32_t>(j) / a.page_tokens];
+      const uint32_t page = table[static_cast<uint32_t>(j) / a.page_tokens];
       const uint32_t slot0 = static_cast<uint32_t>(j) % a.page_tokens;
       const int8_t *kb = a.k + page * a.page_bytes + slot0 * a.row_bytes + kvh * HD;
       const int8_t *vb = a.v + page * a.page_bytes + slot0 * a.row_bytes + kvh * HD;
@@ -420,9 +428,9 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
   if (tid < QPW * HD) {
     const int qh = qh0 + ph;
     const float scale = __fmul_rn(fmaxf(sm.absmax[ph][0], sm.absmax[ph][1]), inv127());
-    if (a.attn) a.attn[qh * HD + pd] = out;
-    a.o8[qh * HD + pd] = static_cast<int8_t>(quant1(out, scale));
-    if (pd == 0) a.os[qh * a.os_col] = scale;
+    if (a.attn) a.attn[brow * a.ld_attn + qh * HD + pd] = out;
+    o8_row[qh * HD + pd] = static_cast<int8_t>(quant1(out, scale));
+    if (pd == 0) os_row[qh * a.os_col] = scale;
   }
 }
 
@@ -434,7 +442,8 @@ hipError_t launch_decode(const AttnArgs &a, hipStream_t s) {
   constexpr int QPW = 1, NW = 8, BPW = 3;
   static_assert(QPW * HD <= NW * 64, "phase 4 needs a thread per (head, dim)");
   const int extra = a.pf_n > 0 ? a.pf_wgs : 0;
-  Q3_LAUNCH((attn_decode_kernel<QPW, NW, BPW>), dim3(a.heads / QPW + extra), dim3(NW * 64), 0, s, a);
+  const int seqs = a.row_pos ? a.rows : 1;
+  Q3_LAUNCH((attn_decode_kernel<QPW, NW, BPW>), dim3(a.heads / QPW + extra, seqs), dim3(NW * 64), 0, s, a);
   return hipGetLastError();
 }
 
@@ -445,10 +454,12 @@ bool attn_decode_supported(const AttnArgs &a) {
   auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
   for (int r = 0; r < a.pf_n; ++r)
     if ((reinterpret_cast<uintptr_t>(a.pf[r]) & 15) != 0 || a.pf_bytes[r] < 0) return false;
-  return a.rows == 1 && a.causal && (grp == 1 || grp == 2) && a.kv_heads * grp == a.heads &&
+  if (a.row_pos && (a.rows < 1 || a.rows > 65535 || a.fuse_heads || a.pf_n || !a.row_tables)) return false;
+  return (a.rows == 1 || a.row_pos) && a.causal && (grp == 1 || grp == 2) && a.kv_heads * grp == a.heads &&
          a.pf_n >= 0 && a.pf_n <= 12 && (a.pf_n == 0 || a.pf_wgs > 0) &&
          (a.row_bytes % 16) == 0 && (a.page_tokens % 32) == 0 && al16(a.k) && al16(a.v) &&
-         al16(a.q8) && (a.scale_row_bytes % 4) == 0 && a.kv_len >= 1 && !a.kv_len_dev;
+         al16(a.q8) && (a.scale_row_bytes % 4) == 0 && (a.kv_len >= 1 || a.row_pos) && !a.kv_len_dev &&
+         (!a.row_pos || (a.ldq % 16) == 0);
 }
 
 hipError_t launch_attn_decode(const AttnArgs &a, hipStream_t s) { return launch_decode(a, s); }

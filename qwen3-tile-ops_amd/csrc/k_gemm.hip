@@ -238,7 +238,8 @@ __global__ void __launch_bounds__(256) argmax_finish_kernel(const unsigned long 
                                                             int64_t best_stride, int32_t *bidx,
                                                             int64_t bidx_stride, int init,
                                                             int32_t *ids_out,
-                                                            const int32_t *pos_dev, int pos_add) {
+                                                            const int32_t *pos_dev, int pos_add,
+                                                            int ids_per_row) {
   __shared__ unsigned long long red[4];
   const int m = blockIdx.x;
   unsigned long long key = 0ull;
@@ -268,7 +269,9 @@ __global__ void __launch_bounds__(256) argmax_finish_kernel(const unsigned long 
   }
   best[m * best_stride] = b;
   bidx[m * bidx_stride] = bi;
-  if (ids_out && m == 0) {
+  if (ids_out && ids_per_row) {
+    ids_out[m] = bi;
+  } else if (ids_out && m == 0) {
     const int p = (pos_dev ? *pos_dev : 0) + pos_add;
     ids_out[p] = bi;
   }
@@ -366,10 +369,11 @@ hipError_t launch_gemm(const GemmArgs &a, hipStream_t s) {
 hipError_t launch_argmax_finish(const unsigned long long *keys, int64_t keys_ld, int nslots,
                                 int M, float *best, int64_t best_stride, int32_t *bidx,
                                 int64_t bidx_stride, int init, int32_t *ids_out,
-                                const int32_t *pos_dev, int pos_add, hipStream_t s) {
+                                const int32_t *pos_dev, int pos_add, hipStream_t s,
+                                int ids_per_row) {
   if (M <= 0) return hipSuccess;
   hipLaunchKernelGGL(argmax_finish_kernel, dim3(M), dim3(256), 0, s, keys, keys_ld, nslots, best,
-                     best_stride, bidx, bidx_stride, init, ids_out, pos_dev, pos_add);
+                     best_stride, bidx, bidx_stride, init, ids_out, pos_dev, pos_add, ids_per_row);
   return hipGetLastError();
 }
 

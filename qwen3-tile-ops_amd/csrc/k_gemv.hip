@@ -509,16 +509,18 @@ __global__ void __launch_bounds__(256) qkv_heads_kernel(QkvHeadArgs a) {
     cs = sn = nullptr;
   }
   float t0 = src[lane], t1 = src[lane + 64];
+  const int64_t csrow = a.row_pos ? static_cast<int64_t>(a.row_pos[m]) : m;
   if (nrq)
-    head_norm_rope(t0, t1, lane, nw, 1, cs + static_cast<int64_t>(m) * a.ld_cs,
-                   sn + static_cast<int64_t>(m) * a.ld_cs, a.inv_hd, true);
+    head_norm_rope(t0, t1, lane, nw, 1, cs + csrow * a.ld_cs, sn + csrow * a.ld_cs, a.inv_hd, true);
   const float mx = max64(fmaxf(fabsf(t0), fabsf(t1)));
   const float scale = __fmul_rn(mx, inv127());
   int8_t *row8;
   float *sp;
   if (d.table) {
-    const uint32_t t = d.pos0 + static_cast<uint32_t>(m);
-    const uint32_t page = d.table[t / d.page_tokens];
+    const bool batched = a.row_pos && h >= a.q_heads;  // K/V of independent sequences
+    const uint32_t t = batched ? static_cast<uint32_t>(a.row_pos[m]) : d.pos0 + static_cast<uint32_t>(m);
+    const uint16_t *table = batched ? a.row_tables + m * a.ld_table : d.table;
+    const uint32_t page = table[t / d.page_tokens];
     const uint32_t slot = t % d.page_tokens;
     row8 = d.q8 + page * d.page_bytes + slot * d.row_bytes + head * 128;
     sp = reinterpret_cast<float *>(reinterpret_cast<int8_t *>(d.qs) + page * d.scale_page_bytes +

@@ -117,13 +117,14 @@ hipError_t launch_gemm(const GemmArgs &a, hipStream_t s);
 // Finishes EPI_ARGMAX: reduces the nslots per-workgroup keys of each row
 // and merges the winner into (best[m], bidx[m]) with the strict
 // `best < value` rule (init != 0: start from -3e38 / 0 instead of the
-// current contents); optionally writes the winning id to ids[*pos].
+// current contents); optionally writes the winning id to ids[*pos] (row 0),
+// or, with ids_per_row, row m's id to ids_out[m].
 hipError_t launch_argmax_finish(const unsigned long long *keys, int64_t keys_ld, int nslots,
                                 int M, float *best,
                                 int64_t best_stride, int32_t *bidx,
                                 int64_t bidx_stride, int init, int32_t *ids_out,
                                 const int32_t *pos_dev, int pos_add,
-                                hipStream_t s);
+                                hipStream_t s, int ids_per_row = 0);
 
 // ---- LDS-staged tiled group GEMM (prefill, M >= 64) ----------------------
 // b1/bs1: the up matrix of EPI_SWIGLUQ (b0/bs0 gate).  Epilogues: STORE, ADD
@@ -213,6 +214,13 @@ struct AttnArgs {
   int pf_n, pf_wgs;
   const int8_t *pf[12];
   int64_t pf_bytes[12];
+  // decode kernel only, independent sequences: when row_pos != null the
+  // launch covers `rows` sequences (one query row each): sequence r attends
+  // over row_pos[r] + 1 keys through page table row_tables + r * ld_table, and
+  // reads/writes row r of q8/qs/o8/os (kv_len and table are ignored)
+  const int32_t *row_pos;
+  const uint16_t *row_tables;
+  int64_t ld_table;
 };
 hipError_t launch_attention(const AttnArgs &a, hipStream_t s);
 
@@ -291,6 +299,12 @@ struct QkvHeadArgs {
   const float *cos_q, *sin_q, *cos_k, *sin_k;  // rows at the rows' positions
   int64_t ld_cs;
   float inv_hd;
+  // independent sequences (batched decode): row m is at position row_pos[m]
+  // (its RoPE row, cos_q/sin_q = table origin) and its K/V go to slot
+  // row_pos[m] of page table row_tables + m * ld_table (kd/vd give the pools)
+  const int32_t *row_pos;
+  const uint16_t *row_tables;
+  int64_t ld_table;
 };
 hipError_t launch_qkv_heads(const QkvHeadArgs &a, hipStream_t s);
 

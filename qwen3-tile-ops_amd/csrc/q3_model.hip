@@ -35,6 +35,23 @@ struct q3_model {
   // argmax workspace: one key per lm_head column block (allocated at open)
   unsigned long long *keys_ws;
   int64_t keys_ld;
+  // batched decode of independent sequences (q3_decode_batch): per-row
+  // positions and page tables (device copies) and argmax key slots
+  // bpos and btab share one device allocation (bstate): positions padded
+  // to 256 bytes, then the tables, so one copy moves both
+  uint8_t *bstate = nullptr;
+  int32_t *bpos = nullptr;         // [seq]
+  uint16_t *btab = nullptr;        // [seq][n_pages]
+  size_t btab_off = 0;
+  // pinned host staging of bstate, two slots: the host fills one while the
+  // copy out of the other may still be pending on the stream
+  uint8_t *bstage[2] = {nullptr, nullptr};
+  hipEvent_t bstage_ev[2] = {nullptr, nullptr};
+  bool bstage_used[2] = {false, false};
+  uint32_t bstage_next = 0;
+  unsigned long long *bkeys = nullptr;  // [seq][bkeys_ld]
+  int64_t bkeys_ld = 0;
+  float *bbest = nullptr;          // [seq] per-row argmax value
   // event timing of decode kernel classes (q3_model_set_kernel_timing)
   uint32_t kt_mask = 0;
   std::vector<hipEvent_t> kt_ev[Q3_KT_COUNT];  // start, end pairs
@@ -56,6 +73,12 @@ constexpr uint32_t kPageTokens = 32;
 constexpr int kMaxGemvRows = 16;
 
 int hip_status(hipError_t e) { return e == hipSuccess ? Q3_OK : Q3_ERR_HIP; }
+
+#define Q3_TRY(expr)             \
+  do {                           \
+    const int rc_ = (expr);      \
+    if (rc_ != Q3_OK) return rc_; \
+  } while (0)
 
 #define Q3_HIP(expr)                                      \
   do {                                                    \
@@ -772,12 +795,25 @@ extern "C" int q3_model_open(void *blob, const q3_layout *lay, void *stream, q3_
   m->keys_ld = lay->vocab / 16 + 64;  // one key per lm_head column block
   m->pf_wgs = 64;
   if (const char *e = std::getenv("Q3_DECODE_PREFETCH_WGS")) m->pf_wgs = std::max(0, std::atoi(e));
+  m->bkeys_ld = lay->vocab / 128 + 64;  // one key per 128-column block of the lm GEMM
+  m->btab_off = (sizeof(int32_t) * lay->seq + 255) & ~size_t(255);
+  const size_t bstate_bytes = m->btab_off + sizeof(uint16_t) * static_cast<size_t>(lay->seq) * m->n_pages;
   if (hipMalloc(&m->ptab, sizeof(uint16_t) * m->n_pages) != hipSuccess ||
       hipMalloc(&m->keys, sizeof(unsigned long long) * 8) != hipSuccess ||
-      hipMalloc(&m->keys_ws, sizeof(unsigned long long) * m->keys_ld) != hipSuccess) {
+      hipMalloc(&m->keys_ws, sizeof(unsigned long long) * m->keys_ld) != hipSuccess ||
+      hipMalloc(&m->bstate, bstate_bytes) != hipSuccess ||
+      hipHostMalloc(&m->bstage[0], bstate_bytes, hipHostMallocDefault) != hipSuccess ||
+      hipHostMalloc(&m->bstage[1], bstate_bytes, hipHostMallocDefault) != hipSuccess ||
+      hipEventCreateWithFlags(&m->bstage_ev[0], hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&m->bstage_ev[1], hipEventDisableTiming) != hipSuccess ||
+      hipMalloc(&m->bkeys, sizeof(unsigned long long) * static_cast<size_t>(lay->seq) * m->bkeys_ld) !=
+          hipSuccess ||
+      hipMalloc(&m->bbest, sizeof(float) * lay->seq) != hipSuccess) {
     q3_model_close(m);
     return Q3_ERR_HIP;
   }
+  m->bpos = reinterpret_cast<int32_t *>(m->bstate);
+  m->btab = reinterpret_cast<uint16_t *>(m->bstate + m->btab_off);
   std::vector<uint16_t> &tab = m->htab;
   tab.resize(m->n_pages);
   for (uint32_t p = 0; p < m->n_pages; ++p) tab[p] = static_cast<uint16_t>(m->n_pages - 1 - p);
@@ -788,6 +824,233 @@ extern "C" int q3_model_open(void *blob, const q3_layout *lay, void *stream, q3_
     return Q3_ERR_HIP;
   }
   *out = m;
+  return Q3_OK;
+}
+
+// One decode step of n independent sequences (batched decode).  The
+// reference's pieces for it are op-level: paged_kv_scatter_batch
+// (kernels/kv_pages.h) writes each request's K/V row through its own page
+// table, and paged attention runs per request (tests/guest/paged_attn_multi
+// .cpp); every GEMM is row-independent, so the rows of different sequences
+// share one launch.  Row r: token ids[r] (device) at position pos[r], pages
+// tables[r * ld_table ...] (host arrays, validated here and staged through
+// pinned memory to the model's device buffers, so the call does not wait for
+// the stream); out_ids[r] (device) receives its greedy id.
+extern "C" int q3_decode_batch(q3_model *m, uint32_t n, const int32_t *ids, const int32_t *pos,
+                               const uint16_t *tables, uint32_t ld_table, int32_t *out_ids) {
+  if (!m || !ids || !pos || !tables || !out_ids || n == 0) return Q3_ERR_ARG;
+  const q3_layout &y = m->lay;
+  if (n > y.seq) return Q3_ERR_RANGE;
+  if (ld_table == 0 || ld_table > m->n_pages) return Q3_ERR_ARG;
+  for (uint32_t r = 0; r < n; ++r) {
+    if (pos[r] < 0 || static_cast<uint32_t>(pos[r]) >= y.max_seq) return Q3_ERR_RANGE;
+    if (static_cast<uint32_t>(pos[r]) / kPageTokens >= ld_table) return Q3_ERR_RANGE;
+    for (uint32_t i = 0; i <= static_cast<uint32_t>(pos[r]) / kPageTokens; ++i)
+      if (tables[static_cast<size_t>(r) * ld_table + i] >= m->n_pages) return Q3_ERR_RANGE;
+  }
+  const hipStream_t s = m->stream;
+  {
+    const uint32_t slot = m->bstage_next;
+    if (m->bstage_used[slot]) Q3_HIP(hipEventSynchronize(m->bstage_ev[slot]));
+    uint8_t *st = m->bstage[slot];
+    const size_t tab_bytes = sizeof(uint16_t) * static_cast<size_t>(n) * ld_table;
+    std::memcpy(st, pos, sizeof(int32_t) * n);
+    std::memcpy(st + m->btab_off, tables, tab_bytes);
+    Q3_HIP(hipMemcpyAsync(m->bstate, st, m->btab_off + tab_bytes, hipMemcpyHostToDevice, s));
+    Q3_HIP(hipEventRecord(m->bstage_ev[slot], s));
+    m->bstage_used[slot] = true;
+    m->bstage_next = slot ^ 1;
+  }
+  const int H = static_cast<int>(y.hidden), HD = static_cast<int>(y.head_dim);
+  const int QW = static_cast<int>(y.heads) * HD, KW = static_cast<int>(y.kv_heads) * HD;
+  const int I = static_cast<int>(y.inter), V = static_cast<int>(y.vocab);
+  const int HALF = static_cast<int>(y.half);
+  const int M = static_cast<int>(n);
+  float *x = at<float>(m, y.kX);
+  float *h = at<float>(m, y.kH);
+  int8_t *h8 = at<int8_t>(m, y.kH8);
+  float *hs = at<float>(m, y.kHS);
+  float *q = at<float>(m, y.kQ);
+  float *k = at<float>(m, y.kK);
+  float *v = at<float>(m, y.kV);
+  int8_t *q8 = at<int8_t>(m, y.kQ8);
+  float *qs = at<float>(m, y.kQS);
+  int8_t *o8 = at<int8_t>(m, y.kO8);
+  float *os = at<float>(m, y.kOS);
+  int8_t *s8 = at<int8_t>(m, y.kS8);
+  float *ss = at<float>(m, y.kSS);
+  const float *cos_t = at<const float>(m, y.kCOS);
+  const float *sin_t = at<const float>(m, y.kSIN);
+  const float qk_scale = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(HD)));
+
+  auto rows = [&](int mode, const float *w) -> int {  // embedding/RMSNorm + quant of n rows
+    q3::RowArgs r{};
+    r.mode = mode;
+    r.rows = M;
+    r.cols = H;
+    r.x = x;
+    r.ldx = H;
+    if (mode == 2) {
+      r.table = at<const int8_t>(m, y.kEMB);
+      r.ldt = H;
+      r.table_rows = y.vocab;
+      r.tscale = at<const float>(m, y.kEMB + static_cast<int64_t>(V) * H);
+      r.tss = 1;
+      r.ids = ids;
+      r.ids_stride = 1;
+      r.x_out = x;
+      r.ldxo = H;
+    }
+    r.w = w;
+    r.w_stride = 1;
+    r.inv = 1.0f / static_cast<float>(H);
+    r.h = h;
+    r.ldh = H;
+    r.h8 = h8;
+    r.ldh8 = H;
+    r.hs = hs;
+    r.ldhs = H / 256;
+    r.group = 256;
+    return hip_status(q3::launch_rows(r, s));
+  };
+  Q3_TRY(rows(2, layer_ptrs(m, 0).n1));
+  for (uint32_t L = 0; L < y.layers; ++L) {
+    const LayerPtrs lp = layer_ptrs(m, L);
+    if (L != 0) Q3_TRY(rows(1, lp.n1));
+    // Q, K, V projections (f32 rows), then the per-row head epilogues
+    {
+      q3::GemmArgs g = gemm_args(M, QW, H, 256, h8, hs, lp.wq, lp.wqs);
+      g.epi = q3::EPI_STORE;
+      g.out = q;
+      g.ldo = QW;
+      Q3_HIP(q3::launch_gemm(g, s));
+      g = gemm_args(M, KW, H, 256, h8, hs, lp.wk, lp.wks);
+      g.epi = q3::EPI_STORE;
+      g.out = k;
+      g.ldo = KW;
+      Q3_HIP(q3::launch_gemm(g, s));
+      g = gemm_args(M, KW, H, 256, h8, hs, lp.wv, lp.wvs);
+      g.epi = q3::EPI_STORE;
+      g.out = v;
+      g.ldo = KW;
+      Q3_HIP(q3::launch_gemm(g, s));
+    }
+    {
+      q3::QkvHeadArgs e;
+      std::memset(&e, 0, sizeof(e));
+      e.M = M;
+      e.q_heads = static_cast<int>(y.heads);
+      e.kv_heads = static_cast<int>(y.kv_heads);
+      e.q = q;
+      e.k = k;
+      e.v = v;
+      e.ldq = QW;
+      e.ldk = KW;
+      set_paged(e.kd, m, lp.kc, lp.kcs, 0);
+      set_paged(e.vd, m, lp.vc, lp.vcs, 0);
+      e.qd.q8 = q8;
+      e.qd.ldq8 = QW;
+      e.qd.qs = qs;
+      e.qd.ldqs = y.heads;
+      e.qd.qs_col = 1;
+      e.nq = lp.nq;
+      e.nk = lp.nk;
+      e.cos_q = e.cos_k = cos_t;
+      e.sin_q = e.sin_k = sin_t;
+      e.ld_cs = HALF;
+      e.inv_hd = 1.0f / static_cast<float>(HD);
+      e.row_pos = m->bpos;
+      e.row_tables = m->btab;
+      e.ld_table = ld_table;
+      Q3_HIP(q3::launch_qkv_heads(e, s));
+    }
+    {
+      q3::AttnArgs t{};
+      t.rows = M;
+      t.heads = static_cast<int>(y.heads);
+      t.kv_heads = static_cast<int>(y.kv_heads);
+      t.causal = 1;
+      t.qk_scale = qk_scale;
+      t.q8 = q8;
+      t.ldq = QW;
+      t.qs = qs;
+      t.ldqs = y.heads;
+      t.qs_col = 1;
+      t.k = lp.kc;
+      t.v = lp.vc;
+      t.ks = lp.kcs;
+      t.vs = lp.vcs;
+      t.table = m->btab;
+      t.page_tokens = kPageTokens;
+      t.page_bytes = static_cast<int64_t>(kPageTokens) * KW;
+      t.row_bytes = KW;
+      t.scale_page_bytes = static_cast<int64_t>(kPageTokens) * y.kv_heads * 4;
+      t.scale_row_bytes = y.kv_heads * 4;
+      t.o8 = o8;
+      t.ldo = QW;
+      t.os = os;
+      t.ldos = y.heads;
+      t.os_col = 1;
+      t.row_pos = m->bpos;
+      t.row_tables = m->btab;
+      t.ld_table = ld_table;
+      if (!q3::attn_decode_supported(t)) return Q3_ERR_UNSUPPORTED;
+      KTimer kt(m, Q3_KT_ATTN_DECODE);
+      Q3_HIP(q3::launch_attn_decode(t, s));
+    }
+    {  // O projection + residual
+      q3::GemmArgs g = gemm_args(M, H, QW, HD, o8, os, lp.wo, lp.wos);
+      g.ldas = y.heads;
+      g.epi = q3::EPI_ADD;
+      g.out = x;
+      g.ldo = H;
+      Q3_HIP(q3::launch_gemm(g, s));
+    }
+    Q3_TRY(rows(1, lp.n2));
+    {  // gate/up + SwiGLU + quant
+      q3::GateUpArgs u;
+      std::memset(&u, 0, sizeof(u));
+      u.M = M;
+      u.N = I;
+      u.K = H;
+      u.group = 256;
+      u.a = h8;
+      u.lda = H;
+      u.as = hs;
+      u.ldas = H / 256;
+      u.wg = lp.wg;
+      u.wu = lp.wu;
+      u.ldw = H;
+      u.wgs = lp.wgs;
+      u.wus = lp.wus;
+      u.ws_stride = 1;
+      u.s8 = s8;
+      u.lds8 = I;
+      u.ss = ss;
+      u.ldss = I / 256;
+      u.ss_col = 1;
+      Q3_HIP(q3::launch_gate_up(u, s));
+    }
+    {  // down projection + residual
+      q3::GemmArgs g = gemm_args(M, H, I, 256, s8, ss, lp.wd, lp.wds);
+      g.epi = q3::EPI_ADD;
+      g.out = x;
+      g.ldo = H;
+      Q3_HIP(q3::launch_gemm(g, s));
+    }
+  }
+  // final RMSNorm + quant, lm_head argmax per row (main_big.cpp:264-290)
+  Q3_TRY(rows(1, at<const float>(m, y.kNF)));
+  {
+    q3::GemmArgs g = gemm_args(M, V, H, 256, h8, hs, at<const int8_t>(m, y.kLM),
+                               at<const float>(m, y.kLM + static_cast<int64_t>(V) * H));
+    g.epi = q3::EPI_ARGMAX;
+    g.keys = m->bkeys;
+    g.keys_ld = m->bkeys_ld;
+    Q3_HIP(q3::launch_gemm(g, s));
+    Q3_HIP(q3::launch_argmax_finish(m->bkeys, m->bkeys_ld, V / 128, M, m->bbest, 1, out_ids, 1,
+                                    /*init=*/1, out_ids, nullptr, 0, s, /*ids_per_row=*/1));
+  }
   return Q3_OK;
 }
 
@@ -867,6 +1130,13 @@ extern "C" int q3_model_close(q3_model *m) {
   if (m->ptab) (void)hipFree(m->ptab);
   if (m->keys) (void)hipFree(m->keys);
   if (m->keys_ws) (void)hipFree(m->keys_ws);
+  if (m->bstate) (void)hipFree(m->bstate);
+  for (int i = 0; i < 2; ++i) {
+    if (m->bstage[i]) (void)hipHostFree(m->bstage[i]);
+    if (m->bstage_ev[i]) (void)hipEventDestroy(m->bstage_ev[i]);
+  }
+  if (m->bkeys) (void)hipFree(m->bkeys);
+  if (m->bbest) (void)hipFree(m->bbest);
   for (int c = 0; c < Q3_KT_COUNT; ++c)
     for (hipEvent_t e : m->kt_ev[c]) (void)hipEventDestroy(e);
   delete m;

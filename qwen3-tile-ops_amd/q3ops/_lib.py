@@ -101,6 +101,7 @@ SIGNATURES = {
     "q3_forward_chunk": (_I, [_VP, _U, _U, _I, _I]),
     "q3_generate": (_I, [_VP]),
     "q3_model_close": (_I, [_VP]),
+    "q3_decode_batch": (_I, [_VP, _U, _VP, _VP, _VP, _U, _VP]),
     "q3_model_set_kernel_timing": (_I, [_VP, _U]),
     "q3_model_kernel_time": (_I, [_VP, _I, C.POINTER(C.c_double), C.POINTER(C.c_uint32)]),
 }

@@ -55,6 +55,21 @@ class Model:
     def synchronize(self) -> None:
         self.stream.synchronize()
 
+    def decode_batch(self, ids: torch.Tensor, pos, tables, out_ids: torch.Tensor) -> None:
+        """q3_decode_batch: one token for each of n independent sequences.
+        ids/out_ids: int32 device tensors [n]; pos: host int32 [n]; tables:
+        host uint16 [n][ld_table] (logical -> physical pages)."""
+        pos = np.ascontiguousarray(pos, np.int32)
+        tables = np.ascontiguousarray(tables, np.uint16)
+        n = pos.shape[0]
+        assert tables.ndim == 2 and tables.shape[0] == n
+        assert ids.dtype == torch.int32 and ids.is_cuda and ids.numel() >= n
+        assert out_ids.dtype == torch.int32 and out_ids.is_cuda and out_ids.numel() >= n
+        check(lib().q3_decode_batch(self.handle, n, C.c_void_p(ids.data_ptr()),
+                                    pos.ctypes.data_as(C.c_void_p),
+                                    tables.ctypes.data_as(C.c_void_p), tables.shape[1],
+                                    C.c_void_p(out_ids.data_ptr())), "q3_decode_batch")
+
     # decode kernel classes of q3_model_set_kernel_timing (include/q3ops.h)
     KERNEL_CLASSES = ("attn_decode", "gemv_qkv", "gemv_o", "gemv_gate_up", "gemv_down", "lm_head")
 
