@@ -1,5 +1,5 @@
 // Paged hd128 GQA attention with the reference's block-quantised online
-// softmax.
+// softmax (prefill and any multi-row chunk).
 //
 //   kernels/attention_gqa.h:404-572 attention_heads_gqa_tokscale_paged /
 //                                   attention_head_hd128_blocks_paged
@@ -14,11 +14,25 @@
 //   res += f32(P8 . V) * pmax
 // then out = res * (1/den) and per-head int8 quantisation of out.
 //
-// Workgroup = 4 waves.  S (32x32) and P8.V (32x128) use
-// v_mfma_i32_16x16x64_i8; the 32-key K operand of P8.V is zero-padded to
-// 64.  The softmax step gives each half-wave one query row, so the block's
-// tree sum is a 32-lane butterfly (equal to the reference's pairwise tree,
-// with +0 padding for a partial last block).
+// Workgroup = 4 waves on one (head, 16-row query block).  The key blocks are
+// streamed through NS LDS stages with global_load_lds copies issued NS - 1
+// blocks ahead, so a block's K, V and scales are resident when its turn
+// comes (the walk over blocks is the reference's sequential recurrence; only
+// the copies run ahead).  The blocks' page ids are read once into LDS.
+//   K stage  [32 keys][128] int8, 16-byte chunks XOR-swizzled by key so the
+//            MFMA operand reads of 16 keys spread over the LDS banks
+//   V stage  [32 keys][128] int8, transposed per block into vt [dim][key]
+//            (rows padded to 80 bytes) with 4x4 byte transposes (v_perm_b32)
+//   scales   ks[32] | vs[32] f32 of the block's keys for this KV head
+// S (16x32) and P8.V (16x128) use v_mfma_i32_16x16x64_i8; the 32-key K
+// operand of P8.V is zero-padded to 64.  The softmax step gives each
+// half-wave one query row, so the block's tree sum is a 32-lane butterfly
+// (equal to the reference's pairwise tree, with +0 padding for a partial
+// last block); a wave's 4 rows run side by side.  The per-block work of a
+// workgroup is VALU-issue bound (one wave per SIMD), and the causal
+// critical path is the last query block, which walks every key block: 16
+// rows per workgroup halve that path against 32 (twice the workgroups, two
+// per CU).
 #include "q3_device.h"
 #include "q3_kernels.h"
 
@@ -32,17 +46,53 @@ __device__ __forceinline__ v4i zero4() {
   return z;
 }
 
-constexpr int QB = 32;    // query rows per workgroup
+constexpr int QB = 16;    // query rows per workgroup
 constexpr int KB = 32;    // keys per block (= reference block)
 constexpr int HD = 128;
 constexpr int LDO = HD + 4;
+constexpr int NS = 4;     // LDS stages (copies run NS - 1 blocks ahead)
+constexpr int PGW = 512;  // page ids held in LDS at a time (blocks)
+// vt row stride: 64 key bytes + 16 bytes of padding, so that the transpose's
+// dword writes of 16 consecutive dims fall in different LDS banks (a 64-byte
+// stride puts them all in one) while rows stay 16-byte aligned for the MFMA
+// operand reads
+constexpr int VTS = 80;
+
+struct Stage {
+  int8_t k[KB * HD];
+  int8_t v[KB * HD];
+  float sc[2 * KB];  // ks[0..31], vs[32..63]
+};
+
+// Copies of key block b (its page id in pg) into stage st.  Every wave
+// copies a quarter of K and of V (one 16-byte global_load_lds each); wave 0
+// also copies the 64 scales (one 4-byte global_load_lds).
+__device__ __forceinline__ void issue_block(const AttnArgs &a, Stage &st, uint32_t page, int b,
+                                            int kvh, int tid, int wave, int lane) {
+  const uint32_t slot0 = static_cast<uint32_t>(b * KB) % a.page_tokens;
+  const int key = tid >> 3;
+  const int chunk = (tid & 7) ^ (key & 7);
+  const int8_t *kp = a.k + page * a.page_bytes + (slot0 + key) * a.row_bytes + kvh * HD + chunk * 16;
+  const int8_t *vp = a.v + page * a.page_bytes + (slot0 + key) * a.row_bytes + kvh * HD + (tid & 7) * 16;
+  __builtin_amdgcn_global_load_lds(const_cast<int8_t *>(kp), to_lds(st.k + wave * 1024), 16, 0, 0);
+  __builtin_amdgcn_global_load_lds(const_cast<int8_t *>(vp), to_lds(st.v + wave * 1024), 16, 0, 0);
+  if (wave == 0) {
+    const int c = lane & 31;
+    const float *sbase = lane < 32 ? a.ks : a.vs;
+    const int8_t *sp = reinterpret_cast<const int8_t *>(sbase) + page * a.scale_page_bytes +
+                       (slot0 + c) * a.scale_row_bytes + kvh * 4;
+    __builtin_amdgcn_global_load_lds(const_cast<int8_t *>(sp), to_lds(st.sc), 4, 0, 0);
+  }
+}
 
 __global__ void __launch_bounds__(256) attention_kernel(AttnArgs a) {
+  __shared__ __align__(16) Stage stg[NS];
   __shared__ int32_t s_i32[QB][KB + 1];
   __shared__ __align__(16) int8_t p8[QB][64];     // [row][key], keys 32..63 = 0
-  __shared__ __align__(16) int8_t vt[HD][64];     // [dim][key], keys 32..63 = 0
-  __shared__ float row_max[QB], row_den[QB], row_corr[QB], row_pmax[QB];
-  __shared__ float otile[QB][LDO];
+  __shared__ __align__(16) int8_t vt[HD][VTS];    // [dim][key], keys 32..63 = 0
+  __shared__ float row_max[QB], row_den[QB], row_corr[QB], row_pmax[QB], row_qs[QB];
+  __shared__ uint64_t etab[32];
+  __shared__ uint32_t pg[PGW];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -59,130 +109,179 @@ __global__ void __launch_bounds__(256) attention_kernel(AttnArgs a) {
   const int pos0 = a.causal ? static_cast<int>(kv_len) - a.rows + qi : 0;
   int kv_end = static_cast<int>(kv_len);
   if (a.causal && pos0 + nr < kv_end) kv_end = pos0 + nr;
+  const int nblk = (kv_end + KB - 1) / KB;
+  const uint32_t ppb = a.page_tokens / KB;  // blocks per page
 
-  // zero the K padding of the P8 and V^T tiles once
+  // ---- prologue: page ids, exp table, row state, Q fragments ----
+  for (int b = tid; b < min(nblk, PGW); b += 256) pg[b] = a.table[static_cast<uint32_t>(b) / ppb];
+  if (tid < 32) etab[tid] = kExp2Tab[tid];
   for (int i = tid; i < QB * 32; i += 256) p8[i / 32][32 + i % 32] = 0;
   for (int i = tid; i < HD * 32; i += 256) vt[i / 32][32 + i % 32] = 0;
   if (tid < QB) {
     row_max[tid] = -3.402823466e38f;
     row_den[tid] = 0.0f;
+    row_qs[tid] = tid < nr ? a.qs[static_cast<int64_t>(qi + tid) * a.ldqs + h * a.qs_col] : 0.0f;
   }
-
-  // Q operand for S: wave w -> m-tile (w >> 1), n-tile (w & 1)
-  const int s_mt = wave >> 1, s_nt = wave & 1;
+  // Q operand for S: waves 0 and 1 -> key n-tile `wave` (16 keys)
+  const int s_nt = wave & 1;
   v4i qa[2];
   {
-    const int r = s_mt * 16 + lr;
+    const int r = lr;
     for (int ks = 0; ks < 2; ++ks)
-      qa[ks] = (r < nr) ? *reinterpret_cast<const v4i *>(
-                              a.q8 + static_cast<int64_t>(qi + r) * a.ldq + h * HD + ks * 64 + lg * 16)
-                        : zero4();
+      qa[ks] = (r < nr && wave < 2) ? *reinterpret_cast<const v4i *>(
+                                          a.q8 + static_cast<int64_t>(qi + r) * a.ldq + h * HD + ks * 64 + lg * 16)
+                                    : zero4();
   }
+  // Q fragments complete before the copies start, so the loop's waits only
+  // count copies (the compiler would otherwise wait for everything at the
+  // first use of qa inside the loop)
+  wait_vmcnt<0>();
+  __syncthreads();
+  for (int b = 0; b < NS - 1 && b < nblk; ++b) issue_block(a, stg[b], pg[b], b, kvh, tid, wave, lane);
 
-  float res[2][2][4];
-  for (int mt = 0; mt < 2; ++mt)
-    for (int nt = 0; nt < 2; ++nt)
-      for (int i = 0; i < 4; ++i) res[mt][nt][i] = 0.0f;
+  float res[2][4];
+  for (int nt = 0; nt < 2; ++nt)
+    for (int i = 0; i < 4; ++i) res[nt][i] = 0.0f;
 
-  for (int j = 0; j < kv_end; j += KB) {
-    const uint32_t page = a.table[static_cast<uint32_t>(j) / a.page_tokens];
-    const uint32_t slot0 = static_cast<uint32_t>(j) % a.page_tokens;
-    const int8_t *kbase = a.k + page * a.page_bytes + slot0 * a.row_bytes + kvh * HD;
-    const int8_t *vbase = a.v + page * a.page_bytes + slot0 * a.row_bytes + kvh * HD;
-    const float *ksb = reinterpret_cast<const float *>(
-        reinterpret_cast<const int8_t *>(a.ks) + page * a.scale_page_bytes + slot0 * a.scale_row_bytes);
-    const float *vsb = reinterpret_cast<const float *>(
-        reinterpret_cast<const int8_t *>(a.vs) + page * a.scale_page_bytes + slot0 * a.scale_row_bytes);
+  for (int jb = 0; jb < nblk; ++jb) {
+    const int j = jb * KB;
     const int nvalid = min(KB, static_cast<int>(kv_len) - j);
+    Stage &st = stg[jb % NS];
+    // ---- copies of block jb + NS - 1 (its stage was last read by block jb - 1) ----
+    const int bi = jb + NS - 1;
+    if (bi < nblk) {
+      if ((bi % PGW) == 0) {  // next window of page ids (contexts over PGW blocks)
+        for (int b = bi + tid; b < min(nblk, bi + PGW); b += 256)
+          pg[b % PGW] = a.table[static_cast<uint32_t>(b) / ppb];
+        __syncthreads();
+      }
+      issue_block(a, stg[bi % NS], pg[bi % PGW], bi, kvh, tid, wave, lane);
+      if (wave == 0)
+        wait_vmcnt<3 * (NS - 1)>();
+      else
+        wait_vmcnt<2 * (NS - 1)>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    lds_barrier();
 
     // ---- S = q8 . k8^T ----
-    {
+    if (wave < 2) {
       const int key = s_nt * 16 + lr;
       v4i c = zero4();
       for (int ks = 0; ks < 2; ++ks) {
-        const v4i kb = (key < nvalid)
-                           ? *reinterpret_cast<const v4i *>(kbase + key * a.row_bytes + ks * 64 + lg * 16)
-                           : zero4();
+        const int chunk = (ks * 4 + lg) ^ (key & 7);
+        const v4i kb = *reinterpret_cast<const v4i *>(st.k + key * HD + chunk * 16);
         c = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa[ks], kb, c, 0, 0, 0);
       }
-      for (int i = 0; i < 4; ++i) s_i32[s_mt * 16 + lg * 4 + i][s_nt * 16 + lr] = c[i];
+      for (int i = 0; i < 4; ++i) s_i32[lg * 4 + i][s_nt * 16 + lr] = c[i];
     }
-    // ---- V block -> LDS, transposed to [dim][key] ----
+    // ---- V block -> vt [dim][key]: thread = 4 keys x 4 dims ----
     {
-      const int key = tid >> 3;        // 0..31
-      const int d0 = (tid & 7) * 16;   // 0..112
-      v4i vv = zero4();
-      if (key < nvalid) vv = *reinterpret_cast<const v4i *>(vbase + key * a.row_bytes + d0);
-      const int8_t *vb = reinterpret_cast<const int8_t *>(&vv);
-      for (int d = 0; d < 16; ++d) vt[d0 + d][key] = vb[d];
+      const int kq = tid >> 5;        // keys 4kq..4kq+3
+      const int dq = tid & 31;        // dims 4dq..4dq+3
+      const uint32_t w0 = *reinterpret_cast<const uint32_t *>(st.v + (4 * kq + 0) * HD + 4 * dq);
+      const uint32_t w1 = *reinterpret_cast<const uint32_t *>(st.v + (4 * kq + 1) * HD + 4 * dq);
+      const uint32_t w2 = *reinterpret_cast<const uint32_t *>(st.v + (4 * kq + 2) * HD + 4 * dq);
+      const uint32_t w3 = *reinterpret_cast<const uint32_t *>(st.v + (4 * kq + 3) * HD + 4 * dq);
+      const uint32_t x01l = __builtin_amdgcn_perm(w1, w0, 0x06020400u);
+      const uint32_t x01h = __builtin_amdgcn_perm(w1, w0, 0x07030501u);
+      const uint32_t x23l = __builtin_amdgcn_perm(w3, w2, 0x06020400u);
+      const uint32_t x23h = __builtin_amdgcn_perm(w3, w2, 0x07030501u);
+      *reinterpret_cast<uint32_t *>(&vt[4 * dq + 0][4 * kq]) = __builtin_amdgcn_perm(x23l, x01l, 0x05040100u);
+      *reinterpret_cast<uint32_t *>(&vt[4 * dq + 1][4 * kq]) = __builtin_amdgcn_perm(x23h, x01h, 0x05040100u);
+      *reinterpret_cast<uint32_t *>(&vt[4 * dq + 2][4 * kq]) = __builtin_amdgcn_perm(x23l, x01l, 0x07060302u);
+      *reinterpret_cast<uint32_t *>(&vt[4 * dq + 3][4 * kq]) = __builtin_amdgcn_perm(x23h, x01h, 0x07060302u);
     }
-    __syncthreads();
+    lds_barrier();
 
-    // ---- online softmax, one query row per half-wave ----
-    for (int pass = 0; pass < 4; ++pass) {
-      const int r = wave * 8 + pass * 2 + (lane >> 5);
+    // ---- online softmax: a half-wave per query row, a wave's 4 rows ----
+    // ---- side by side (independent chains interleave)             ----
+    {
       const int c = lane & 31;
-      if (r < nr) {  // whole half-wave agrees on r
-        const bool kvalid = c < nvalid;
-        float s = -INFINITY;
-        if (kvalid) {
-          s = static_cast<float>(s_i32[r][c]);
-          s = __fmul_rn(s, ksb[c * (a.scale_row_bytes / 4) + kvh]);
-          s = __fmul_rn(s, a.qs[static_cast<int64_t>(qi + r) * a.ldqs + h * a.qs_col]);
-          s = __fmul_rn(s, a.qk_scale);
-          if (a.causal && (c - r) > (pos0 - j)) s = -INFINITY;
-        }
-        const float bmax = max32(s);
-        const float mold = row_max[r];
-        const float nmm = (mold > bmax) ? mold : bmax;
-        const float corr = exp_f32(__fsub_rn(mold, nmm));
-        const float p = kvalid ? exp_f32(__fsub_rn(s, nmm)) : 0.0f;
-        const float psum = tree_sum32(p);
-        float pv = 0.0f;
-        if (kvalid) pv = __fmul_rn(p, vsb[c * (a.scale_row_bytes / 4) + kvh]);
-        const float pm = __fmul_rn(max32(pv), inv127());
-        p8[r][c] = static_cast<int8_t>(quant1(pv, pm));
-        if (c == 0) {
-          row_den[r] = __fadd_rn(__fmul_rn(row_den[r], corr), psum);
-          row_max[r] = nmm;
-          row_corr[r] = corr;
-          row_pmax[r] = pm;
+      const bool kvalid = c < nvalid;
+      const float ksc = st.sc[c];
+      const float vsc = kvalid ? st.sc[KB + c] : 0.0f;  // keys past kv_len: P = 0, P*vs = 0
+      constexpr int NP = QB / 8;  // rows per half-wave
+      int rr[NP];
+      float sv[NP], mold[NP];
+#pragma unroll
+      for (int pass = 0; pass < NP; ++pass) {
+        const int r = wave * (2 * NP) + pass * 2 + (lane >> 5);
+        rr[pass] = r;
+        // read unconditionally (r, c < 32), select afterwards
+        float x = static_cast<float>(s_i32[r][c]);
+        x = __fmul_rn(x, ksc);
+        x = __fmul_rn(x, row_qs[r]);
+        x = __fmul_rn(x, a.qk_scale);
+        const bool masked = !kvalid || r >= nr || (a.causal && (c - r) > (pos0 - j));
+        sv[pass] = masked ? -INFINITY : x;
+        mold[pass] = row_max[r];
+      }
+      float nmm[NP], corr[NP], p[NP], psum[NP], pv[NP], pm[NP];
+#pragma unroll
+      for (int pass = 0; pass < NP; ++pass) {
+        const float bmax = max32(sv[pass]);
+        nmm[pass] = (mold[pass] > bmax) ? mold[pass] : bmax;
+      }
+#pragma unroll
+      for (int pass = 0; pass < NP; ++pass) {
+        corr[pass] = exp_f32_le0_tab(__fsub_rn(mold[pass], nmm[pass]), etab);
+        // masked and missing keys hold -inf: exp gives exactly +0
+        p[pass] = exp_f32_le0_tab(__fsub_rn(sv[pass], nmm[pass]), etab);
+      }
+#pragma unroll
+      for (int pass = 0; pass < NP; ++pass) {
+        psum[pass] = tree_sum32(p[pass]);
+        pv[pass] = __fmul_rn(p[pass], vsc);
+      }
+#pragma unroll
+      for (int pass = 0; pass < NP; ++pass) pm[pass] = __fmul_rn(max32(pv[pass]), inv127());
+#pragma unroll
+      for (int pass = 0; pass < NP; ++pass) {
+        const int r = rr[pass];
+        if (r < nr) {  // whole half-wave agrees on r
+          p8[r][c] = static_cast<int8_t>(quant1(pv[pass], pm[pass]));
+          if (c == 0) {
+            row_den[r] = __fadd_rn(__fmul_rn(row_den[r], corr[pass]), psum[pass]);
+            row_max[r] = nmm[pass];
+            row_corr[r] = corr[pass];
+            row_pmax[r] = pm[pass];
+          }
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- res = res * corr + f32(P8 . V) * pmax ----
     {
-      v4i pa[2], vb[2];
-      for (int mt = 0; mt < 2; ++mt) pa[mt] = *reinterpret_cast<const v4i *>(&p8[mt * 16 + lr][lg * 16]);
+      const v4i pa = *reinterpret_cast<const v4i *>(&p8[lr][lg * 16]);
+      v4i vb[2];
       for (int nt = 0; nt < 2; ++nt)
         vb[nt] = *reinterpret_cast<const v4i *>(&vt[wave * 32 + nt * 16 + lr][lg * 16]);
-      for (int mt = 0; mt < 2; ++mt)
-        for (int nt = 0; nt < 2; ++nt) {
-          const v4i c = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa[mt], vb[nt], zero4(), 0, 0, 0);
-          for (int i = 0; i < 4; ++i) {
-            const int r = mt * 16 + lg * 4 + i;
-            if (r < nr) {
-              const float part = __fmul_rn(static_cast<float>(c[i]), row_pmax[r]);
-              res[mt][nt][i] = __fadd_rn(__fmul_rn(res[mt][nt][i], row_corr[r]), part);
-            }
-          }
+      for (int nt = 0; nt < 2; ++nt) {
+        const v4i c = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa, vb[nt], zero4(), 0, 0, 0);
+        for (int i = 0; i < 4; ++i) {
+          const int r = lg * 4 + i;  // rows >= nr are never stored
+          const float part = __fmul_rn(static_cast<float>(c[i]), row_pmax[r]);
+          res[nt][i] = __fadd_rn(__fmul_rn(res[nt][i], row_corr[r]), part);
         }
+      }
     }
-    __syncthreads();
+    lds_barrier();  // s_i32, vt, p8, row state and stage jb % NS are rewritten next
   }
 
   // ---- out = res * (1/den), then per-head int8 quantisation ----
-  for (int mt = 0; mt < 2; ++mt)
-    for (int nt = 0; nt < 2; ++nt)
-      for (int i = 0; i < 4; ++i) {
-        const int r = mt * 16 + lg * 4 + i;
-        if (r < nr) {
-          const float rd = __fdiv_rn(1.0f, row_den[r]);
-          otile[r][wave * 32 + nt * 16 + lr] = __fmul_rn(res[mt][nt][i], rd);
-        }
+  float(*otile)[LDO] = reinterpret_cast<float(*)[LDO]>(&stg[0]);  // stages are free now
+  static_assert(sizeof(float) * QB * LDO <= sizeof(Stage) * NS, "otile fits in the stages");
+  for (int nt = 0; nt < 2; ++nt)
+    for (int i = 0; i < 4; ++i) {
+      const int r = lg * 4 + i;
+      if (r < nr) {
+        const float rd = __fdiv_rn(1.0f, row_den[r]);
+        otile[r][wave * 32 + nt * 16 + lr] = __fmul_rn(res[nt][i], rd);
       }
+    }
   __syncthreads();
   for (int r = wave; r < nr; r += 4) {
     const float t0 = otile[r][lane], t1 = otile[r][lane + 64];
@@ -204,6 +303,10 @@ __global__ void __launch_bounds__(256) attention_kernel(AttnArgs a) {
 
 hipError_t launch_attention(const AttnArgs &a, hipStream_t s) {
   if (a.rows <= 0) return hipSuccess;
+  // the stage copies address whole 32-key blocks inside one page
+  if (a.page_tokens % KB || a.row_bytes % 16 || a.kv_heads <= 0 || a.heads % a.kv_heads ||
+      (a.scale_row_bytes % 4))
+    return hipErrorInvalidValue;
   const dim3 grid(a.heads, (a.rows + QB - 1) / QB);
   hipLaunchKernelGGL(attention_kernel, grid, dim3(256), 0, s, a);
   return hipGetLastError();

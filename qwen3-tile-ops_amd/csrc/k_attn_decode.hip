@@ -101,13 +101,15 @@ struct Smem {
 // Operands of the fused head epilogue of one wave (see fused_load).
 struct FusedRegs {
   float t0, t1, w0, w1, c, s;
+  uint32_t page;  // K/V waves of the writing workgroup: page of the new token
 };
 
 // wave 0: K head kvh, wave 1: V head kvh, waves 2..: query heads qh0 + h
 template <int QPW>
 __device__ __forceinline__ void fused_load(const AttnArgs &a, int kvh, int qh0, int wave, int lane,
-                                           FusedRegs &r) {
+                                           bool kv_writer, FusedRegs &r) {
   if (wave >= 2 + QPW) return;
+  if (wave < 2 && kv_writer) r.page = a.table[(a.kv_len - 1) / a.page_tokens];
   const float *src = wave == 0 ? a.fk + kvh * HD : wave == 1 ? a.fv + kvh * HD : a.fq + (qh0 + wave - 2) * HD;
   r.t0 = src[lane];
   r.t1 = src[lane + 64];
@@ -137,7 +139,7 @@ __device__ void fused_compute(const AttnArgs &a, SM &sm, FusedRegs r, int kvh, i
     lrow = wave == 0 ? sm.knew : sm.vnew;
     lsp = wave == 0 ? &sm.ksnew : &sm.vsnew;
     if (kv_writer) {
-      const uint32_t page = a.table[t / a.page_tokens];
+      const uint32_t page = r.page;
       const uint32_t slot = t % a.page_tokens;
       int8_t *row8 = const_cast<int8_t *>(wave == 0 ? a.k : a.v) + page * a.page_bytes +
                      slot * a.row_bytes + kvh * HD;
@@ -230,13 +232,17 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
   int8_t q8a = 0, q8b = 0;
   float qsa = 0.0f;
   if (a.fuse_heads) {
-    fused_load<QPW>(a, kvh, qh0, wave, lane, fr);
+    fused_load<QPW>(a, kvh, qh0, wave, lane, kv_writer, fr);
   } else if (wave < QPW) {
     const int qh = qh0 + wave;
     q8a = q8_row[qh * HD + lane];
     q8b = q8_row[qh * HD + lane + 64];
     qsa = qs_row[qh * a.qs_col];
   }
+  // the exp table too, so that filling LDS from it does not wait for the
+  // K/V loads issued next
+  uint64_t tabv = 0;
+  if (tid < 32) tabv = kExp2Tab[tid];
 
   for (int b0 = 0; b0 < nblocks; b0 += CB) {
     const int nb = min(CB, nblocks - b0);
@@ -281,7 +287,7 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
     }
     if (b0 == 0) {
       // ---- prologue (overlaps the loads above) ----
-      if (tid < 32) sm.tab[tid] = kExp2Tab[tid];
+      if (tid < 32) sm.tab[tid] = tabv;
       if (tid < QPW) sm.run[tid] = -3.402823466e38f;
       if (a.fuse_heads) {
         fused_compute<QPW>(a, sm, fr, kvh, qh0, kv_writer, wave, lane);
@@ -329,7 +335,7 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
         int acc = 0;
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc = sdot4(qv[h][e], kw[i][e], acc);
-        acc += __shfl_xor(acc, 1);  // exact int32: both halves of the key
+        acc += lane_xor<1>(acc);  // exact int32: both halves of the key
         float s = -INFINITY;
         if (valid) {
           s = __fmul_rn(static_cast<float>(acc), kscale[i]);
@@ -370,7 +376,7 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
         const bool hok = h < QPW;
         float p = 0.0f, pv = 0.0f;
         if (hok && valid) {
-          p = exp_f32_tab(__fsub_rn(sm.s[h][jb * 32 + c], sm.nmm[h][jb]), sm.tab);
+          p = exp_f32_le0_tab(__fsub_rn(sm.s[h][jb * 32 + c], sm.nmm[h][jb]), sm.tab);
           pv = __fmul_rn(p, vscale[i]);
         }
         const float psum = tree_sum32(p);
@@ -378,16 +384,16 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
         const int p8 = hok ? quant1(pv, pm) : 0;
         if (hok && c == 0) {
           sm.psum[h][jb] = psum;
-          sm.corr[h][jb] = exp_f32_tab(__fsub_rn(sm.prev[h][jb], sm.nmm[h][jb]), sm.tab);
+          sm.corr[h][jb] = exp_f32_le0_tab(__fsub_rn(sm.prev[h][jb], sm.nmm[h][jb]), sm.tab);
         }
         int acc[2][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
         pv_dot<(QPW > 1 ? 2 : 1)>(vw[i], p8, lane, reinterpret_cast<int(&)[(QPW > 1 ? 2 : 1)][4]>(acc));
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) acc[s2][e] += __shfl_xor(acc[s2][e], 32);
+          for (int e = 0; e < 4; ++e) acc[s2][e] += lane_xor<32>(acc[s2][e]);
         // lanes 0..31 own the result; pmax of head hp+s2 lives in lane 32*s2
-        const float pm0 = __shfl(pm, 0), pm1 = __shfl(pm, 32);
+        const float pm0 = lane_bcast<0>(pm), pm1 = lane_bcast<32>(pm);
         if (lane < 32) {
 #pragma unroll
           for (int s2 = 0; s2 < 2; ++s2) {

@@ -50,12 +50,6 @@ __device__ __forceinline__ float key_value(uint32_t k) {
   return bits_f32(b);
 }
 
-__device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v, int m) {
-  const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), m);
-  const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), m);
-  return (static_cast<unsigned long long>(hi) << 32) | lo;
-}
-
 // Row destination of the int8 head output (dense view or paged KV slot).
 __device__ __forceinline__ void qdest_row(const QDest &d, int m, int head,
                                           int8_t **row8, float **scale) {
@@ -195,7 +189,7 @@ __global__ void __launch_bounds__(256) gemm_group_kernel(GemmArgs a) {
         best = other > best ? other : best;
 #pragma unroll
         for (int s = 1; s < 64; s <<= 1) {
-          const unsigned long long o = shfl_xor_u64(best, s);
+          const unsigned long long o = lane_xor_u64(best, s);
           best = o > best ? o : best;
         }
         if (lane == 0) a.keys[static_cast<int64_t>(m) * a.keys_ld + blockIdx.x] = best;
@@ -247,8 +241,9 @@ __global__ void __launch_bounds__(256) argmax_finish_kernel(const unsigned long 
     const unsigned long long k = keys[static_cast<int64_t>(m) * keys_ld + i];
     key = k > key ? k : key;
   }
+#pragma unroll
   for (int s = 1; s < 64; s <<= 1) {
-    const unsigned long long o = shfl_xor_u64(key, s);
+    const unsigned long long o = lane_xor_u64(key, s);
     key = o > key ? o : key;
   }
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = key;
@@ -312,9 +307,10 @@ __global__ void __launch_bounds__(64) argmax_logits_kernel(const float *logits, 
     }
   }
   // wave reduction of (best, best_idx); lanes without blocks hold key 0
+#pragma unroll
   for (int s = 1; s < 64; s <<= 1) {
-    const unsigned long long o = shfl_xor_u64(best, s);
-    const int oi = __shfl_xor(best_idx, s);
+    const unsigned long long o = lane_xor_u64(best, s);
+    const int oi = static_cast<int>(lane_xor_m(static_cast<uint32_t>(best_idx), s));
     if (o > best) {
       best = o;
       best_idx = oi;

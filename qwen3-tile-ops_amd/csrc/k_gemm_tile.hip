@@ -34,32 +34,11 @@ namespace q3 {
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void *lds_void_ptr;
-
-__device__ __forceinline__ lds_void_ptr to_lds(const void *p) {
-  return reinterpret_cast<lds_void_ptr>(reinterpret_cast<uintptr_t>(p));
-}
-
 __device__ __forceinline__ v4i zero4() {
   v4i z = {0, 0, 0, 0};
   return z;
 }
 
-// s_waitcnt vmcnt(N), the other counters untouched (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
-// Workgroup barrier for the k-loop: LDS operations of this wave complete
-// (lgkmcnt), then s_barrier.  __syncthreads() would also wait for every
-// outstanding vector load (vmcnt(0)), i.e. for the copies of the next
-// k-steps that are meant to stay in flight; each wave instead waits for its
-// own copies of the current step with wait_vmcnt before this barrier.
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
 
 
 // ref_qwen3.py:194-200: e = exp(-g); e = e + 1; e = 1/e; out = (g * e) * u.

@@ -38,12 +38,6 @@ __device__ __forceinline__ v4i zero4() {
   return z;
 }
 
-__device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v, int m) {
-  const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), m);
-  const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), m);
-  return (static_cast<unsigned long long>(hi) << 32) | lo;
-}
-
 __device__ __forceinline__ uint32_t ordered_key(float v) {
   uint32_t b = f32_bits(v);
   if (b == 0x80000000u) b = 0u;
@@ -137,9 +131,9 @@ __device__ void pro_compute_row(const GemvArgs &a, int m, const ProRow<QW> &r, i
     for (int q = 0; q < QW; ++q) {
       float s = __fadd_rn(__fadd_rn(__fmul_rn(v[q][0], v[q][0]), __fmul_rn(v[q][1], v[q][1])),
                           __fadd_rn(__fmul_rn(v[q][2], v[q][2]), __fmul_rn(v[q][3], v[q][3])));
-      s = __fadd_rn(s, __shfl_xor(s, 1));
-      s = __fadd_rn(s, __shfl_xor(s, 2));
-      s = __fadd_rn(s, __shfl_xor(s, 4));
+      s = __fadd_rn(s, lane_xor<1>(s));
+      s = __fadd_rn(s, lane_xor<2>(s));
+      s = __fadd_rn(s, lane_xor<4>(s));
       if ((lane & 7) == 0) blk[(wave + 4 * q) * 8 + (lane >> 3)] = s;
     }
     __syncthreads();
@@ -304,7 +298,7 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
       // NB consecutive threads share a row when NB <= 64 (wave-aligned)
 #pragma unroll
       for (int s = 1; s < NB && s < 64; s <<= 1) {
-        const unsigned long long o = shfl_xor_u64(key, s);
+        const unsigned long long o = lane_xor_u64(key, s);
         key = o > key ? o : key;
       }
       if (m < M && j == 0) a.keys[static_cast<int64_t>(m) * a.keys_ld + blockIdx.x] = key;
@@ -460,7 +454,7 @@ __global__ void __launch_bounds__(256) gemv_stream_kernel(GemvArgs a, int ntiles
       unsigned long long key = best[kk];
 #pragma unroll
       for (int sft = 1; sft < 64; sft <<= 1) {
-        const unsigned long long o = shfl_xor_u64(key, sft);
+        const unsigned long long o = lane_xor_u64(key, sft);
         key = o > key ? o : key;
       }
       if (lane == 0) a.keys[static_cast<int64_t>(it / NB) * a.keys_ld + blockIdx.x] = key;

@@ -53,8 +53,8 @@ __global__ void __launch_bounds__(256) rows_kernel(RowArgs a) {
         if (a.mode == 2 && a.x_out) a.x_out[static_cast<int64_t>(row) * a.ldxo + c] = v;
       }
       const float bsum = tree_sum32(__fmul_rn(v, v));
-      const float b_lo = __shfl(bsum, 0);
-      const float b_hi = __shfl(bsum, 32);
+      const float b_lo = lane_bcast<0>(bsum);
+      const float b_hi = lane_bcast<32>(bsum);
       ss = __fadd_rn(ss, b_lo);
       if ((c0 >> 5) + 1 < nblk) ss = __fadd_rn(ss, b_hi);
     }
@@ -152,9 +152,9 @@ __global__ void __launch_bounds__(256) rows1024_kernel(RowArgs a) {
   if (a.mode != 0) {
     float s = __fadd_rn(__fadd_rn(__fmul_rn(v[0], v[0]), __fmul_rn(v[1], v[1])),
                         __fadd_rn(__fmul_rn(v[2], v[2]), __fmul_rn(v[3], v[3])));
-    s = __fadd_rn(s, __shfl_xor(s, 1));
-    s = __fadd_rn(s, __shfl_xor(s, 2));
-    s = __fadd_rn(s, __shfl_xor(s, 4));
+    s = __fadd_rn(s, lane_xor<1>(s));
+    s = __fadd_rn(s, lane_xor<2>(s));
+    s = __fadd_rn(s, lane_xor<4>(s));
     if ((t & 7) == 0) bsum[t >> 3] = s;
     __syncthreads();
     float ss = 0.0f;

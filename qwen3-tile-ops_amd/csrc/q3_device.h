@@ -33,6 +33,32 @@ __device__ __forceinline__ int wave_id() {
   return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
 }
 
+// ---- LDS staging ------------------------------------------------------
+// Generic pointer to an LDS object as the address-space-3 pointer that
+// __builtin_amdgcn_global_load_lds takes (through an integer so that the
+// host pass of the same source also compiles).
+typedef __attribute__((address_space(3))) void *lds_void_ptr;
+
+__device__ __forceinline__ lds_void_ptr to_lds(const void *p) {
+  return reinterpret_cast<lds_void_ptr>(reinterpret_cast<uintptr_t>(p));
+}
+
+// s_waitcnt vmcnt(N), the other counters untouched (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Workgroup barrier for pipelined loops: LDS operations of this wave
+// complete (lgkmcnt), then s_barrier.  __syncthreads() would also wait for
+// every outstanding vector load (vmcnt(0)), i.e. for the copies of later
+// steps that are meant to stay in flight; each wave instead waits for its
+// own copies of the current step with wait_vmcnt before this barrier.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 __device__ __forceinline__ float bits_f32(uint32_t u) { return __uint_as_float(u); }
 __device__ __forceinline__ uint32_t f32_bits(float f) { return __float_as_uint(f); }
 
@@ -49,23 +75,31 @@ __constant__ static const uint64_t kExp2Tab[32] = {
     0x3fef3720dcef9069ull, 0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full,
     0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
 
-// glibc-compatible exp2f (see the header comment).
-__device__ __forceinline__ float exp2f_glibc(float x) {
+// Special cases of exp2f (|x| >= 128, Inf, NaN) as selects over the result
+// of the main path, which is computed for every input: no branch, so
+// independent exp chains interleave.  For -150 < x <= -128 (subnormal
+// results) the main path's value is kept, as in glibc.
+__device__ __forceinline__ float exp2f_special(float x, float y) {
   const uint32_t ux = f32_bits(x);
   const uint32_t abstop = (ux >> 20) & 0x7ffu;
-  if (abstop >= (0x43000000u >> 20)) {  // |x| >= 128, Inf or NaN
-    if (ux == 0xff800000u) return 0.0f;
-    if (abstop >= (0x7f800000u >> 20)) return x + x;
-    if (x > 0.0f) return bits_f32(0x7f800000u);
-    if (x <= -150.0f) return 0.0f;
-  }
+  float sp = y;
+  sp = (x <= -150.0f) ? 0.0f : sp;
+  sp = (x > 0.0f) ? bits_f32(0x7f800000u) : sp;
+  sp = (abstop >= (0x7f800000u >> 20)) ? x + x : sp;
+  sp = (ux == 0xff800000u) ? 0.0f : sp;
+  return (abstop >= (0x43000000u >> 20)) ? sp : y;
+}
+
+// Main path of glibc's exp2f for a table entry read by `tab_at`.
+template <class TabAt>
+__device__ __forceinline__ float exp2f_glibc_main(float x, TabAt tab_at) {
   const double xd = static_cast<double>(x);
   const double shift = 0x1.8p+52 / 32;
   double kd = __dadd_rn(xd, shift);
   const uint64_t ki = static_cast<uint64_t>(__double_as_longlong(kd));
   kd = __dsub_rn(kd, shift);
   const double r = __dsub_rn(xd, kd);
-  uint64_t t = kExp2Tab[ki & 31u];
+  uint64_t t = tab_at(static_cast<uint32_t>(ki & 31u));
   t += ki << 47;
   const double s = __longlong_as_double(static_cast<long long>(t));
   const double z = __fma_rn(0x1.c6af84b912394p-5, r, 0x1.ebfce50fac4f3p-3);
@@ -74,6 +108,14 @@ __device__ __forceinline__ float exp2f_glibc(float x) {
   y = __fma_rn(z, r2, y);
   y = __dmul_rn(y, s);
   return __double2float_rn(y);
+}
+
+// glibc-compatible exp2f (see the header comment).  For |x| >= 128 the main
+// path's table index and exponent are meaningless but harmless (integer and
+// f64 arithmetic only); exp2f_special then picks the glibc result.
+__device__ __forceinline__ float exp2f_glibc(float x) {
+  const float y = exp2f_glibc_main(x, [](uint32_t i) { return kExp2Tab[i]; });
+  return exp2f_special(x, y);
 }
 
 // ref_qwen3.py:27-29.
@@ -85,33 +127,21 @@ __device__ __forceinline__ float exp_f32(float x) {
 // staged in LDS by the caller), so a latency-critical loop does not wait on
 // a global-memory table lookup per call.
 __device__ __forceinline__ float exp2f_glibc_tab(float x, const uint64_t *tab) {
-  const uint32_t ux = f32_bits(x);
-  const uint32_t abstop = (ux >> 20) & 0x7ffu;
-  if (abstop >= (0x43000000u >> 20)) {
-    if (ux == 0xff800000u) return 0.0f;
-    if (abstop >= (0x7f800000u >> 20)) return x + x;
-    if (x > 0.0f) return bits_f32(0x7f800000u);
-    if (x <= -150.0f) return 0.0f;
-  }
-  const double xd = static_cast<double>(x);
-  const double shift = 0x1.8p+52 / 32;
-  double kd = __dadd_rn(xd, shift);
-  const uint64_t ki = static_cast<uint64_t>(__double_as_longlong(kd));
-  kd = __dsub_rn(kd, shift);
-  const double r = __dsub_rn(xd, kd);
-  uint64_t t = tab[ki & 31u];
-  t += ki << 47;
-  const double s = __longlong_as_double(static_cast<long long>(t));
-  const double z = __fma_rn(0x1.c6af84b912394p-5, r, 0x1.ebfce50fac4f3p-3);
-  const double r2 = __dmul_rn(r, r);
-  double y = __fma_rn(0x1.62e42ff0c52d6p-1, r, 1.0);
-  y = __fma_rn(z, r2, y);
-  y = __dmul_rn(y, s);
-  return __double2float_rn(y);
+  const float y = exp2f_glibc_main(x, [tab](uint32_t i) { return tab[i]; });
+  return exp2f_special(x, y);
 }
 
 __device__ __forceinline__ float exp_f32_tab(float x, const uint64_t *tab) {
   return exp2f_glibc_tab(__fmul_rn(x, bits_f32(0x3FB8AA3Bu)), tab);
+}
+
+// exp_f32_tab for x <= 0 or x = -inf (softmax arguments s - max): of
+// exp2f's special cases only "x2 <= -150 -> +0" can occur (x2 = x*log2(e)
+// <= 0; -inf included); -150 < x2 < -128 takes the main path in glibc too.
+__device__ __forceinline__ float exp_f32_le0_tab(float x, const uint64_t *tab) {
+  const float x2 = __fmul_rn(x, bits_f32(0x3FB8AA3Bu));
+  const float y = exp2f_glibc_main(x2, [tab](uint32_t i) { return tab[i]; });
+  return (x2 <= -150.0f) ? 0.0f : y;
 }
 
 __device__ __forceinline__ float inv127() { return 1.0f / 127.0f; }
@@ -124,33 +154,121 @@ __device__ __forceinline__ int quant1(float x, float scale) {
   return static_cast<int>(r);
 }
 
+// ---- lane exchanges in VALU (no LDS round trip) -----------------------
+// lane_xor<M>(x): lane i receives x of lane i ^ M.  M = 1, 2: DPP quad_perm;
+// M = 4: quad_perm [3,2,1,0] then row_half_mirror (i -> (i ^ 3) ^ 7);
+// M = 8: DPP row_ror:8; M = 16, 32: v_permlane16_swap / v_permlane32_swap,
+// which return the register with its odd/even 16- (32-) lane halves
+// exchanged, split over two results: a lane in an odd half finds its
+// partner in the first result, a lane in an even half in the second.
+// Every lane gets exactly its partner's value, as with ds_swizzle /
+// ds_bpermute, so reductions built on it add the same operands in the same
+// order.  The DPP controls used read no lane outside its row, so bound_ctrl
+// changes no value; it is set so that the compiler can fold the move into
+// the instruction that uses it.
+template <int M>
+__device__ __forceinline__ uint32_t lane_xor(uint32_t x) {
+  const int v = static_cast<int>(x);
+  if constexpr (M == 1) {
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(v, 0xB1, 0xf, 0xf, true));
+  } else if constexpr (M == 2) {
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(v, 0x4E, 0xf, 0xf, true));
+  } else if constexpr (M == 4) {
+    const int t = __builtin_amdgcn_mov_dpp(v, 0x1B, 0xf, 0xf, true);
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(t, 0x141, 0xf, 0xf, true));
+  } else if constexpr (M == 8) {
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(v, 0x128, 0xf, 0xf, true));
+  } else if constexpr (M == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return (__lane_id() & 16) ? r[0] : r[1];
+  } else {
+    static_assert(M == 32, "lane_xor: M is a power of two below 64");
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return (__lane_id() & 32) ? r[0] : r[1];
+  }
+}
+
+template <int M>
+__device__ __forceinline__ float lane_xor(float x) {
+  return __uint_as_float(lane_xor<M>(__float_as_uint(x)));
+}
+
+template <int M>
+__device__ __forceinline__ int lane_xor(int x) {
+  return static_cast<int>(lane_xor<M>(static_cast<uint32_t>(x)));
+}
+
+// Same with the distance as a value; every call site sits in a fully
+// unrolled loop, so m is a constant there and one case remains.
+__device__ __forceinline__ uint32_t lane_xor_m(uint32_t x, int m) {
+  switch (m) {
+    case 1: return lane_xor<1>(x);
+    case 2: return lane_xor<2>(x);
+    case 4: return lane_xor<4>(x);
+    case 8: return lane_xor<8>(x);
+    case 16: return lane_xor<16>(x);
+    case 32: return lane_xor<32>(x);
+    default: return static_cast<uint32_t>(__shfl_xor(static_cast<int>(x), m));
+  }
+}
+
+__device__ __forceinline__ unsigned long long lane_xor_u64(unsigned long long v, int m) {
+  const uint32_t lo = lane_xor_m(static_cast<uint32_t>(v), m);
+  const uint32_t hi = lane_xor_m(static_cast<uint32_t>(v >> 32), m);
+  return (static_cast<unsigned long long>(hi) << 32) | lo;
+}
+
+// {x_i, x_(i^16)} (resp. i^32) at every lane i, in an order that depends on
+// the lane: for a commutative combine (f32 add, max, integer add) the result
+// equals combine(x, lane_xor<16>(x)) bit for bit, without the select.
+struct LanePair {
+  uint32_t a, b;
+};
+
+__device__ __forceinline__ LanePair lane_pair16(uint32_t x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+  return {r[0], r[1]};
+}
+
+__device__ __forceinline__ LanePair lane_pair32(uint32_t x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  return {r[0], r[1]};
+}
+
+// Value of lane L (a constant) in every lane.
+template <int L>
+__device__ __forceinline__ float lane_bcast(float x) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), L));
+}
+
 // ---- wave reductions --------------------------------------------------
 // Pairwise tree over 32 consecutive lanes: level k adds lanes i and i^2^k.
 // For 32 leaves this is exactly ref_qwen3.py:41-50's tree (pairs (0,1),
 // (2,3), ...); for n < 32 leaves padded with +0.0 it equals the reference's
 // carry-the-odd-element tree because a carried node only ever meets +0.0.
 __device__ __forceinline__ float tree_sum32(float v) {
-  v = __fadd_rn(v, __shfl_xor(v, 1));
-  v = __fadd_rn(v, __shfl_xor(v, 2));
-  v = __fadd_rn(v, __shfl_xor(v, 4));
-  v = __fadd_rn(v, __shfl_xor(v, 8));
-  v = __fadd_rn(v, __shfl_xor(v, 16));
-  return v;
+  v = __fadd_rn(v, lane_xor<1>(v));
+  v = __fadd_rn(v, lane_xor<2>(v));
+  v = __fadd_rn(v, lane_xor<4>(v));
+  v = __fadd_rn(v, lane_xor<8>(v));
+  const LanePair p = lane_pair16(__float_as_uint(v));
+  return __fadd_rn(__uint_as_float(p.a), __uint_as_float(p.b));
 }
 
 // max is exact in any order (NaN-free inputs).
 __device__ __forceinline__ float max32(float v) {
-  v = fmaxf(v, __shfl_xor(v, 1));
-  v = fmaxf(v, __shfl_xor(v, 2));
-  v = fmaxf(v, __shfl_xor(v, 4));
-  v = fmaxf(v, __shfl_xor(v, 8));
-  v = fmaxf(v, __shfl_xor(v, 16));
-  return v;
+  v = fmaxf(v, lane_xor<1>(v));
+  v = fmaxf(v, lane_xor<2>(v));
+  v = fmaxf(v, lane_xor<4>(v));
+  v = fmaxf(v, lane_xor<8>(v));
+  const LanePair p = lane_pair16(__float_as_uint(v));
+  return fmaxf(__uint_as_float(p.a), __uint_as_float(p.b));
 }
 
 __device__ __forceinline__ float max64(float v) {
   v = max32(v);
-  return fmaxf(v, __shfl_xor(v, 32));
+  const LanePair p = lane_pair32(__float_as_uint(v));
+  return fmaxf(__uint_as_float(p.a), __uint_as_float(p.b));
 }
 
 // RMSNorm factor from the ordered 32-column block sums (ref_qwen3.py:161-170):
@@ -179,10 +297,10 @@ __device__ __forceinline__ void head_norm_rope_regs(float &t0, float &t1, float 
   const float sa = tree_sum32(__fmul_rn(t0, t0));
   const float sb = tree_sum32(__fmul_rn(t1, t1));
   float ss = 0.0f;
-  ss = __fadd_rn(ss, __shfl(sa, 0));
-  ss = __fadd_rn(ss, __shfl(sa, 32));
-  ss = __fadd_rn(ss, __shfl(sb, 0));
-  ss = __fadd_rn(ss, __shfl(sb, 32));
+  ss = __fadd_rn(ss, lane_bcast<0>(sa));
+  ss = __fadd_rn(ss, lane_bcast<32>(sa));
+  ss = __fadd_rn(ss, lane_bcast<0>(sb));
+  ss = __fadd_rn(ss, lane_bcast<32>(sb));
   const float rinv = rms_factor(ss, inv_hd);
   const float y0 = __fmul_rn(__fmul_rn(t0, rinv), w0);
   const float y1 = __fmul_rn(__fmul_rn(t1, rinv), w1);
