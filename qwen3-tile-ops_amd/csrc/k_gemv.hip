@@ -201,14 +201,20 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
   __shared__ uint64_t exptab[32];
   constexpr int QW = GPW * KSTEPS / 4;  // 256-column groups per wave
 
-  // row 0's prologue operands, then the weight stream (see ProRow)
+  // row 0's prologue operands and the exp table, then the weight stream
+  // (see ProRow).  The weight loads are unconditional (a wave past the last
+  // group reloads that group and never uses it): vector loads complete in
+  // order, and with a fixed count after the prologue operands the compiler
+  // waits for those operands alone (vmcnt(#weight loads)) instead of for
+  // everything.
   ProRow<QW> r0;
   if (a.pro != PRO_NONE) pro_load_row<QW>(a, 0, r0);
+  uint64_t tabv = 0;
+  if (NMAT == 2 && threadIdx.x < 32) tabv = kExp2Tab[threadIdx.x];
   v4i bv[NMAT][NT][GPW][KSTEPS];
 #pragma unroll
   for (int gi = 0; gi < GPW; ++gi) {
-    const int g = wave + 4 * gi;
-    const bool ok = g < ngroups;
+    const int g = min(wave + 4 * gi, ngroups - 1);
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) {
       const int k = g * G + ks * 64 + lg * 16;
@@ -218,11 +224,11 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
         for (int nt = 0; nt < NT; ++nt) {
           const int8_t *b = (mi == 0 ? sg.b : sg.b2) +
                             static_cast<int64_t>(n_blk - sg.n0 + nt * 16 + lr) * K;
-          bv[mi][nt][gi][ks] = ok ? *reinterpret_cast<const v4i *>(b + k) : zero4();
+          bv[mi][nt][gi][ks] = *reinterpret_cast<const v4i *>(b + k);
         }
     }
   }
-  if (NMAT == 2 && threadIdx.x < 32) exptab[threadIdx.x] = kExp2Tab[threadIdx.x];
+  if (NMAT == 2 && threadIdx.x < 32) exptab[threadIdx.x] = tabv;
 
   const int8_t *arow;
   const float *as;
@@ -347,7 +353,12 @@ __global__ void __launch_bounds__(256) gemv_stream_kernel(GemvArgs a, int ntiles
   ProRow<QW> r0;
   if (a.pro != PRO_NONE) pro_load_row<QW>(a, 0, r0);
 
-  auto load_tile = [&](v4i (&bv)[NT][GPW][KSTEPS], int t) {
+  // a tile's column scales, then its weights: issued together one tile
+  // ahead, so that using tile t waits only for loads issued before tile
+  // t + 1's (vector loads complete in order)
+  auto load_tile = [&](v4i (&bv)[NT][GPW][KSTEPS], float (&bsv)[NT], int t) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) bsv[nt] = sg.bs[t * NB + nt * 16 + lr];
 #pragma unroll
     for (int gi = 0; gi < GPW; ++gi) {
       const int g = min(wave + 4 * gi, ngroups - 1);
@@ -362,13 +373,31 @@ __global__ void __launch_bounds__(256) gemv_stream_kernel(GemvArgs a, int ntiles
       }
     }
   };
+  // A operand rows and scales of the unfused path are loaded before the
+  // first tile (so that waiting for them does not wait for the tile)
+  v4i av[GPW][KSTEPS];
+  float asv[GPW][4];
+  if (a.pro == PRO_NONE) {
+    const int8_t *arow = a.a + static_cast<int64_t>(lr < M ? lr : 0) * a.lda + lg * 16;
+#pragma unroll
+    for (int gi = 0; gi < GPW; ++gi) {
+      const int g = min(wave + 4 * gi, ngroups - 1);
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks)
+        av[gi][ks] = lr < M ? *reinterpret_cast<const v4i *>(arow + g * G + ks * 64) : zero4();
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = lg * 4 + i;
+        asv[gi][i] = m < M ? a.as[static_cast<int64_t>(m) * a.ldas + g] : 0.0f;
+      }
+    }
+  }
+  const int step = static_cast<int>(gridDim.x);
   int t = blockIdx.x;
-  v4i bv[NT][GPW][KSTEPS];
-  load_tile(bv, t);
+  v4i b0[NT][GPW][KSTEPS], b1[NT][GPW][KSTEPS];
+  float s0[NT], s1[NT];
+  load_tile(b0, s0, t);
 
-  const int8_t *arow;
-  const float *as;
-  int64_t ldas;
   if (a.pro != PRO_NONE) {
     pro_compute_row<QW>(a, 0, r0, a_lds, as_lds, blk);
     for (int m = 1; m < M; ++m) {
@@ -376,33 +405,24 @@ __global__ void __launch_bounds__(256) gemv_stream_kernel(GemvArgs a, int ntiles
       pro_load_row<QW>(a, m, r);
       pro_compute_row<QW>(a, m, r, a_lds, as_lds, blk);
     }
-    arow = a_lds + (lr < M ? lr : 0) * K + lg * 16;
-    as = as_lds;
-    ldas = K / 256;
-  } else {
-    arow = a.a + static_cast<int64_t>(lr < M ? lr : 0) * a.lda + lg * 16;
-    as = a.as;
-    ldas = a.ldas;
-  }
-  v4i av[GPW][KSTEPS];
-  float asv[GPW][4];
+    const int8_t *arow = a_lds + (lr < M ? lr : 0) * K + lg * 16;
 #pragma unroll
-  for (int gi = 0; gi < GPW; ++gi) {
-    const int g = wave + 4 * gi;
+    for (int gi = 0; gi < GPW; ++gi) {
+      const int g = wave + 4 * gi;
 #pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks)
-      av[gi][ks] = (g < ngroups && lr < M) ? *reinterpret_cast<const v4i *>(arow + g * G + ks * 64) : zero4();
+      for (int ks = 0; ks < KSTEPS; ++ks)
+        av[gi][ks] = (g < ngroups && lr < M) ? *reinterpret_cast<const v4i *>(arow + g * G + ks * 64) : zero4();
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = lg * 4 + i;
-      asv[gi][i] = (g < ngroups && m < M) ? as[static_cast<int64_t>(m) * ldas + g] : 0.0f;
+      for (int i = 0; i < 4; ++i) {
+        const int m = lg * 4 + i;
+        asv[gi][i] = (g < ngroups && m < M) ? as_lds[m * (K / 256) + g] : 0.0f;
+      }
     }
   }
 
   unsigned long long best[4] = {0ull, 0ull, 0ull, 0ull};  // items tid + 256 k
-  for (; t < ntiles; t += gridDim.x) {
-    v4i bn[NT][GPW][KSTEPS];
-    load_tile(bn, min(t + static_cast<int>(gridDim.x), ntiles - 1));
+  // one tile: MFMAs, per-group dequant into LDS, ordered group sums
+  auto tile = [&](const v4i (&bv)[NT][GPW][KSTEPS], const float (&bsv)[NT], int tt) {
 #pragma unroll
     for (int gi = 0; gi < GPW; ++gi) {
       const int g = wave + 4 * gi;
@@ -413,11 +433,10 @@ __global__ void __launch_bounds__(256) gemv_stream_kernel(GemvArgs a, int ntiles
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks)
           acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[gi][ks], bv[nt][gi][ks], acc, 0, 0, 0);
-        const float bsv = sg.bs[t * NB + nt * 16 + lr];
         float *pt = part + (g * 16) * PP + nt * 16 + lr;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          pt[(lg * 4 + i) * PP] = __fmul_rn(__fmul_rn(static_cast<float>(acc[i]), bsv), asv[gi][i]);
+          pt[(lg * 4 + i) * PP] = __fmul_rn(__fmul_rn(static_cast<float>(acc[i]), bsv[nt]), asv[gi][i]);
       }
     }
     __syncthreads();
@@ -429,7 +448,7 @@ __global__ void __launch_bounds__(256) gemv_stream_kernel(GemvArgs a, int ntiles
       const int j = it % NB;
       float out = 0.0f;
       for (int g = 0; g < ngroups; ++g) out = __fadd_rn(out, part[(g * 16 + m) * PP + j]);
-      const int ncol = t * NB + j;
+      const int ncol = tt * NB + j;
       if (sg.epi == EPI_ARGMAX) {
         const unsigned long long key = (static_cast<unsigned long long>(ordered_key(out)) << 32) |
                                        (0xFFFFFFFFu - static_cast<uint32_t>(ncol));
@@ -439,12 +458,17 @@ __global__ void __launch_bounds__(256) gemv_stream_kernel(GemvArgs a, int ntiles
       }
     }
     __syncthreads();  // part is rewritten by the next tile
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-      for (int gi = 0; gi < GPW; ++gi)
-#pragma unroll
-        for (int ks = 0; ks < KSTEPS; ++ks) bv[nt][gi][ks] = bn[nt][gi][ks];
+  };
+  // two register sets in turn, the next tile's loads in flight during each
+  // tile (no register copy between tiles, which would wait for them)
+  while (t < ntiles) {
+    load_tile(b1, s1, min(t + step, ntiles - 1));
+    tile(b0, s0, t);
+    t += step;
+    if (t >= ntiles) break;
+    load_tile(b0, s0, min(t + step, ntiles - 1));
+    tile(b1, s1, t);
+    t += step;
   }
   if (sg.epi == EPI_ARGMAX) {
 #pragma unroll
