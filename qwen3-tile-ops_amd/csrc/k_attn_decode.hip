@@ -247,18 +247,25 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
   for (int b0 = 0; b0 < nblocks; b0 += CB) {
     const int nb = min(CB, nblocks - b0);
     // ---- issue every load of this chunk ----
+    // Page ids first, then K, V and scales with no condition around any load
+    // (a block past the chunk reloads the last block, a key past kv_end the
+    // last key of its block): vector loads complete in order, and with a
+    // fixed count the compiler waits for exactly the loads a use needs
+    // instead of for all of them.  The duplicates are never used: phase 1
+    // masks keys >= kv_end to -inf, so their P, P8 and P8.V terms are 0.
+    uint32_t pgs[BPW];
+#pragma unroll
+    for (int i = 0; i < BPW; ++i) {
+      const int jblk = min(b0 + wave + NW * i, nblocks - 1);
+      pgs[i] = table[static_cast<uint32_t>(jblk * 32) / a.page_tokens];
+    }
     int kw[BPW][16], vw[BPW][16];
     float kscale[BPW], vscale[BPW];
 #pragma unroll
     for (int i = 0; i < BPW; ++i) {
-      const int jb = wave + NW * i;
-      kscale[i] = 0.0f;
-      vscale[i] = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) kw[i][e] = vw[i][e] = 0;
-      if (jb >= nb) continue;
-      const int j = (b0 + jb) * 32;
-      const uint32_t page = table[static_cast<uint32_t>(j) / a.page_tokens];
+      const int j = min(b0 + wave + NW * i, nblocks - 1) * 32;
+      const int last = kv_end - 1 - j;  // >= 0: the block holds key kv_end - 1 or is full
+      const uint32_t page = pgs[i];
       const uint32_t slot0 = static_cast<uint32_t>(j) % a.page_tokens;
       const int8_t *kb = a.k + page * a.page_bytes + slot0 * a.row_bytes + kvh * HD;
       const int8_t *vb = a.v + page * a.page_bytes + slot0 * a.row_bytes + kvh * HD;
@@ -266,24 +273,21 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
                           slot0 * a.scale_row_bytes;
       const int8_t *vsb = reinterpret_cast<const int8_t *>(a.vs) + page * a.scale_page_bytes +
                           slot0 * a.scale_row_bytes;
-      if (j + kc < kv_end) {
-        const int4 *kp = reinterpret_cast<const int4 *>(kb + kc * a.row_bytes + half * 64);
+      const int kr = min(kc, last);
+      const int4 *kp = reinterpret_cast<const int4 *>(kb + kr * a.row_bytes + half * 64);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int4 v = kp[e];
-          kw[i][4 * e] = v.x;
-          kw[i][4 * e + 1] = v.y;
-          kw[i][4 * e + 2] = v.z;
-          kw[i][4 * e + 3] = v.w;
-        }
-        kscale[i] = reinterpret_cast<const float *>(ksb + kc * a.scale_row_bytes)[kvh];
+      for (int e = 0; e < 4; ++e) {
+        const int4 v = kp[e];
+        kw[i][4 * e] = v.x;
+        kw[i][4 * e + 1] = v.y;
+        kw[i][4 * e + 2] = v.z;
+        kw[i][4 * e + 3] = v.w;
       }
+      kscale[i] = reinterpret_cast<const float *>(ksb + kr * a.scale_row_bytes)[kvh];
 #pragma unroll
       for (int cc = 0; cc < 16; ++cc)
-        if (j + kh + cc < kv_end)
-          vw[i][cc] = *reinterpret_cast<const int *>(vb + (kh + cc) * a.row_bytes + d0);
-      if (j + (lane & 31) < kv_end)
-        vscale[i] = reinterpret_cast<const float *>(vsb + (lane & 31) * a.scale_row_bytes)[kvh];
+        vw[i][cc] = *reinterpret_cast<const int *>(vb + min(kh + cc, last) * a.row_bytes + d0);
+      vscale[i] = reinterpret_cast<const float *>(vsb + min(lane & 31, last) * a.scale_row_bytes)[kvh];
     }
     if (b0 == 0) {
       // ---- prologue (overlaps the loads above) ----

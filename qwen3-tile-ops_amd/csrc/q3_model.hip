@@ -59,7 +59,7 @@ struct q3_model {
   double kt_ms[Q3_KT_COUNT] = {};              // folded totals
   uint32_t kt_n[Q3_KT_COUNT] = {};
   // decode: workgroups that prefetch the next kernels' weights during the
-  // attention kernel (Q3_DECODE_PREFETCH_WGS, default 64; 0 disables)
+  // attention kernel (Q3_DECODE_PREFETCH_WGS, default 128; 0 disables)
   int pf_wgs;
 };
 
@@ -793,7 +793,7 @@ extern "C" int q3_model_open(void *blob, const q3_layout *lay, void *stream, q3_
   m->stream = static_cast<hipStream_t>(stream);
   m->n_pages = lay->max_seq / kPageTokens;
   m->keys_ld = lay->vocab / 16 + 64;  // one key per lm_head column block
-  m->pf_wgs = 64;
+  m->pf_wgs = 128;
   if (const char *e = std::getenv("Q3_DECODE_PREFETCH_WGS")) m->pf_wgs = std::max(0, std::atoi(e));
   m->bkeys_ld = lay->vocab / 128 + 64;  // one key per 128-column block of the lm GEMM
   m->btab_off = (sizeof(int32_t) * lay->seq + 255) & ~size_t(255);
