@@ -32,6 +32,8 @@
 // K/V page slot of position kv_len - 1 (one workgroup per KV head) and the Q
 // int8 row for the record, and keep copies in LDS that the attention uses in
 // place of the global K/V of that position.
+#include <type_traits>
+
 #include "q3_device.h"
 #include "q3_kernels.h"
 
@@ -104,22 +106,23 @@ struct FusedRegs {
   uint32_t page;  // K/V waves of the writing workgroup: page of the new token
 };
 
-// wave 0: K head kvh, wave 1: V head kvh, waves 2..: query heads qh0 + h
+// wave 0: K head kvh, wave 1: V head kvh, waves 2..: query heads qh0 + h.
+// Every wave issues the same seven loads (waves past the heads repeat wave
+// 0's, the V wave loads gains it does not use): with a fixed count the
+// compiler's waits after them stay exact.
 template <int QPW>
 __device__ __forceinline__ void fused_load(const AttnArgs &a, int kvh, int qh0, int wave, int lane,
-                                           bool kv_writer, FusedRegs &r) {
-  if (wave >= 2 + QPW) return;
-  if (wave < 2 && kv_writer) r.page = a.table[(a.kv_len - 1) / a.page_tokens];
-  const float *src = wave == 0 ? a.fk + kvh * HD : wave == 1 ? a.fv + kvh * HD : a.fq + (qh0 + wave - 2) * HD;
+                                           FusedRegs &r) {
+  const int w = wave < 2 + QPW ? wave : 0;
+  const float *src = w == 0 ? a.fk + kvh * HD : w == 1 ? a.fv + kvh * HD : a.fq + (qh0 + w - 2) * HD;
   r.t0 = src[lane];
   r.t1 = src[lane + 64];
-  if (wave != 1) {
-    const float *nw = wave == 0 ? a.nk : a.nq;
-    r.w0 = nw[lane];
-    r.w1 = nw[lane + 64];
-    r.c = a.cos_row[lane];
-    r.s = a.sin_row[lane];
-  }
+  const float *nw = w == 0 ? a.nk : a.nq;
+  r.w0 = nw[lane];
+  r.w1 = nw[lane + 64];
+  r.c = a.cos_row[lane];
+  r.s = a.sin_row[lane];
+  r.page = a.table[(a.kv_len - 1) / a.page_tokens];
 }
 
 template <int QPW, class SM>
@@ -187,7 +190,10 @@ __device__ void prefetch_ranges(const AttnArgs &a, int w) {
   }
 }
 
-template <int QPW, int NW, int BPW>
+// FUSE: the head epilogues run in the prologue (a.fuse_heads); a template
+// parameter rather than a branch so that both variants issue a fixed number
+// of loads.
+template <int QPW, int NW, int BPW, bool FUSE>
 __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
   constexpr int CB = NW * BPW;
   __shared__ __align__(16) Smem<QPW, CB> sm;
@@ -227,24 +233,52 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
   int qv[QPW][16];
   float qscale[QPW];
 
-  // prologue operands first
+  // The exp table into LDS from immediates (no load to wait for; first
+  // read in phase 3, after barriers), the first chunk's page ids, then the
+  // prologue operands.
+  if (tid == 0) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) sm.tab[i] = kExp2Tab[i];
+  }
+  uint32_t pgs0[BPW];
+#pragma unroll
+  for (int i = 0; i < BPW; ++i) {
+    const int jblk = min(wave + NW * i, nblocks - 1);
+    pgs0[i] = table[static_cast<uint32_t>(jblk * 32) / a.page_tokens];
+  }
   FusedRegs fr{};
   int8_t q8a = 0, q8b = 0;
   float qsa = 0.0f;
-  if (a.fuse_heads) {
-    fused_load<QPW>(a, kvh, qh0, wave, lane, kv_writer, fr);
-  } else if (wave < QPW) {
-    const int qh = qh0 + wave;
+  if constexpr (FUSE) {
+    fused_load<QPW>(a, kvh, qh0, wave, lane, fr);
+  } else {
+    const int qh = qh0 + min(wave, QPW - 1);  // every wave loads (fixed count)
     q8a = q8_row[qh * HD + lane];
     q8b = q8_row[qh * HD + lane + 64];
     qsa = qs_row[qh * a.qs_col];
   }
-  // the exp table too, so that filling LDS from it does not wait for the
-  // K/V loads issued next
-  uint64_t tabv = 0;
-  if (tid < 32) tabv = kExp2Tab[tid];
+  // keep this issue order (page ids, prologue operands, then the chunk's
+  // K/V): the scheduler would otherwise wait for the page ids first
+  __builtin_amdgcn_sched_barrier(0);
 
-  for (int b0 = 0; b0 < nblocks; b0 += CB) {
+  // page ids of this wave's blocks in chunk b0 (for the first chunk they are
+  // issued before the prologue operands, above)
+  uint32_t pgs[BPW];
+#pragma unroll
+  for (int i = 0; i < BPW; ++i) pgs[i] = pgs0[i];
+  auto load_pages = [&](int b0) {
+#pragma unroll
+    for (int i = 0; i < BPW; ++i) {
+      const int jblk = min(b0 + wave + NW * i, nblocks - 1);
+      pgs[i] = table[static_cast<uint32_t>(jblk * 32) / a.page_tokens];
+    }
+  };
+
+  // One chunk of up to CB blocks.  The first chunk is a separate instance
+  // (FIRST) so that the prologue's arithmetic stays between the chunk's load
+  // issues instead of being hoisted in front of all of them.
+  auto chunk = [&](const int b0, auto first_tag) {
+    constexpr bool FIRST = decltype(first_tag)::value;
     const int nb = min(CB, nblocks - b0);
     // ---- issue every load of this chunk ----
     // Page ids first, then K, V and scales with no condition around any load
@@ -253,16 +287,10 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
     // fixed count the compiler waits for exactly the loads a use needs
     // instead of for all of them.  The duplicates are never used: phase 1
     // masks keys >= kv_end to -inf, so their P, P8 and P8.V terms are 0.
-    uint32_t pgs[BPW];
-#pragma unroll
-    for (int i = 0; i < BPW; ++i) {
-      const int jblk = min(b0 + wave + NW * i, nblocks - 1);
-      pgs[i] = table[static_cast<uint32_t>(jblk * 32) / a.page_tokens];
-    }
+    if constexpr (!FIRST) load_pages(b0);
     int kw[BPW][16], vw[BPW][16];
     float kscale[BPW], vscale[BPW];
-#pragma unroll
-    for (int i = 0; i < BPW; ++i) {
+    auto issue_block = [&](int i) {
       const int j = min(b0 + wave + NW * i, nblocks - 1) * 32;
       const int last = kv_end - 1 - j;  // >= 0: the block holds key kv_end - 1 or is full
       const uint32_t page = pgs[i];
@@ -288,12 +316,17 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
       for (int cc = 0; cc < 16; ++cc)
         vw[i][cc] = *reinterpret_cast<const int *>(vb + min(kh + cc, last) * a.row_bytes + d0);
       vscale[i] = reinterpret_cast<const float *>(vsb + min(lane & 31, last) * a.scale_row_bytes)[kvh];
-    }
-    if (b0 == 0) {
+    };
+    // 22 loads per block: the last block is issued after the prologue, so
+    // that the prologue does not stall on a full load counter (vmcnt holds
+    // 63) waiting for the first block's data
+#pragma unroll
+    for (int i = 0; i < BPW - 1; ++i) issue_block(i);
+    if constexpr (FIRST) __builtin_amdgcn_sched_barrier(0);
+    if constexpr (FIRST) {
       // ---- prologue (overlaps the loads above) ----
-      if (tid < 32) sm.tab[tid] = tabv;
       if (tid < QPW) sm.run[tid] = -3.402823466e38f;
-      if (a.fuse_heads) {
+      if constexpr (FUSE) {
         fused_compute<QPW>(a, sm, fr, kvh, qh0, kv_writer, wave, lane);
       } else if (wave < QPW) {
         sm.q8[wave][lane] = q8a;
@@ -309,8 +342,9 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
         qscale[h] = sm.qs[h];
       }
     }
+    issue_block(BPW - 1);
     // the new token (position kv_len - 1) comes from the prologue's LDS copy
-    if (a.fuse_heads) {
+    if constexpr (FUSE) {
 #pragma unroll
       for (int i = 0; i < BPW; ++i) {
         const int j = (b0 + wave + NW * i) * 32;
@@ -425,7 +459,10 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
       }
     }
     __syncthreads();
-  }
+  };
+  chunk(0, std::true_type{});
+  for (int b0 = CB; b0 < nblocks; b0 += CB) chunk(b0, std::false_type{});
+
 
   // ---- epilogue: out = res * (1/den); per-head int8 quant (522-546) ----
   float out = 0.0f;
@@ -453,7 +490,10 @@ hipError_t launch_decode(const AttnArgs &a, hipStream_t s) {
   static_assert(QPW * HD <= NW * 64, "phase 4 needs a thread per (head, dim)");
   const int extra = a.pf_n > 0 ? a.pf_wgs : 0;
   const int seqs = a.row_pos ? a.rows : 1;
-  Q3_LAUNCH((attn_decode_kernel<QPW, NW, BPW>), dim3(a.heads / QPW + extra, seqs), dim3(NW * 64), 0, s, a);
+  if (a.fuse_heads)
+    Q3_LAUNCH((attn_decode_kernel<QPW, NW, BPW, true>), dim3(a.heads / QPW + extra, seqs), dim3(NW * 64), 0, s, a);
+  else
+    Q3_LAUNCH((attn_decode_kernel<QPW, NW, BPW, false>), dim3(a.heads / QPW + extra, seqs), dim3(NW * 64), 0, s, a);
   return hipGetLastError();
 }
 
