@@ -209,8 +209,35 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
   // everything.
   ProRow<QW> r0;
   if (a.pro != PRO_NONE) pro_load_row<QW>(a, 0, r0);
+  // A operand rows and scales of the unfused path, also before the weights
+  const bool avalid = lr < M;
+  v4i av[GPW][KSTEPS];
+  float asv[GPW][4];
+  if (a.pro == PRO_NONE) {
+    const int8_t *arow = a.a + static_cast<int64_t>(avalid ? lr : 0) * a.lda + lg * 16;
+#pragma unroll
+    for (int gi = 0; gi < GPW; ++gi) {
+      const int g = min(wave + 4 * gi, ngroups - 1);
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks) {
+        const v4i v = *reinterpret_cast<const v4i *>(arow + g * G + ks * 64);
+        av[gi][ks] = avalid ? v : zero4();
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = min(lg * 4 + i, M - 1);
+        asv[gi][i] = a.as[static_cast<int64_t>(m) * a.ldas + g];
+      }
+    }
+  }
+  // the weight rows' scales, then the weights
+  float bsv[NMAT][NT];
+#pragma unroll
+  for (int mi = 0; mi < NMAT; ++mi)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) bsv[mi][nt] = (mi == 0 ? sg.bs : sg.bs2)[n_blk - sg.n0 + nt * 16 + lr];
   uint64_t tabv = 0;
-  if (NMAT == 2 && threadIdx.x < 32) tabv = kExp2Tab[threadIdx.x];
+  if (NMAT == 2) tabv = kExp2Tab[threadIdx.x & 31];
   v4i bv[NMAT][NT][GPW][KSTEPS];
 #pragma unroll
   for (int gi = 0; gi < GPW; ++gi) {
@@ -230,9 +257,6 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
   }
   if (NMAT == 2 && threadIdx.x < 32) exptab[threadIdx.x] = tabv;
 
-  const int8_t *arow;
-  const float *as;
-  int64_t ldas;
   if (a.pro != PRO_NONE) {
     pro_compute_row<QW>(a, 0, r0, a_lds, as_lds, blk);
     for (int m = 1; m < M; ++m) {
@@ -240,34 +264,24 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
       pro_load_row<QW>(a, m, r);
       pro_compute_row<QW>(a, m, r, a_lds, as_lds, blk);
     }
-    arow = a_lds + (lr < M ? lr : 0) * K + lg * 16;
-    as = as_lds;
-    ldas = K / 256;
-  } else {
-    arow = a.a + static_cast<int64_t>(lr < M ? lr : 0) * a.lda + lg * 16;
-    as = a.as;
-    ldas = a.ldas;
-  }
-  const bool avalid = lr < M;
-  v4i av[GPW][KSTEPS];
+    const int8_t *arow = a_lds + (avalid ? lr : 0) * K + lg * 16;
 #pragma unroll
-  for (int gi = 0; gi < GPW; ++gi) {
-    const int g = wave + 4 * gi;
+    for (int gi = 0; gi < GPW; ++gi) {
+      const int g = min(wave + 4 * gi, ngroups - 1);
 #pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks)
-      av[gi][ks] = (g < ngroups && avalid) ? *reinterpret_cast<const v4i *>(arow + g * G + ks * 64)
-                                           : zero4();
+      for (int ks = 0; ks < KSTEPS; ++ks)
+        av[gi][ks] = avalid ? *reinterpret_cast<const v4i *>(arow + g * G + ks * 64) : zero4();
+#pragma unroll
+      for (int i = 0; i < 4; ++i) asv[gi][i] = as_lds[min(lg * 4 + i, M - 1) * (K / 256) + g];
+    }
   }
 #pragma unroll
   for (int gi = 0; gi < GPW; ++gi) {
     const int g = wave + 4 * gi;
     if (g >= ngroups) break;
-    float asv[4];
+    float asv_[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = lg * 4 + i;
-      asv[i] = (m < M) ? as[static_cast<int64_t>(m) * ldas + g] : 0.0f;
-    }
+    for (int i = 0; i < 4; ++i) asv_[i] = (lg * 4 + i < M) ? asv[gi][i] : 0.0f;
 #pragma unroll
     for (int mi = 0; mi < NMAT; ++mi)
 #pragma unroll
@@ -276,12 +290,10 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks)
           acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[gi][ks], bv[mi][nt][gi][ks], acc, 0, 0, 0);
-        const int ncol = n_blk - sg.n0 + nt * 16 + lr;
-        const float bsv = (mi == 0 ? sg.bs : sg.bs2)[ncol];
         float *pt = part + ((mi * ngroups + g) * 16) * PP + nt * 16 + lr;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          pt[(lg * 4 + i) * PP] = __fmul_rn(__fmul_rn(static_cast<float>(acc[i]), bsv), asv[i]);
+          pt[(lg * 4 + i) * PP] = __fmul_rn(__fmul_rn(static_cast<float>(acc[i]), bsv[mi][nt]), asv_[i]);
       }
   }
   __syncthreads();
