@@ -485,6 +485,15 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
 // model instead of 8 halves the per-workgroup work, which matters more here
 // than reading each KV head's rows twice.  8 waves x 3 blocks (768 keys per
 // chunk) keep K and V of the chunk in registers without spilling.
+// Independent sequences (row_pos set): one workgroup per KV head and
+// sequence with both query heads of the group, so each K/V row is read once;
+// the batch supplies the parallelism that b = 1 has to find in query heads.
+hipError_t launch_decode_batch(const AttnArgs &a, hipStream_t s) {
+  constexpr int QPW = 2, NW = 8, BPW = 3;
+  Q3_LAUNCH((attn_decode_kernel<QPW, NW, BPW, false>), dim3(a.heads / QPW, a.rows), dim3(NW * 64), 0, s, a);
+  return hipGetLastError();
+}
+
 hipError_t launch_decode(const AttnArgs &a, hipStream_t s) {
   constexpr int QPW = 1, NW = 8, BPW = 3;
   static_assert(QPW * HD <= NW * 64, "phase 4 needs a thread per (head, dim)");
@@ -512,6 +521,9 @@ bool attn_decode_supported(const AttnArgs &a) {
          (!a.row_pos || (a.ldq % 16) == 0);
 }
 
-hipError_t launch_attn_decode(const AttnArgs &a, hipStream_t s) { return launch_decode(a, s); }
+hipError_t launch_attn_decode(const AttnArgs &a, hipStream_t s) {
+  if (a.row_pos && a.heads == 2 * a.kv_heads) return launch_decode_batch(a, s);
+  return launch_decode(a, s);
+}
 
 }  // namespace q3

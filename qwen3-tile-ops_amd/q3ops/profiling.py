@@ -35,8 +35,10 @@ CLASS_OF = [
 ]
 
 
-def short_name(name: str) -> str:
-    """Kernel symbol without return type, anonymous namespace and argument list."""
+def short_name(name: str, width: int = 90) -> str:
+    """Kernel symbol without return type, anonymous namespace and argument
+    list, cut to `width` characters (library kernels have very long template
+    names)."""
     n = name.replace("(anonymous namespace)::", "").replace("void ", "")
     depth = 0
     for i, ch in enumerate(n):
@@ -45,8 +47,9 @@ def short_name(name: str) -> str:
         elif ch == ">":
             depth -= 1
         elif ch == "(" and depth == 0:
-            return n[:i]
-    return n
+            n = n[:i]
+            break
+    return n if len(n) <= width else n[:width - 3] + "..."
 
 
 def class_of(name: str) -> str | None:
