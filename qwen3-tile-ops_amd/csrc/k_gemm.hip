@@ -37,14 +37,6 @@ __device__ __forceinline__ v4i zero4() {
   return z;
 }
 
-// Ordered 32-bit key of an f32 (main_big.cpp:314), with -0 folded into +0 so
-// that equal values compare equal, as the reference's float `<` does.
-__device__ __forceinline__ uint32_t ordered_key(float v) {
-  uint32_t b = f32_bits(v);
-  if (b == 0x80000000u) b = 0u;
-  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
-
 __device__ __forceinline__ float key_value(uint32_t k) {
   const uint32_t b = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
   return bits_f32(b);
@@ -326,7 +318,9 @@ __global__ void __launch_bounds__(64) argmax_logits_kernel(const float *logits, 
 
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t s) {
   if (a.M <= 0) return hipSuccess;
-  if (a.M > 16 && a.epi != EPI_ARGMAX) {  // prefill shapes: the LDS-staged tile kernel
+  // prefill shapes and batches of sequences: the LDS-staged tile kernel
+  // (ARGMAX over at most 64 rows, so that one row tile reads the weights once)
+  if (a.M > 16 && (a.epi != EPI_ARGMAX || a.M <= 64)) {
     TileArgs t{};
     t.M = a.M;
     t.N = a.N;
@@ -350,6 +344,8 @@ hipError_t launch_gemm(const GemmArgs &a, hipStream_t s) {
     t.ld_cs = a.ld_cs;
     t.cs_row_dev = a.cs_row_dev;
     t.inv_hd = a.inv_hd;
+    t.keys = a.keys;
+    t.keys_ld = a.keys_ld;
     if (gemm_tile_supported(t, a.epi)) return launch_gemm_tile(t, a.epi, s);
   }
   switch (a.epi) {

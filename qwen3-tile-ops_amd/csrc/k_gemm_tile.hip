@@ -264,7 +264,25 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(TileArgs a) {
     for (int rr = wave; rr < BM; rr += S::NW) {
       const int m = m0 + rr;
       if (m >= M) break;
-      if constexpr (EPI == EPI_SWIGLUQ) {
+      if constexpr (EPI == EPI_ARGMAX) {
+        // lm_argmax.h:72-182: the row's (max, first column) over the tile's
+        // 128 columns as one 64-bit key; the finish kernel takes the max
+        // over the tiles
+        static_assert(EPI != EPI_ARGMAX || BN == 128, "one key per 128 columns");
+        const float t0 = tile[rr * S::LDT + lane];
+        const float t1 = tile[rr * S::LDT + lane + 64];
+        unsigned long long best = (static_cast<unsigned long long>(ordered_key(t0)) << 32) |
+                                  (0xFFFFFFFFu - static_cast<uint32_t>(n0 + lane));
+        const unsigned long long other = (static_cast<unsigned long long>(ordered_key(t1)) << 32) |
+                                         (0xFFFFFFFFu - static_cast<uint32_t>(n0 + lane + 64));
+        best = other > best ? other : best;
+#pragma unroll
+        for (int sft = 1; sft < 64; sft <<= 1) {
+          const unsigned long long o = lane_xor_u64(best, sft);
+          best = o > best ? o : best;
+        }
+        if (lane == 0) a.keys[static_cast<int64_t>(m) * a.keys_ld + blockIdx.x] = best;
+      } else if constexpr (EPI == EPI_SWIGLUQ) {
         // swiglu_quant.h:195-231: per 256-column group absmax * (1/127)
         static_assert(EPI != EPI_SWIGLUQ || BN % 256 == 0, "whole quantisation groups");
 #pragma unroll
@@ -283,7 +301,7 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(TileArgs a) {
           if (lane == 0) a.ss[static_cast<int64_t>(m) * a.ldss + ((n0 + q * 256) / 256) * a.ss_col] = scale;
         }
       } else {
-        static_assert(EPI == EPI_SWIGLUQ || BN == 128, "one head (128 columns) per tile");
+        static_assert(EPI == EPI_SWIGLUQ || EPI == EPI_ARGMAX || BN == 128, "one head (128 columns) per tile");
         float t0 = tile[rr * S::LDT + lane];
         float t1 = tile[rr * S::LDT + lane + 64];
         if constexpr (EPI == EPI_NRQ) {
@@ -341,12 +359,20 @@ bool gemm_tile_supported(const TileArgs &a, int epi) {
 hipError_t launch_gemm_tile(const TileArgs &a, int epi, hipStream_t s) {
   if (a.M <= 0) return hipSuccess;
   if (!gemm_tile_supported(a, epi)) return hipErrorInvalidValue;
+  // a batch of sequences (M <= 64): 32-column tiles, for 4x the workgroups
+  if (a.M <= 64 && (epi == EPI_STORE || epi == EPI_ADD)) {
+    if (epi == EPI_STORE) return launch_shape<64, 32, 4, 1, 3, 256, EPI_STORE>(a, s);
+    return launch_shape<64, 32, 4, 1, 3, 256, EPI_ADD>(a, s);
+  }
   switch (epi) {
     case EPI_STORE: return launch_shape<64, 128, 2, 1, 3, 256, EPI_STORE>(a, s);
     case EPI_ADD: return launch_shape<32, 128, 2, 1, 3, 256, EPI_ADD>(a, s);
     case EPI_HEADQ: return launch_shape<64, 128, 2, 1, 3, 256, EPI_HEADQ>(a, s);
     case EPI_NRQ: return launch_shape<64, 128, 2, 1, 3, 256, EPI_NRQ>(a, s);
     case EPI_SWIGLUQ: return launch_shape<32, 256, 2, 2, 2, 128, EPI_SWIGLUQ>(a, s);
+    case EPI_ARGMAX:  // rows of a batch of sequences (M <= 64): the weights are read once
+      if (!a.keys || a.keys_ld < a.N / 128) return hipErrorInvalidValue;
+      return launch_shape<64, 128, 2, 1, 3, 256, EPI_ARGMAX>(a, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -38,12 +38,6 @@ __device__ __forceinline__ v4i zero4() {
   return z;
 }
 
-__device__ __forceinline__ uint32_t ordered_key(float v) {
-  uint32_t b = f32_bits(v);
-  if (b == 0x80000000u) b = 0u;
-  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
-
 // ref_qwen3.py:194-200 (exp table staged in LDS).
 __device__ __forceinline__ float swiglu1(float g, float u, const uint64_t *tab) {
   float e = __fmul_rn(g, -1.0f);

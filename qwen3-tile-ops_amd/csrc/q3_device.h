@@ -33,6 +33,16 @@ __device__ __forceinline__ int wave_id() {
   return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
 }
 
+// Ordered 32-bit key of an f32 (main_big.cpp:314), with -0 folded into +0 so
+// that equal values compare equal, as the reference's float `<` does.  With
+// (0xFFFFFFFF - column) in the low half, the largest 64-bit key is the
+// first column holding the maximum (lm_argmax.h:58-66).
+__device__ __forceinline__ uint32_t ordered_key(float v) {
+  uint32_t b = __float_as_uint(v);
+  if (b == 0x80000000u) b = 0u;
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
 // ---- LDS staging ------------------------------------------------------
 // Generic pointer to an LDS object as the address-space-3 pointer that
 // __builtin_amdgcn_global_load_lds takes (through an integer so that the

@@ -152,6 +152,8 @@ struct TileArgs {
   int64_t lds8;
   float *ss;
   int64_t ldss, ss_col;
+  unsigned long long *keys;  // EPI_ARGMAX: [M][keys_ld], one key per 128-column tile
+  int64_t keys_ld;
 };
 bool gemm_tile_supported(const TileArgs &a, int epi);
 hipError_t launch_gemm_tile(const TileArgs &a, int epi, hipStream_t s);

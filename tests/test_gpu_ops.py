@@ -46,7 +46,7 @@ SHAPES = [(1024, 2048, 256), (1024, 1024, 256), (1024, 6144, 256), (3072, 1024, 
           (2048, 1024, 128)]
 
 
-@pytest.mark.parametrize("M", [1, 5, 32, 512])
+@pytest.mark.parametrize("M", [1, 5, 32, 64, 512])
 @pytest.mark.parametrize("K,N,group", SHAPES)
 def test_gemm_store(cuda, M, K, N, group):
     note(f"gemm store M={M} K={K} N={N} g={group}")
@@ -80,7 +80,7 @@ def test_gemm_golden_guest_fixture(cuda):
         assert bits_equal(got, g[key]), describe_diff(got, g[key])
 
 
-@pytest.mark.parametrize("M", [1, 7, 64, 300])
+@pytest.mark.parametrize("M", [1, 7, 40, 64, 300])
 def test_gemm_residual_add(cuda, M):
     rng = np.random.default_rng(M)
     a, as_, b, bs = rand_gemm(rng, M, 2048, 1024, 128)
@@ -307,10 +307,12 @@ def test_lm_argmax(cuda, N):
     assert int(host(bidx2)[0]) == -5 and host(best2)[0] == np.float32(1e30)
 
 
-@pytest.mark.parametrize("M", [2, 5, 16])
+@pytest.mark.parametrize("M", [2, 5, 16, 33, 64, 100])
 def test_lm_argmax_wide_multirow(cuda, M):
     """lm_head width with several rows: one running key per row and
-    workgroup across the column tiles each workgroup walks."""
+    workgroup across the column tiles each workgroup walks (M <= 16), one key
+    per row and 128-column tile of the LDS-staged tile kernel (M <= 64), and
+    the per-32-row kernel beyond."""
     note(f"lm argmax M={M} N=151936")
     rng = np.random.default_rng(40 + M)
     a, as_, b, bs = rand_gemm(rng, M, 1024, 151936, 256)
