@@ -489,7 +489,7 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
 // sequence with both query heads of the group, so each K/V row is read once;
 // the batch supplies the parallelism that b = 1 has to find in query heads.
 hipError_t launch_decode_batch(const AttnArgs &a, hipStream_t s) {
-  constexpr int QPW = 2, NW = 8, BPW = 3;
+  constexpr int QPW = 2, NW = 4, BPW = 3;
   Q3_LAUNCH((attn_decode_kernel<QPW, NW, BPW, false>), dim3(a.heads / QPW, a.rows), dim3(NW * 64), 0, s, a);
   return hipGetLastError();
 }
