@@ -203,7 +203,19 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
   }
   // a batch of independent sequences: sequence blockIdx.y's length, pages
   // and rows of q8/qs/o8/os
-  const int brow = a.row_pos ? static_cast<int>(blockIdx.y) : 0;
+  // Batches whose row count is a multiple of 8: workgroup i runs on XCD
+  // i % 8 (round-robin dispatch), so the KV-head groups of one sequence are
+  // given ids with equal residues and share that XCD's L2 (the per-row scale
+  // sectors and page table lines they have in common).
+  int bx = static_cast<int>(blockIdx.x), by = static_cast<int>(blockIdx.y);
+  if (a.row_pos && (gridDim.y & 7) == 0) {
+    const int nx = static_cast<int>(gridDim.x);
+    const int id = bx + nx * by;
+    const int slot = id >> 3;
+    by = (id & 7) + 8 * (slot / nx);
+    bx = slot % nx;
+  }
+  const int brow = a.row_pos ? by : 0;
   const uint16_t *table = a.row_pos ? a.row_tables + brow * a.ld_table : a.table;
   const int8_t *q8_row = a.q8 + brow * a.ldq;
   const float *qs_row = a.qs + brow * a.ldqs;
@@ -213,7 +225,7 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
   const int lane = tid & 63;
   const int wave = wave_id();
   const int grp = a.heads / a.kv_heads;
-  const int qh0 = blockIdx.x * QPW;
+  const int qh0 = bx * QPW;
   const int kvh = qh0 / grp;
   const bool kv_writer = (qh0 % grp) == 0;
   const uint32_t kv_len = a.row_pos ? static_cast<uint32_t>(a.row_pos[brow]) + 1 : a.kv_len;
