@@ -507,7 +507,7 @@ hipError_t launch_decode_batch(const AttnArgs &a, hipStream_t s) {
 }
 
 hipError_t launch_decode(const AttnArgs &a, hipStream_t s) {
-  constexpr int QPW = 1, NW = 8, BPW = 3;
+  constexpr int QPW = 1, NW = 12, BPW = 2;
   static_assert(QPW * HD <= NW * 64, "phase 4 needs a thread per (head, dim)");
   const int extra = a.pf_n > 0 ? a.pf_wgs : 0;
   const int seqs = a.row_pos ? a.rows : 1;
