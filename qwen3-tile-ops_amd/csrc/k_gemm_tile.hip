@@ -366,7 +366,7 @@ hipError_t launch_gemm_tile(const TileArgs &a, int epi, hipStream_t s) {
   }
   switch (epi) {
     case EPI_STORE: return launch_shape<64, 128, 2, 1, 3, 256, EPI_STORE>(a, s);
-    case EPI_ADD: return launch_shape<32, 128, 2, 1, 3, 256, EPI_ADD>(a, s);
+    case EPI_ADD: return launch_shape<32, 64, 2, 1, 3, 256, EPI_ADD>(a, s);
     case EPI_HEADQ: return launch_shape<64, 128, 2, 1, 3, 256, EPI_HEADQ>(a, s);
     case EPI_NRQ: return launch_shape<64, 128, 2, 1, 3, 256, EPI_NRQ>(a, s);
     case EPI_SWIGLUQ: return launch_shape<32, 256, 2, 2, 2, 128, EPI_SWIGLUQ>(a, s);
