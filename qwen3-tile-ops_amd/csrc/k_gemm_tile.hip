@@ -104,6 +104,25 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(TileArgs a) {
   const int lg = lane >> 4;
   const int m0 = blockIdx.y * BM;
   const int n0 = blockIdx.x * BN;
+  // the tile's column segment (EPI_QKV: Q, K or V; else the single matrix):
+  // its weights, scales, first column within them, destination and norm
+  const int8_t *B0 = a.b0;
+  const float *BS0 = a.bs0;
+  int nb = n0;
+  QDest qd = a.qd;
+  const float *nw = a.nw;
+  bool do_norm = EPI == EPI_NRQ;
+  if constexpr (EPI == EPI_QKV) {
+    int si = 0;
+    for (int i = 1; i < a.nseg; ++i)
+      if (n0 >= a.seg[i].n0) si = i;
+    B0 = a.seg[si].b;
+    BS0 = a.seg[si].bs;
+    nb = n0 - a.seg[si].n0;
+    qd = a.seg[si].qd;
+    nw = a.seg[si].nw;
+    do_norm = a.seg[si].norm != 0;
+  }
   const int M = a.M;
   const int T = a.K / KS;            // k-steps
   const int SPG = a.group / 64;      // k-slices per group
@@ -126,8 +145,8 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(TileArgs a) {
         src = a.a + static_cast<int64_t>(row) * a.lda + t * KS + 16 * c;
       } else {
         const int rb = r - BM;
-        const int8_t *bm = (NMAT == 2 && rb >= BN) ? a.b1 : a.b0;
-        src = bm + static_cast<int64_t>(n0 + rb % BN) * a.ldb + t * KS + 16 * c;
+        const int8_t *bm = (NMAT == 2 && rb >= BN) ? a.b1 : B0;
+        src = bm + static_cast<int64_t>(nb + rb % BN) * a.ldb + t * KS + 16 * c;
       }
       __builtin_amdgcn_global_load_lds(const_cast<int8_t *>(src), to_lds(st + 1024 * j), 16, 0, 0);
     }
@@ -144,8 +163,8 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(TileArgs a) {
   for (int mi = 0; mi < NMAT; ++mi)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      const float *bs = mi == 0 ? a.bs0 : a.bs1;
-      bsv[mi][nt] = bs[static_cast<int64_t>(n0 + wn * S::WN + nt * 16 + lr) * a.bs_stride];
+      const float *bs = mi == 0 ? BS0 : a.bs1;
+      bsv[mi][nt] = bs[static_cast<int64_t>(nb + wn * S::WN + nt * 16 + lr) * a.bs_stride];
     }
 
   // scales first, then the first STAGES-1 copies: vector loads complete in
@@ -304,17 +323,17 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(TileArgs a) {
         static_assert(EPI == EPI_SWIGLUQ || EPI == EPI_ARGMAX || BN == 128, "one head (128 columns) per tile");
         float t0 = tile[rr * S::LDT + lane];
         float t1 = tile[rr * S::LDT + lane + 64];
-        if constexpr (EPI == EPI_NRQ) {
+        if (do_norm) {
           int64_t crow = m;
           if (a.cs_row_dev) crow += *a.cs_row_dev;
-          head_norm_rope(t0, t1, lane, a.nw, a.nw_stride, a.cos_t + crow * a.ld_cs, a.sin_t + crow * a.ld_cs,
+          head_norm_rope(t0, t1, lane, nw, a.nw_stride, a.cos_t + crow * a.ld_cs, a.sin_t + crow * a.ld_cs,
                          a.inv_hd, true);
         }
         const float mx = max64(fmaxf(fabsf(t0), fabsf(t1)));
         const float scale = __fmul_rn(mx, inv127());
         int8_t *row8;
         float *sp;
-        qdest_row(a.qd, m, n0 / 128, &row8, &sp);
+        qdest_row(qd, m, nb / 128, &row8, &sp);
         row8[lane] = static_cast<int8_t>(quant1(t0, scale));
         row8[lane + 64] = static_cast<int8_t>(quant1(t1, scale));
         if (lane == 0) *sp = scale;
@@ -351,7 +370,7 @@ bool gemm_tile_supported(const TileArgs &a, int epi) {
   if (a.M < 1 || a.K % 256 || a.group % 64 || a.K % a.group || a.N <= 0) return false;
   if (a.K / a.group > 64) return false;
   auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-  if (!al16(a.a) || !al16(a.b0) || (a.lda % 16) || (a.ldb % 16)) return false;
+  if (!al16(a.a) || (epi != EPI_QKV && !al16(a.b0)) || (a.lda % 16) || (a.ldb % 16)) return false;
   if (epi == EPI_SWIGLUQ) return a.N % 256 == 0 && a.b1 && al16(a.b1);
   return a.N % 128 == 0;
 }
@@ -369,6 +388,13 @@ hipError_t launch_gemm_tile(const TileArgs &a, int epi, hipStream_t s) {
     case EPI_ADD: return launch_shape<32, 64, 2, 1, 3, 256, EPI_ADD>(a, s);
     case EPI_HEADQ: return launch_shape<64, 128, 2, 1, 3, 256, EPI_HEADQ>(a, s);
     case EPI_NRQ: return launch_shape<64, 128, 2, 1, 3, 256, EPI_NRQ>(a, s);
+    case EPI_QKV:
+      if (a.nseg < 1 || a.nseg > 3 || a.seg[0].n0 != 0 || a.seg[a.nseg - 1].n1 != a.N) return hipErrorInvalidValue;
+      for (int i = 0; i < a.nseg; ++i)
+        if (a.seg[i].n0 % 128 || a.seg[i].n1 % 128 || a.seg[i].n1 <= a.seg[i].n0 ||
+            (i > 0 && a.seg[i].n0 != a.seg[i - 1].n1) || (reinterpret_cast<uintptr_t>(a.seg[i].b) & 15))
+          return hipErrorInvalidValue;
+      return launch_shape<64, 128, 2, 1, 3, 256, EPI_QKV>(a, s);
     case EPI_SWIGLUQ: return launch_shape<32, 256, 2, 2, 2, 128, EPI_SWIGLUQ>(a, s);
     case EPI_ARGMAX:  // rows of a batch of sequences (M <= 64): the weights are read once
       if (!a.keys || a.keys_ld < a.N / 128) return hipErrorInvalidValue;

@@ -68,6 +68,7 @@ enum Epi : int {
   EPI_ARGMAX = 4,  // fold D into per-row (max, first index) keys
   EPI_SWIGLU = 5,  // gate/up pair -> f32 SwiGLU (decode GEMV only)
   EPI_SWIGLUQ = 6, // gate/up pair -> SwiGLU -> per-256-column int8 quant (tiled)
+  EPI_QKV = 7,     // column segments with their own weights and HEADQ/NRQ epilogue (tiled)
 };
 
 // Destination of the HEADQ/NRQ int8 rows: either a dense [M][N] i8 view
@@ -154,6 +155,19 @@ struct TileArgs {
   int64_t ldss, ss_col;
   unsigned long long *keys;  // EPI_ARGMAX: [M][keys_ld], one key per 128-column tile
   int64_t keys_ld;
+  // EPI_QKV: N = sum of the segments' widths (multiples of 128); segment i
+  // covers columns [n0, n1) with its own weights b / scales bs (ldb and
+  // bs_stride shared), destination qd, and, if norm, RMSNorm gains nw
+  // (+ RoPE with the shared cos/sin rows) before the quant (else HEADQ).
+  int nseg;
+  struct Seg {
+    int n0, n1;
+    const int8_t *b;
+    const float *bs;
+    QDest qd;
+    const float *nw;
+    int norm;
+  } seg[3];
 };
 bool gemm_tile_supported(const TileArgs &a, int epi);
 hipError_t launch_gemm_tile(const TileArgs &a, int epi, hipStream_t s);

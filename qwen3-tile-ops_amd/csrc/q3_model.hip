@@ -599,6 +599,52 @@ int qkv_projections(q3_model *m, const LayerPtrs &lp, uint32_t pos, uint32_t row
   const float *cos_t = at<const float>(m, y.kCOS);
   const float *sin_t = at<const float>(m, y.kSIN);
   const float inv_hd = 1.0f / static_cast<float>(HD);
+  if (do_tail && tr0 == 0 && tr == rows) {
+    // Q | K | V as one launch (3x the workgroups of each alone), each column
+    // segment with its own weights, epilogue and destination
+    q3::TileArgs t{};
+    t.M = static_cast<int>(rows);
+    t.N = QW + 2 * KW;
+    t.K = H;
+    t.group = 256;
+    t.a = h8;
+    t.lda = H;
+    t.as = hs;
+    t.ldas = H / 256;
+    t.ldb = H;
+    t.bs_stride = 1;
+    t.nw_stride = 1;
+    t.cos_t = cos_t + static_cast<int64_t>(pos) * HALF;
+    t.sin_t = sin_t + static_cast<int64_t>(pos) * HALF;
+    t.ld_cs = HALF;
+    t.inv_hd = inv_hd;
+    t.nseg = 3;
+    t.seg[0].n0 = 0;
+    t.seg[0].n1 = QW;
+    t.seg[0].b = lp.wq;
+    t.seg[0].bs = lp.wqs;
+    t.seg[0].qd.q8 = q8;
+    t.seg[0].qd.ldq8 = QW;
+    t.seg[0].qd.qs = qs;
+    t.seg[0].qd.ldqs = y.heads;
+    t.seg[0].qd.qs_col = 1;
+    t.seg[0].nw = lp.nq;
+    t.seg[0].norm = 1;
+    t.seg[1].n0 = QW;
+    t.seg[1].n1 = QW + KW;
+    t.seg[1].b = lp.wk;
+    t.seg[1].bs = lp.wks;
+    set_paged(t.seg[1].qd, m, lp.kc, lp.kcs, pos);
+    t.seg[1].nw = lp.nk;
+    t.seg[1].norm = 1;
+    t.seg[2].n0 = QW + KW;
+    t.seg[2].n1 = QW + 2 * KW;
+    t.seg[2].b = lp.wv;
+    t.seg[2].bs = lp.wvs;
+    set_paged(t.seg[2].qd, m, lp.vc, lp.vcs, pos);
+    t.seg[2].norm = 0;
+    if (q3::gemm_tile_supported(t, q3::EPI_QKV)) return hip_status(q3::launch_gemm_tile(t, q3::EPI_QKV, s));
+  }
   {
     q3::GemmArgs g = gemm_args(static_cast<int>(rows), KW, H, 256, h8, hs, lp.wv, lp.wvs);
     g.epi = q3::EPI_HEADQ;
