@@ -52,10 +52,15 @@ __device__ __forceinline__ float swiglu1(float g, float u, const uint64_t *tab) 
 
 // Row destination of the int8 head output (dense view or paged KV slot).
 __device__ __forceinline__ void qdest_row(const QDest &d, int m, int head, int8_t **row8, float **scale) {
-  if (d.table) {
+  if (d.table || d.row_pos) {
     uint32_t t = d.pos0 + static_cast<uint32_t>(m);
     if (d.pos_dev) t += static_cast<uint32_t>(*d.pos_dev);
-    const uint32_t page = d.table[t / d.page_tokens];
+    const uint16_t *table = d.table;
+    if (d.row_pos) {
+      t = static_cast<uint32_t>(d.row_pos[m]);
+      table = d.row_tables + m * d.ld_table;
+    }
+    const uint32_t page = table[t / d.page_tokens];
     const uint32_t slot = t % d.page_tokens;
     *row8 = d.q8 + page * d.page_bytes + slot * d.row_bytes + head * 128;
     *scale = reinterpret_cast<float *>(reinterpret_cast<int8_t *>(d.qs) + page * d.scale_page_bytes +
@@ -326,6 +331,7 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(TileArgs a) {
         if (do_norm) {
           int64_t crow = m;
           if (a.cs_row_dev) crow += *a.cs_row_dev;
+          if (a.cs_row_pos) crow = a.cs_row_pos[m];
           head_norm_rope(t0, t1, lane, nw, a.nw_stride, a.cos_t + crow * a.ld_cs, a.sin_t + crow * a.ld_cs,
                          a.inv_hd, true);
         }
@@ -385,7 +391,7 @@ hipError_t launch_gemm_tile(const TileArgs &a, int epi, hipStream_t s) {
   }
   switch (epi) {
     case EPI_STORE: return launch_shape<64, 128, 2, 1, 3, 256, EPI_STORE>(a, s);
-    case EPI_ADD: return launch_shape<32, 64, 2, 1, 3, 256, EPI_ADD>(a, s);
+    case EPI_ADD: return launch_shape<32, 64, 2, 1, 5, 256, EPI_ADD>(a, s);
     case EPI_HEADQ: return launch_shape<64, 128, 2, 1, 3, 256, EPI_HEADQ>(a, s);
     case EPI_NRQ: return launch_shape<64, 128, 2, 1, 3, 256, EPI_NRQ>(a, s);
     case EPI_QKV:

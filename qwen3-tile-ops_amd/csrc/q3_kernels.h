@@ -86,6 +86,11 @@ struct QDest {
   int64_t scale_page_bytes, scale_row_bytes; // f32 pages
   uint32_t pos0;
   const int32_t *pos_dev;  // optional: pos0 += *pos_dev
+  // optional (paged): row m of a batch of independent sequences goes to
+  // position row_pos[m] through its own table row_tables + m * ld_table
+  const int32_t *row_pos;
+  const uint16_t *row_tables;
+  int64_t ld_table;
 };
 
 struct GemmArgs {
@@ -149,6 +154,7 @@ struct TileArgs {
   int64_t ld_cs;
   const int32_t *cs_row_dev;
   float inv_hd;
+  const int32_t *cs_row_pos;  // optional: RoPE row of output row m = cs_row_pos[m]
   int8_t *s8;
   int64_t lds8;
   float *ss;

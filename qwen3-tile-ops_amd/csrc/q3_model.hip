@@ -916,9 +916,6 @@ extern "C" int q3_decode_batch(q3_model *m, uint32_t n, const int32_t *ids, cons
   float *h = at<float>(m, y.kH);
   int8_t *h8 = at<int8_t>(m, y.kH8);
   float *hs = at<float>(m, y.kHS);
-  float *q = at<float>(m, y.kQ);
-  float *k = at<float>(m, y.kK);
-  float *v = at<float>(m, y.kV);
   int8_t *q8 = at<int8_t>(m, y.kQ8);
   float *qs = at<float>(m, y.kQS);
   int8_t *o8 = at<int8_t>(m, y.kO8);
@@ -963,52 +960,60 @@ extern "C" int q3_decode_batch(q3_model *m, uint32_t n, const int32_t *ids, cons
   for (uint32_t L = 0; L < y.layers; ++L) {
     const LayerPtrs lp = layer_ptrs(m, L);
     if (L != 0) Q3_TRY(rows(1, lp.n1));
-    // Q, K, V projections (f32 rows), then the per-row head epilogues
+    // Q | K | V in one tile launch with the head epilogues: Q (norm, RoPE,
+    // quant) into the dense q8/qs rows, K (norm, RoPE, quant) and V (quant)
+    // into each row's page slot at its own position
     {
-      q3::GemmArgs g = gemm_args(M, QW, H, 256, h8, hs, lp.wq, lp.wqs);
-      g.epi = q3::EPI_STORE;
-      g.out = q;
-      g.ldo = QW;
-      Q3_HIP(q3::launch_gemm(g, s));
-      g = gemm_args(M, KW, H, 256, h8, hs, lp.wk, lp.wks);
-      g.epi = q3::EPI_STORE;
-      g.out = k;
-      g.ldo = KW;
-      Q3_HIP(q3::launch_gemm(g, s));
-      g = gemm_args(M, KW, H, 256, h8, hs, lp.wv, lp.wvs);
-      g.epi = q3::EPI_STORE;
-      g.out = v;
-      g.ldo = KW;
-      Q3_HIP(q3::launch_gemm(g, s));
-    }
-    {
-      q3::QkvHeadArgs e;
-      std::memset(&e, 0, sizeof(e));
-      e.M = M;
-      e.q_heads = static_cast<int>(y.heads);
-      e.kv_heads = static_cast<int>(y.kv_heads);
-      e.q = q;
-      e.k = k;
-      e.v = v;
-      e.ldq = QW;
-      e.ldk = KW;
-      set_paged(e.kd, m, lp.kc, lp.kcs, 0);
-      set_paged(e.vd, m, lp.vc, lp.vcs, 0);
-      e.qd.q8 = q8;
-      e.qd.ldq8 = QW;
-      e.qd.qs = qs;
-      e.qd.ldqs = y.heads;
-      e.qd.qs_col = 1;
-      e.nq = lp.nq;
-      e.nk = lp.nk;
-      e.cos_q = e.cos_k = cos_t;
-      e.sin_q = e.sin_k = sin_t;
-      e.ld_cs = HALF;
-      e.inv_hd = 1.0f / static_cast<float>(HD);
-      e.row_pos = m->bpos;
-      e.row_tables = m->btab;
-      e.ld_table = ld_table;
-      Q3_HIP(q3::launch_qkv_heads(e, s));
+      q3::TileArgs t{};
+      t.M = M;
+      t.N = QW + 2 * KW;
+      t.K = H;
+      t.group = 256;
+      t.a = h8;
+      t.lda = H;
+      t.as = hs;
+      t.ldas = H / 256;
+      t.ldb = H;
+      t.bs_stride = 1;
+      t.nw_stride = 1;
+      t.cos_t = cos_t;
+      t.sin_t = sin_t;
+      t.ld_cs = HALF;
+      t.cs_row_pos = m->bpos;
+      t.inv_hd = 1.0f / static_cast<float>(HD);
+      t.nseg = 3;
+      t.seg[0].n0 = 0;
+      t.seg[0].n1 = QW;
+      t.seg[0].b = lp.wq;
+      t.seg[0].bs = lp.wqs;
+      t.seg[0].qd.q8 = q8;
+      t.seg[0].qd.ldq8 = QW;
+      t.seg[0].qd.qs = qs;
+      t.seg[0].qd.ldqs = y.heads;
+      t.seg[0].qd.qs_col = 1;
+      t.seg[0].nw = lp.nq;
+      t.seg[0].norm = 1;
+      t.seg[1].n0 = QW;
+      t.seg[1].n1 = QW + KW;
+      t.seg[1].b = lp.wk;
+      t.seg[1].bs = lp.wks;
+      set_paged(t.seg[1].qd, m, lp.kc, lp.kcs, 0);
+      t.seg[1].nw = lp.nk;
+      t.seg[1].norm = 1;
+      t.seg[2].n0 = QW + KW;
+      t.seg[2].n1 = QW + 2 * KW;
+      t.seg[2].b = lp.wv;
+      t.seg[2].bs = lp.wvs;
+      set_paged(t.seg[2].qd, m, lp.vc, lp.vcs, 0);
+      t.seg[2].norm = 0;
+      for (int sg = 1; sg < 3; ++sg) {
+        t.seg[sg].qd.table = nullptr;
+        t.seg[sg].qd.row_pos = m->bpos;
+        t.seg[sg].qd.row_tables = m->btab;
+        t.seg[sg].qd.ld_table = ld_table;
+      }
+      if (!q3::gemm_tile_supported(t, q3::EPI_QKV)) return Q3_ERR_UNSUPPORTED;
+      Q3_HIP(q3::launch_gemm_tile(t, q3::EPI_QKV, s));
     }
     {
       q3::AttnArgs t{};
