@@ -98,7 +98,24 @@ struct Smem {
   float pv[QPW][CB][HD];  // f32(P8.V) * pmax per block
   float run[QPW];
   float absmax[QPW][2];
+  int8_t o8[HD];  // OFUSE: the head's quantised output and its scale
+  float os;
 };
+
+// OFUSE: the O projection's row scales (shared by every head)
+constexpr int kORowsMax = 1024;
+template <bool OFUSE>
+struct SmemO {
+  float wos[OFUSE ? kORowsMax : 1];
+};
+
+// OFUSE (QPW = 1): the head's slice of the O projection weights, rows
+// n = 96 i + tid / 8 (i < kOPieces), 16 bytes (columns 16 (tid % 8) ..) of
+// the head's 128 per thread; up to kORowsMax rows.
+constexpr int kOPieces = 11;
+// pieces loaded after phase 1 of a chunk; the rest after its phase 3 (V rows
+// consumed): all of them at once do not fit the register file
+constexpr int kOPiecesEarly = 6;
 
 // Operands of the fused head epilogue of one wave (see fused_load).
 struct FusedRegs {
@@ -192,11 +209,14 @@ __device__ void prefetch_ranges(const AttnArgs &a, int w) {
 
 // FUSE: the head epilogues run in the prologue (a.fuse_heads); a template
 // parameter rather than a branch so that both variants issue a fixed number
-// of loads.
-template <int QPW, int NW, int BPW, bool FUSE>
+// of loads.  OFUSE (with FUSE, QPW = 1): the O projection partials of the
+// head (AttnArgs::opart) are computed after the epilogue.
+template <int QPW, int NW, int BPW, bool FUSE, bool OFUSE = false>
 __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
   constexpr int CB = NW * BPW;
+  static_assert(!OFUSE || (FUSE && QPW == 1), "O projection fusion: one head per workgroup");
   __shared__ __align__(16) Smem<QPW, CB> sm;
+  __shared__ __align__(16) SmemO<OFUSE> smo;
   if (static_cast<int>(blockIdx.x) >= a.heads / QPW) {  // prefetch workgroups
     prefetch_ranges(a, static_cast<int>(blockIdx.x) - a.heads / QPW);
     return;
@@ -261,8 +281,14 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
   FusedRegs fr{};
   int8_t q8a = 0, q8b = 0;
   float qsa = 0.0f;
+  constexpr int kWosPerThread = (kORowsMax + NW * 64 - 1) / (NW * 64);
+  float wosr[OFUSE ? kWosPerThread : 1];
   if constexpr (FUSE) {
     fused_load<QPW>(a, kvh, qh0, wave, lane, fr);
+    if constexpr (OFUSE) {
+#pragma unroll
+      for (int i = 0; i < kWosPerThread; ++i) wosr[i] = a.wos[min(tid + i * NW * 64, a.o_rows - 1)];
+    }
   } else {
     const int qh = qh0 + min(wave, QPW - 1);  // every wave loads (fixed count)
     q8a = q8_row[qh * HD + lane];
@@ -272,6 +298,22 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
   // keep this issue order (page ids, prologue operands, then the chunk's
   // K/V): the scheduler would otherwise wait for the page ids first
   __builtin_amdgcn_sched_barrier(0);
+
+  // OFUSE: the head's O projection weight slice (see kOPieces) in registers,
+  // used after the epilogue; the row scales go to LDS in the prologue.
+  // Every chunk issues the loads once its K (then V) rows are consumed, so
+  // that the registers are overwritten rather than carried from chunk to
+  // chunk (a conditional load would keep them live across all chunks); in
+  // all but the last chunk every lane reads the same 16 bytes.
+  int4 wov[OFUSE ? kOPieces : 1];
+  auto issue_wo = [&](int i0, int i1, bool live) {
+    const int64_t col = live ? static_cast<int64_t>(qh0) * HD + 16 * (tid & 7) : 0;
+#pragma unroll
+    for (int i = i0; i < i1; ++i) {
+      const int n = live ? min(i * NW * 8 + tid / 8, a.o_rows - 1) : 0;
+      wov[i] = *reinterpret_cast<const int4 *>(a.wo + n * a.ldwo + col);
+    }
+  };
 
   // page ids of this wave's blocks in chunk b0 (for the first chunk they are
   // issued before the prologue operands, above)
@@ -338,6 +380,11 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
     if constexpr (FIRST) {
       // ---- prologue (overlaps the loads above) ----
       if (tid < QPW) sm.run[tid] = -3.402823466e38f;
+      if constexpr (OFUSE) {
+#pragma unroll
+        for (int i = 0; i < kWosPerThread; ++i)
+          if (tid + i * NW * 64 < kORowsMax) smo.wos[tid + i * NW * 64] = wosr[i];
+      }
       if constexpr (FUSE) {
         fused_compute<QPW>(a, sm, fr, kvh, qh0, kv_writer, wave, lane);
       } else if (wave < QPW) {
@@ -397,6 +444,11 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
         if (half == 0) sm.s[h][jb * 32 + kc] = s;
         if (lane == 0) sm.bmax[h][jb] = bm;
       }
+    }
+    if constexpr (OFUSE) {
+      __builtin_amdgcn_sched_barrier(0);
+      issue_wo(0, kOPiecesEarly, b0 + CB >= nblocks);
+      __builtin_amdgcn_sched_barrier(0);
     }
     __syncthreads();
     // ---- phase 2: prefix max (attention_gqa.h:476-477) ----
@@ -461,6 +513,11 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
         }
       }
     }
+    if constexpr (OFUSE) {
+      __builtin_amdgcn_sched_barrier(0);
+      issue_wo(kOPiecesEarly, kOPieces, b0 + CB >= nblocks);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     __syncthreads();
     // ---- phase 4: the sequential den/res chain (attention_gqa.h:476-519) ----
     if (tid < QPW * HD) {
@@ -488,8 +545,35 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
     const int qh = qh0 + ph;
     const float scale = __fmul_rn(fmaxf(sm.absmax[ph][0], sm.absmax[ph][1]), inv127());
     if (a.attn) a.attn[brow * a.ld_attn + qh * HD + pd] = out;
-    o8_row[qh * HD + pd] = static_cast<int8_t>(quant1(out, scale));
+    const int8_t o8 = static_cast<int8_t>(quant1(out, scale));
+    o8_row[qh * HD + pd] = o8;
     if (pd == 0) os_row[qh * a.os_col] = scale;
+    if constexpr (OFUSE) {
+      sm.o8[pd] = o8;
+      if (pd == 0) sm.os = scale;
+    }
+  }
+  if constexpr (OFUSE) {
+    // O projection partials of this head: 8 lanes per row n, 16 columns
+    // each (exact int32 dot products, summed across the 8 lanes), then the
+    // two dequant roundings of the group GEMM
+    __syncthreads();
+    const int *op = reinterpret_cast<const int *>(sm.o8 + 16 * (tid & 7));
+    const int o0 = op[0], o1 = op[1], o2 = op[2], o3 = op[3];
+    const float osh = sm.os;
+    float *dst = a.opart + static_cast<int64_t>(qh0) * a.ld_opart;
+#pragma unroll
+    for (int i = 0; i < kOPieces; ++i) {
+      int acc = sdot4(wov[i].x, o0, 0);
+      acc = sdot4(wov[i].y, o1, acc);
+      acc = sdot4(wov[i].z, o2, acc);
+      acc = sdot4(wov[i].w, o3, acc);
+      acc += lane_xor<1>(acc);
+      acc += lane_xor<2>(acc);
+      acc += lane_xor<4>(acc);
+      const int n = i * NW * 8 + tid / 8;
+      if ((tid & 7) == 0 && n < a.o_rows) dst[n] = __fmul_rn(__fmul_rn(static_cast<float>(acc), smo.wos[n]), osh);
+    }
   }
 }
 
@@ -511,7 +595,11 @@ hipError_t launch_decode(const AttnArgs &a, hipStream_t s) {
   static_assert(QPW * HD <= NW * 64, "phase 4 needs a thread per (head, dim)");
   const int extra = a.pf_n > 0 ? a.pf_wgs : 0;
   const int seqs = a.row_pos ? a.rows : 1;
-  if (a.fuse_heads)
+  static_assert(kOPieces * NW * 8 >= kORowsMax, "O projection rows per workgroup");
+  if (a.fuse_heads && a.opart)
+    Q3_LAUNCH((attn_decode_kernel<QPW, NW, BPW, true, true>), dim3(a.heads / QPW + extra, seqs), dim3(NW * 64), 0,
+              s, a);
+  else if (a.fuse_heads)
     Q3_LAUNCH((attn_decode_kernel<QPW, NW, BPW, true>), dim3(a.heads / QPW + extra, seqs), dim3(NW * 64), 0, s, a);
   else
     Q3_LAUNCH((attn_decode_kernel<QPW, NW, BPW, false>), dim3(a.heads / QPW + extra, seqs), dim3(NW * 64), 0, s, a);
@@ -526,6 +614,12 @@ bool attn_decode_supported(const AttnArgs &a) {
   for (int r = 0; r < a.pf_n; ++r)
     if ((reinterpret_cast<uintptr_t>(a.pf[r]) & 15) != 0 || a.pf_bytes[r] < 0) return false;
   if (a.row_pos && (a.rows < 1 || a.rows > 65535 || a.fuse_heads || a.pf_n || !a.row_tables)) return false;
+  // O projection fusion: b = 1 with the head epilogues; rows of wo cover
+  // every head's 128 columns and are 16-byte aligned
+  if (a.opart && (!a.fuse_heads || a.row_pos || !a.wo || !a.wos || !al16(a.wo) || (a.ldwo % 16) != 0 ||
+                  a.ldwo < static_cast<int64_t>(a.heads) * HD || a.o_rows < 1 || a.o_rows > kORowsMax ||
+                  a.ld_opart < a.o_rows))
+    return false;
   return (a.rows == 1 || a.row_pos) && a.causal && (grp == 1 || grp == 2) && a.kv_heads * grp == a.heads &&
          a.pf_n >= 0 && a.pf_n <= 12 && (a.pf_n == 0 || a.pf_wgs > 0) &&
          (a.row_bytes % 16) == 0 && (a.page_tokens % 32) == 0 && al16(a.k) && al16(a.v) &&

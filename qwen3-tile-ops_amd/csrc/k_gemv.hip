@@ -57,16 +57,17 @@ __device__ __forceinline__ float swiglu1(float g, float u, const uint64_t *tab) 
 // (pro_load_row) before any of them is used.  The kernel loads row 0 before
 // it issues the weight stream: vector loads return in order, so operands
 // requested after the weights would wait for all of them.
-template <int QW>
+template <int QW, int NP>
 struct ProRow {
   float4 x[QW];     // f32 row (PRO_NORM / PRO_QUANT)
   float4 w[QW];     // RMSNorm gain (PRO_NORM / PRO_EMBED)
   uint32_t e[QW];   // four int8 embedding values (PRO_EMBED)
   float esc;        // embedding row scale
+  float4 p[QW][NP > 0 ? NP : 1];  // O projection partials (GemvArgs::part)
 };
 
-template <int QW>
-__device__ __forceinline__ void pro_load_row(const GemvArgs &a, int m, ProRow<QW> &r) {
+template <int QW, int NP>
+__device__ __forceinline__ void pro_load_row(const GemvArgs &a, int m, ProRow<QW, NP> &r) {
   const int lane = threadIdx.x & 63;
   const int wave = wave_id();
   const int K = a.K;
@@ -85,6 +86,19 @@ __device__ __forceinline__ void pro_load_row(const GemvArgs &a, int m, ProRow<QW
       const int c = (wave + 4 * q) * 256 + 4 * lane;
       r.x[q] = *reinterpret_cast<const float4 *>(a.x + static_cast<int64_t>(m) * a.ldx + c);
     }
+    // the O projection partials (row 0 only; every row of the fixed count is
+    // loaded, rows past npart repeat the last one and are not added)
+    if constexpr (NP > 0) {
+      {
+#pragma unroll
+        for (int q = 0; q < QW; ++q) {
+          const int c = (wave + 4 * q) * 256 + 4 * lane;
+#pragma unroll
+          for (int h = 0; h < NP; ++h)
+            r.p[q][h] = *reinterpret_cast<const float4 *>(a.part + min(h, a.npart - 1) * a.ld_part + c);
+        }
+      }
+    }
   }
   if (a.pro != PRO_QUANT) {
 #pragma unroll
@@ -93,8 +107,8 @@ __device__ __forceinline__ void pro_load_row(const GemvArgs &a, int m, ProRow<QW
   }
 }
 
-template <int QW>
-__device__ void pro_compute_row(const GemvArgs &a, int m, const ProRow<QW> &r, int8_t *a_lds,
+template <int QW, int NP>
+__device__ void pro_compute_row(const GemvArgs &a, int m, const ProRow<QW, NP> &r, int8_t *a_lds,
                                 float *as_lds, float *blk) {
   const int lane = threadIdx.x & 63;
   const int wave = wave_id();
@@ -118,6 +132,24 @@ __device__ void pro_compute_row(const GemvArgs &a, int m, const ProRow<QW> &r, i
       v[q][1] = r.x[q].y;
       v[q][2] = r.x[q].z;
       v[q][3] = r.x[q].w;
+      if constexpr (NP > 0) {
+        // residual of the O projection: x + (((0 + p0) + p1) + ...), the
+        // partials summed in head order like the group GEMM's groups
+        {
+          float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int h = 0; h < NP; ++h) {
+            if (h < a.npart) {
+              o[0] = __fadd_rn(o[0], r.p[q][h].x);
+              o[1] = __fadd_rn(o[1], r.p[q][h].y);
+              o[2] = __fadd_rn(o[2], r.p[q][h].z);
+              o[3] = __fadd_rn(o[3], r.p[q][h].w);
+            }
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[q][i] = __fadd_rn(v[q][i], o[i]);
+        }
+      }
     }
   }
   if (a.pro != PRO_QUANT) {
@@ -167,8 +199,15 @@ __device__ void pro_compute_row(const GemvArgs &a, int m, const ProRow<QW> &r, i
   __syncthreads();  // blk is reused by the next row; A is complete
 }
 
-template <int GPW, int KSTEPS, int NT, int NMAT>
+// The O projection partials (GemvArgs::part, M = 1): PART = kPartPro adds
+// them in the PRO_NORM prologue, PART = kPartEpi in the EPI_ADD epilogue.
+constexpr int kMaxPart = 16;
+constexpr int kPartPro = 1, kPartEpi = 2;
+template <int GPW, int KSTEPS, int NT, int NMAT, int PART>
 __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
+  static_assert(PART == 0 || NT == 1, "partials: one item column per thread");
+  constexpr int NPRO = PART == kPartPro ? kMaxPart : 0;
+  constexpr int NEPI = PART == kPartEpi ? kMaxPart : 0;
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int NB = 16 * NT;       // columns per workgroup
   constexpr int PP = NB + 1;        // partial-tile pitch
@@ -201,8 +240,17 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
   // order, and with a fixed count after the prologue operands the compiler
   // waits for those operands alone (vmcnt(#weight loads)) instead of for
   // everything.
-  ProRow<QW> r0;
-  if (a.pro != PRO_NONE) pro_load_row<QW>(a, 0, r0);
+  ProRow<QW, NPRO> r0;
+  if (a.pro != PRO_NONE) pro_load_row<QW, NPRO>(a, 0, r0);
+  // EPI_ADD with partials: those of the thread's item column, before the
+  // weights (the column j = it % NB is the same for every item it of the
+  // thread since 256 is a multiple of NB)
+  float pe[NEPI > 0 ? NEPI : 1];
+  if constexpr (NEPI > 0) {
+    const float *pc = a.part + (n_blk - sg.n0 + static_cast<int>(threadIdx.x) % NB);
+#pragma unroll
+    for (int h = 0; h < NEPI; ++h) pe[h] = pc[min(h, a.npart - 1) * a.ld_part];
+  }
   // A operand rows and scales of the unfused path, also before the weights
   const bool avalid = lr < M;
   v4i av[GPW][KSTEPS];
@@ -230,8 +278,6 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
   for (int mi = 0; mi < NMAT; ++mi)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) bsv[mi][nt] = (mi == 0 ? sg.bs : sg.bs2)[n_blk - sg.n0 + nt * 16 + lr];
-  uint64_t tabv = 0;
-  if (NMAT == 2) tabv = kExp2Tab[threadIdx.x & 31];
   v4i bv[NMAT][NT][GPW][KSTEPS];
 #pragma unroll
   for (int gi = 0; gi < GPW; ++gi) {
@@ -249,14 +295,19 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
         }
     }
   }
-  if (NMAT == 2 && threadIdx.x < 32) exptab[threadIdx.x] = tabv;
+  // the exp table from immediates (a load here would be issued after the
+  // weights and waited for with them); first read after barriers
+  if (NMAT == 2 && threadIdx.x == 0) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) exptab[i] = kExp2Tab[i];
+  }
 
   if (a.pro != PRO_NONE) {
-    pro_compute_row<QW>(a, 0, r0, a_lds, as_lds, blk);
+    pro_compute_row<QW, NPRO>(a, 0, r0, a_lds, as_lds, blk);
     for (int m = 1; m < M; ++m) {
-      ProRow<QW> r;
-      pro_load_row<QW>(a, m, r);
-      pro_compute_row<QW>(a, m, r, a_lds, as_lds, blk);
+      ProRow<QW, 0> r;
+      pro_load_row<QW, 0>(a, m, r);
+      pro_compute_row<QW, 0>(a, m, r, a_lds, as_lds, blk);
     }
     const int8_t *arow = a_lds + (avalid ? lr : 0) * K + lg * 16;
 #pragma unroll
@@ -318,9 +369,17 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
     }
     if (m >= M) continue;
     float *dst = sg.out + static_cast<int64_t>(m) * sg.ldo + ncol;
-    if (sg.epi == EPI_ADD)
-      *dst = __fadd_rn(*dst, out);
-    else if (sg.epi == EPI_SWIGLU)
+    if (sg.epi == EPI_ADD) {
+      float base = *dst;
+      if constexpr (NEPI > 0) {
+        float o = 0.0f;  // the O projection, partials in head order
+#pragma unroll
+        for (int h = 0; h < NEPI; ++h)
+          if (h < a.npart) o = __fadd_rn(o, pe[h]);
+        base = __fadd_rn(base, o);
+      }
+      *dst = __fadd_rn(base, out);
+    } else if (sg.epi == EPI_SWIGLU)
       *dst = swiglu1(out, out2, exptab);
     else
       *dst = out;
@@ -356,8 +415,8 @@ __global__ void __launch_bounds__(256) gemv_stream_kernel(GemvArgs a, int ntiles
   float *as_lds = reinterpret_cast<float *>(a_lds + ((M * K + 15) & ~15));
   float *blk = as_lds + M * (K / 256);
 
-  ProRow<QW> r0;
-  if (a.pro != PRO_NONE) pro_load_row<QW>(a, 0, r0);
+  ProRow<QW, 0> r0;
+  if (a.pro != PRO_NONE) pro_load_row<QW, 0>(a, 0, r0);
 
   // a tile's column scales, then its weights: issued together one tile
   // ahead, so that using tile t waits only for loads issued before tile
@@ -405,11 +464,11 @@ __global__ void __launch_bounds__(256) gemv_stream_kernel(GemvArgs a, int ntiles
   load_tile(b0, s0, t);
 
   if (a.pro != PRO_NONE) {
-    pro_compute_row<QW>(a, 0, r0, a_lds, as_lds, blk);
+    pro_compute_row<QW, 0>(a, 0, r0, a_lds, as_lds, blk);
     for (int m = 1; m < M; ++m) {
-      ProRow<QW> r;
-      pro_load_row<QW>(a, m, r);
-      pro_compute_row<QW>(a, m, r, a_lds, as_lds, blk);
+      ProRow<QW, 0> r;
+      pro_load_row<QW, 0>(a, m, r);
+      pro_compute_row<QW, 0>(a, m, r, a_lds, as_lds, blk);
     }
     const int8_t *arow = a_lds + (lr < M ? lr : 0) * K + lg * 16;
 #pragma unroll
@@ -558,7 +617,7 @@ __global__ void __launch_bounds__(256) qkv_heads_kernel(QkvHeadArgs a) {
   if (lane == 0) *sp = scale;
 }
 
-template <int GPW, int KSTEPS, int NT, int NMAT>
+template <int GPW, int KSTEPS, int NT, int NMAT, int PART>
 hipError_t launch_t(const GemvArgs &a, int ncols, hipStream_t s) {
   constexpr int NB = 16 * NT;
   // the prologue gives each wave GPW * KSTEPS / 4 groups of 256 columns
@@ -568,17 +627,32 @@ hipError_t launch_t(const GemvArgs &a, int ncols, hipStream_t s) {
   if (a.pro != PRO_NONE)
     lds += ((a.M * a.K + 15) & ~15) + sizeof(float) * (a.M * (a.K / 256) + a.K / 32);
   if (lds > 65536) return hipErrorInvalidValue;
-  Q3_LAUNCH((gemv_kernel<GPW, KSTEPS, NT, NMAT>), dim3(ncols / NB), dim3(256), lds, s, a);
+  Q3_LAUNCH((gemv_kernel<GPW, KSTEPS, NT, NMAT, PART>), dim3(ncols / NB), dim3(256), lds, s, a);
   return hipGetLastError();
 }
 
 template <int NT, int NMAT>
 hipError_t dispatch_k(const GemvArgs &a, int ncols, hipStream_t s) {
-  if (a.K == 1024 && a.group == 256) return launch_t<1, 4, NT, NMAT>(a, ncols, s);
-  if (a.K == 1024 && a.group == 128) return launch_t<2, 2, NT, NMAT>(a, ncols, s);
-  if (a.K == 2048 && a.group == 128) return launch_t<4, 2, NT, NMAT>(a, ncols, s);
-  if (a.K == 2048 && a.group == 256) return launch_t<2, 4, NT, NMAT>(a, ncols, s);
-  if (a.K == 3072 && a.group == 256) return launch_t<3, 4, NT, NMAT>(a, ncols, s);
+  if (a.K == 1024 && a.group == 256) return launch_t<1, 4, NT, NMAT, 0>(a, ncols, s);
+  if (a.K == 1024 && a.group == 128) return launch_t<2, 2, NT, NMAT, 0>(a, ncols, s);
+  if (a.K == 2048 && a.group == 128) return launch_t<4, 2, NT, NMAT, 0>(a, ncols, s);
+  if (a.K == 2048 && a.group == 256) return launch_t<2, 4, NT, NMAT, 0>(a, ncols, s);
+  if (a.K == 3072 && a.group == 256) return launch_t<3, 4, NT, NMAT, 0>(a, ncols, s);
+  return hipErrorInvalidValue;
+}
+
+// With O projection partials (decode): the gate/up launch (PRO_NORM with
+// SWIGLU, K = hidden) and the down launch (EPI_ADD, K = intermediate),
+// group 256.
+template <int NMAT>
+hipError_t dispatch_part(const GemvArgs &a, int ncols, hipStream_t s) {
+  if (a.M != 1 || a.npart < 1 || a.npart > kMaxPart || a.nseg != 1 || a.group != 256) return hipErrorInvalidValue;
+  const bool pro = a.pro == PRO_NORM, epi = a.seg[0].epi == EPI_ADD;
+  if (pro == epi || a.ld_part < (pro ? a.K : ncols) ||
+      (reinterpret_cast<uintptr_t>(a.part) & 15) != 0 || (a.ld_part % 4) != 0)
+    return hipErrorInvalidValue;
+  if (pro && NMAT == 2 && a.K == 1024) return launch_t<1, 4, 1, NMAT, kPartPro>(a, ncols, s);
+  if (epi && NMAT == 1 && a.K == 3072) return launch_t<3, 4, 1, NMAT, kPartEpi>(a, ncols, s);
   return hipErrorInvalidValue;
 }
 
@@ -639,6 +713,7 @@ hipError_t launch_gemv(const GemvArgs &a, hipStream_t s) {
     return hipGetLastError();
   }
   const bool two = a.seg[0].epi == EPI_SWIGLU;
+  if (a.part) return two ? dispatch_part<2>(a, ncols, s) : dispatch_part<1>(a, ncols, s);
   if (two) return dispatch_k<1, 2>(a, ncols, s);
   if (ncols >= 65536) return dispatch_k<4, 1>(a, ncols, s);
   return dispatch_k<1, 1>(a, ncols, s);

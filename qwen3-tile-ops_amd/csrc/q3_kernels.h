@@ -243,6 +243,18 @@ struct AttnArgs {
   const int32_t *row_pos;
   const uint16_t *row_tables;
   int64_t ld_table;
+  // decode kernel with fuse_heads only: the O projection's per-head group
+  // partials (group = head, group_gemm.h:27-222 with ref_qwen3.py:145-158)
+  //   opart[h * ld_opart + n] = RN(RN(f32(o8_h . wo[n][128h, 128h + 128))
+  //                                   * wos[n]) * os_h),  n < o_rows
+  // are written by head h's workgroup; the residual add sums them in head
+  // order (GemvArgs::part).  wo: [o_rows][ldwo] int8.
+  const int8_t *wo;
+  const float *wos;
+  int64_t ldwo;
+  int o_rows;
+  float *opart;
+  int64_t ld_opart;
 };
 hipError_t launch_attention(const AttnArgs &a, hipStream_t s);
 
@@ -304,6 +316,13 @@ struct GemvArgs {
   GemvSeg seg[3];
   unsigned long long *keys;  // EPI_ARGMAX: [M][keys_ld] one key per workgroup
   int64_t keys_ld;
+  // O projection partials of the decode attention (AttnArgs::opart), M = 1:
+  // o = ((0 + part[0]) + part[1]) + ... + part[npart - 1] (1 <= npart <= 16,
+  // row stride ld_part).  PRO_NORM normalises x + o instead of x; EPI_ADD
+  // stores (dst + o) + out instead of dst + out (same columns as dst).
+  const float *part;
+  int npart;
+  int64_t ld_part;
 };
 bool gemv_supported(int M, int K, int group);
 // key slots per row that an EPI_ARGMAX launch writes (keys_ld must cover it)

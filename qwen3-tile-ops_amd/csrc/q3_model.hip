@@ -52,6 +52,9 @@ struct q3_model {
   unsigned long long *bkeys = nullptr;  // [seq][bkeys_ld]
   int64_t bkeys_ld = 0;
   float *bbest = nullptr;          // [seq] per-row argmax value
+  // decode (b = 1): the O projection's per-head partials [heads][hidden],
+  // written by the attention kernel, summed by the gate/up and down GEMVs
+  float *opart = nullptr;
   // event timing of decode kernel classes (q3_model_set_kernel_timing)
   uint32_t kt_mask = 0;
   std::vector<hipEvent_t> kt_ev[Q3_KT_COUNT];  // start, end pairs
@@ -61,6 +64,9 @@ struct q3_model {
   // decode: workgroups that prefetch the next kernels' weights during the
   // attention kernel (Q3_DECODE_PREFETCH_WGS, default 128; 0 disables)
   int pf_wgs;
+  // decode: O projection folded into the attention kernel
+  // (Q3_DECODE_FUSE_OPROJ, default 1; 0 runs it as its own GEMV)
+  bool ofuse = true;
 };
 
 namespace q3 {
@@ -434,9 +440,30 @@ int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int opti
     t.os = os + static_cast<int64_t>(tr0) * y.heads;
     t.ldos = y.heads;
     t.os_col = 1;
-    // one decode token: the head epilogues run in the attention prologue
+    // one decode token: the head epilogues run in the attention prologue,
+    // and the O projection in its epilogue (per-head partials into opart)
     const bool fuse = do_tail && rows == 1 && q3::attn_decode_supported(t);
+    bool ofuse = false;
     if (fuse) {
+      q3::AttnArgs to = t;
+      to.fuse_heads = 1;
+      to.wo = lp.wo;
+      to.wos = lp.wos;
+      to.ldwo = QW;
+      to.o_rows = H;
+      to.opart = m->opart;
+      to.ld_opart = H;
+      ofuse = m->ofuse && q3::attn_decode_supported(to);
+    }
+    if (fuse) {
+      if (ofuse) {
+        t.wo = lp.wo;
+        t.wos = lp.wos;
+        t.ldwo = QW;
+        t.o_rows = H;
+        t.opart = m->opart;
+        t.ld_opart = H;
+      }
       t.fuse_heads = 1;
       t.fq = q;
       t.fk = k;
@@ -455,7 +482,9 @@ int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int opti
         t.pf_bytes[t.pf_n] = bytes;
         ++t.pf_n;
       };
-      add_pf(lp.wo, HH * QW);
+      // (with the O projection fused, this layer's Wo is read by the
+      // attention itself, so the next layer's is fetched instead)
+      if (!ofuse) add_pf(lp.wo, HH * QW);
       add_pf(lp.wg, static_cast<int64_t>(I) * H);
       add_pf(lp.wu, static_cast<int64_t>(I) * H);
       add_pf(lp.wd, HH * I);
@@ -464,6 +493,7 @@ int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int opti
         add_pf(nx.wq, static_cast<int64_t>(QW) * H);
         add_pf(nx.wk, static_cast<int64_t>(KW) * H);
         add_pf(nx.wv, static_cast<int64_t>(KW) * H);
+        if (ofuse) add_pf(nx.wo, HH * QW);
       }
       // the K/V pages (and scales) the next attention reads: the next
       // layer's, or layer 0's for the next token after the last layer
@@ -535,8 +565,9 @@ int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int opti
       Q3_HIP(q3::launch_attention(t, s));
     }
     float *xt = x + static_cast<int64_t>(tr0) * H;
-    // O projection (group = head_dim) + residual
-    {
+    // O projection (group = head_dim) + residual (unless the attention
+    // computed its partials: then the next two launches add them)
+    if (!ofuse) {
       q3::GemvArgs g = gemv_args(M, QW, HD);
       g.a = o8 + static_cast<int64_t>(tr0) * QW;
       g.lda = QW;
@@ -562,6 +593,11 @@ int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int opti
       g.seg[0] = gemv_seg(0, I, q3::EPI_SWIGLU, lp.wg, lp.wgs, sw + static_cast<int64_t>(tr0) * I, I);
       g.seg[0].b2 = lp.wu;
       g.seg[0].bs2 = lp.wus;
+      if (ofuse) {  // normalises x + O
+        g.part = m->opart;
+        g.npart = static_cast<int>(y.heads);
+        g.ld_part = H;
+      }
       KTimer kt(m, Q3_KT_GEMV_GATE_UP);
       Q3_HIP(q3::launch_gemv(g, s));
     }
@@ -575,6 +611,11 @@ int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int opti
       g.hs_out = ss + static_cast<int64_t>(tr0) * (I / 256);
       g.nseg = 1;
       g.seg[0] = gemv_seg(0, H, q3::EPI_ADD, lp.wd, lp.wds, xt, H);
+      if (ofuse) {  // x = (x + O) + down
+        g.part = m->opart;
+        g.npart = static_cast<int>(y.heads);
+        g.ld_part = H;
+      }
       KTimer kt(m, Q3_KT_GEMV_DOWN);
       Q3_HIP(q3::launch_gemv(g, s));
     }
@@ -841,6 +882,7 @@ extern "C" int q3_model_open(void *blob, const q3_layout *lay, void *stream, q3_
   m->keys_ld = lay->vocab / 16 + 64;  // one key per lm_head column block
   m->pf_wgs = 128;
   if (const char *e = std::getenv("Q3_DECODE_PREFETCH_WGS")) m->pf_wgs = std::max(0, std::atoi(e));
+  if (const char *e = std::getenv("Q3_DECODE_FUSE_OPROJ")) m->ofuse = std::atoi(e) != 0;
   m->bkeys_ld = lay->vocab / 128 + 64;  // one key per 128-column block of the lm GEMM
   m->btab_off = (sizeof(int32_t) * lay->seq + 255) & ~size_t(255);
   const size_t bstate_bytes = m->btab_off + sizeof(uint16_t) * static_cast<size_t>(lay->seq) * m->n_pages;
@@ -854,7 +896,8 @@ extern "C" int q3_model_open(void *blob, const q3_layout *lay, void *stream, q3_
       hipEventCreateWithFlags(&m->bstage_ev[1], hipEventDisableTiming) != hipSuccess ||
       hipMalloc(&m->bkeys, sizeof(unsigned long long) * static_cast<size_t>(lay->seq) * m->bkeys_ld) !=
           hipSuccess ||
-      hipMalloc(&m->bbest, sizeof(float) * lay->seq) != hipSuccess) {
+      hipMalloc(&m->bbest, sizeof(float) * lay->seq) != hipSuccess ||
+      hipMalloc(&m->opart, sizeof(float) * lay->heads * lay->hidden) != hipSuccess) {
     q3_model_close(m);
     return Q3_ERR_HIP;
   }
@@ -1188,6 +1231,7 @@ extern "C" int q3_model_close(q3_model *m) {
   }
   if (m->bkeys) (void)hipFree(m->bkeys);
   if (m->bbest) (void)hipFree(m->bbest);
+  if (m->opart) (void)hipFree(m->opart);
   for (int c = 0; c < Q3_KT_COUNT; ++c)
     for (hipEvent_t e : m->kt_ev[c]) (void)hipEventDestroy(e);
   delete m;
