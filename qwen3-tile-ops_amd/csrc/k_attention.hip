@@ -114,7 +114,7 @@ __global__ void __launch_bounds__(256) attention_kernel(AttnArgs a) {
 
   // ---- prologue: page ids, exp table, row state, Q fragments ----
   for (int b = tid; b < min(nblk, PGW); b += 256) pg[b] = a.table[static_cast<uint32_t>(b) / ppb];
-  if (tid < 32) etab[tid] = kExp2Tab[tid];
+  if (tid == 0) stage_exp2_table(etab);
   for (int i = tid; i < QB * 32; i += 256) p8[i / 32][32 + i % 32] = 0;
   for (int i = tid; i < HD * 32; i += 256) vt[i / 32][32 + i % 32] = 0;
   if (tid < QB) {

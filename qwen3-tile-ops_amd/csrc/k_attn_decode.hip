@@ -124,7 +124,7 @@ struct FusedRegs {
 };
 
 // wave 0: K head kvh, wave 1: V head kvh, waves 2..: query heads qh0 + h.
-// Every wave issues the same seven loads (waves past the heads repeat wave
+// Every wave issues the same six loads (waves past the heads repeat wave
 // 0's, the V wave loads gains it does not use): with a fixed count the
 // compiler's waits after them stay exact.
 template <int QPW>
@@ -139,7 +139,7 @@ __device__ __forceinline__ void fused_load(const AttnArgs &a, int kvh, int qh0, 
   r.w1 = nw[lane + 64];
   r.c = a.cos_row[lane];
   r.s = a.sin_row[lane];
-  r.page = a.table[(a.kv_len - 1) / a.page_tokens];
+  r.page = a.new_page;
 }
 
 template <int QPW, class SM>
@@ -227,16 +227,18 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
   // i % 8 (round-robin dispatch), so the KV-head groups of one sequence are
   // given ids with equal residues and share that XCD's L2 (the per-row scale
   // sectors and page table lines they have in common).
+  // (the fused b = 1 variants never have row_pos: no test of it there)
+  const bool batch = !FUSE && a.row_pos;
   int bx = static_cast<int>(blockIdx.x), by = static_cast<int>(blockIdx.y);
-  if (a.row_pos && (gridDim.y & 7) == 0) {
+  if (batch && (gridDim.y & 7) == 0) {
     const int nx = static_cast<int>(gridDim.x);
     const int id = bx + nx * by;
     const int slot = id >> 3;
     by = (id & 7) + 8 * (slot / nx);
     bx = slot % nx;
   }
-  const int brow = a.row_pos ? by : 0;
-  const uint16_t *table = a.row_pos ? a.row_tables + brow * a.ld_table : a.table;
+  const int brow = batch ? by : 0;
+  const uint16_t *table = batch ? a.row_tables + brow * a.ld_table : a.table;
   const int8_t *q8_row = a.q8 + brow * a.ldq;
   const float *qs_row = a.qs + brow * a.ldqs;
   int8_t *o8_row = a.o8 + brow * a.ldo;
@@ -248,7 +250,7 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
   const int qh0 = bx * QPW;
   const int kvh = qh0 / grp;
   const bool kv_writer = (qh0 % grp) == 0;
-  const uint32_t kv_len = a.row_pos ? static_cast<uint32_t>(a.row_pos[brow]) + 1 : a.kv_len;
+  const uint32_t kv_len = batch ? static_cast<uint32_t>(a.row_pos[brow]) + 1 : a.kv_len;
   // one query row: pos0 = kv_len - 1, so kv_end = kv_len and the causal mask
   // only removes keys >= kv_len (attention_gqa.h:454-458)
   const int pos0 = static_cast<int>(kv_len) - 1;
@@ -268,15 +270,14 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
   // The exp table into LDS from immediates (no load to wait for; first
   // read in phase 3, after barriers), the first chunk's page ids, then the
   // prologue operands.
-  if (tid == 0) {
-#pragma unroll
-    for (int i = 0; i < 32; ++i) sm.tab[i] = kExp2Tab[i];
-  }
+  if (tid == 0) stage_exp2_table(sm.tab);
+  // (with FUSE from the arguments: a wave-uniform index, scalar loads)
+  static_assert(!FUSE || CB <= 32, "first chunk's page ids come from blk_page");
   uint32_t pgs0[BPW];
 #pragma unroll
   for (int i = 0; i < BPW; ++i) {
-    const int jblk = min(wave + NW * i, nblocks - 1);
-    pgs0[i] = table[static_cast<uint32_t>(jblk * 32) / a.page_tokens];
+    const int jblk = __builtin_amdgcn_readfirstlane(min(wave + NW * i, nblocks - 1));
+    pgs0[i] = FUSE ? a.blk_page[jblk] : table[static_cast<uint32_t>(jblk * 32) / a.page_tokens];
   }
   FusedRegs fr{};
   int8_t q8a = 0, q8b = 0;

@@ -162,7 +162,7 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(TileArgs a) {
     const int r = i / ngroups, g = i % ngroups;
     as_lds[i] = (m0 + r < M) ? a.as[static_cast<int64_t>(m0 + r) * a.ldas + g] : 0.0f;
   }
-  if (EPI == EPI_SWIGLUQ && threadIdx.x < 32) tab[threadIdx.x] = kExp2Tab[threadIdx.x];
+  if (EPI == EPI_SWIGLUQ && threadIdx.x == 0) stage_exp2_table(tab);
   float bsv[NMAT][NT];
 #pragma unroll
   for (int mi = 0; mi < NMAT; ++mi)

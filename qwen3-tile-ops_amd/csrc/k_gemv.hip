@@ -297,10 +297,7 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
   }
   // the exp table from immediates (a load here would be issued after the
   // weights and waited for with them); first read after barriers
-  if (NMAT == 2 && threadIdx.x == 0) {
-#pragma unroll
-    for (int i = 0; i < 32; ++i) exptab[i] = kExp2Tab[i];
-  }
+  if (NMAT == 2 && threadIdx.x == 0) stage_exp2_table(exptab);
 
   if (a.pro != PRO_NONE) {
     pro_compute_row<QW, NPRO>(a, 0, r0, a_lds, as_lds, blk);

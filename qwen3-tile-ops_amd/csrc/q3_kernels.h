@@ -226,6 +226,13 @@ struct AttnArgs {
   // K norm+RoPE+quant and V quant into their page slots, Q norm+RoPE+quant
   // into q8/qs (which must then be writable).
   int fuse_heads;
+  // with fuse_heads: the page ids of the first 32 key blocks
+  // (blk_page[j] = table[32 j / page_tokens], j < min(32, blocks)) and of
+  // the new token (table[(kv_len - 1) / page_tokens]), copied from the
+  // caller's host mirror of the table, so that the first K/V addresses come
+  // from kernel arguments instead of a table load
+  uint32_t blk_page[32];
+  uint32_t new_page;
   const float *fq, *fk, *fv;
   const float *nq, *nk;
   const float *cos_row, *sin_row;

@@ -456,6 +456,12 @@ int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int opti
       ofuse = m->ofuse && q3::attn_decode_supported(to);
     }
     if (fuse) {
+      // page ids of the first key blocks and of the new token, from the
+      // host mirror of the table
+      const uint32_t kv_len = pos + rows;
+      const uint32_t nblk = std::min<uint32_t>(32, (kv_len + 31) / 32);
+      for (uint32_t j = 0; j < nblk; ++j) t.blk_page[j] = m->htab[j * 32 / kPageTokens];
+      t.new_page = m->htab[(kv_len - 1) / kPageTokens];
       if (ofuse) {
         t.wo = lp.wo;
         t.wos = lp.wos;
