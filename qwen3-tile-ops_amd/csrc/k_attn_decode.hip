@@ -117,6 +117,70 @@ constexpr int kOPieces = 11;
 // consumed): all of them at once do not fit the register file
 constexpr int kOPiecesEarly = 6;
 
+// The kernel arguments the first K/V loads depend on, read together and
+// pinned in SGPRs in the fused variants: otherwise the K/V addresses wait on
+// a chain of scalar-cache round trips (each read issued where it is first
+// needed).
+struct HotArgs {
+  uint32_t kv_len, page_tokens, new_page;
+  const int8_t *k, *v;
+  const float *ks, *vs;
+  int64_t page_bytes, row_bytes, scale_page_bytes, scale_row_bytes;
+  const float *fq, *fk, *fv, *nq, *nk, *cos_row, *sin_row;
+  const float *wos;
+  int o_rows;
+};
+
+template <bool PIN, bool OFUSE>
+__device__ __forceinline__ HotArgs hot_args(const AttnArgs &a) {
+  HotArgs h;
+  h.kv_len = a.kv_len;
+  h.page_tokens = a.page_tokens;
+  h.new_page = a.new_page;
+  h.k = a.k;
+  h.v = a.v;
+  h.ks = a.ks;
+  h.vs = a.vs;
+  h.page_bytes = a.page_bytes;
+  h.row_bytes = a.row_bytes;
+  h.scale_page_bytes = a.scale_page_bytes;
+  h.scale_row_bytes = a.scale_row_bytes;
+  h.fq = a.fq;
+  h.fk = a.fk;
+  h.fv = a.fv;
+  h.nq = a.nq;
+  h.nk = a.nk;
+  h.cos_row = a.cos_row;
+  h.sin_row = a.sin_row;
+  h.wos = OFUSE ? a.wos : nullptr;
+  h.o_rows = OFUSE ? a.o_rows : 0;
+  if constexpr (PIN) {
+    h.kv_len = pin_sgpr(h.kv_len);
+    h.page_tokens = pin_sgpr(h.page_tokens);
+    h.new_page = pin_sgpr(h.new_page);
+    h.k = pin_sgpr(h.k);
+    h.v = pin_sgpr(h.v);
+    h.ks = pin_sgpr(h.ks);
+    h.vs = pin_sgpr(h.vs);
+    h.page_bytes = pin_sgpr(h.page_bytes);
+    h.row_bytes = pin_sgpr(h.row_bytes);
+    h.scale_page_bytes = pin_sgpr(h.scale_page_bytes);
+    h.scale_row_bytes = pin_sgpr(h.scale_row_bytes);
+    h.fq = pin_sgpr(h.fq);
+    h.fk = pin_sgpr(h.fk);
+    h.fv = pin_sgpr(h.fv);
+    h.nq = pin_sgpr(h.nq);
+    h.nk = pin_sgpr(h.nk);
+    h.cos_row = pin_sgpr(h.cos_row);
+    h.sin_row = pin_sgpr(h.sin_row);
+    if constexpr (OFUSE) {
+      h.wos = pin_sgpr(h.wos);
+      h.o_rows = pin_sgpr(h.o_rows);
+    }
+  }
+  return h;
+}
+
 // Operands of the fused head epilogue of one wave (see fused_load).
 struct FusedRegs {
   float t0, t1, w0, w1, c, s;
@@ -128,7 +192,7 @@ struct FusedRegs {
 // 0's, the V wave loads gains it does not use): with a fixed count the
 // compiler's waits after them stay exact.
 template <int QPW>
-__device__ __forceinline__ void fused_load(const AttnArgs &a, int kvh, int qh0, int wave, int lane,
+__device__ __forceinline__ void fused_load(const HotArgs &a, int kvh, int qh0, int wave, int lane,
                                            FusedRegs &r) {
   const int w = wave < 2 + QPW ? wave : 0;
   const float *src = w == 0 ? a.fk + kvh * HD : w == 1 ? a.fv + kvh * HD : a.fq + (qh0 + w - 2) * HD;
@@ -143,10 +207,10 @@ __device__ __forceinline__ void fused_load(const AttnArgs &a, int kvh, int qh0, 
 }
 
 template <int QPW, class SM>
-__device__ void fused_compute(const AttnArgs &a, SM &sm, FusedRegs r, int kvh, int qh0,
+__device__ void fused_compute(const AttnArgs &a, const HotArgs &h, SM &sm, FusedRegs r, int kvh, int qh0,
                               bool kv_writer, int wave, int lane) {
   if (wave >= 2 + QPW) return;
-  const uint32_t t = a.kv_len - 1;  // the new token
+  const uint32_t t = h.kv_len - 1;  // the new token
   float t0 = r.t0, t1 = r.t1;
   if (wave != 1) head_norm_rope_regs(t0, t1, r.w0, r.w1, r.c, r.s, a.inv_hd, true);
   const float mx = max64(fmaxf(fabsf(t0), fabsf(t1)));
@@ -160,11 +224,11 @@ __device__ void fused_compute(const AttnArgs &a, SM &sm, FusedRegs r, int kvh, i
     lsp = wave == 0 ? &sm.ksnew : &sm.vsnew;
     if (kv_writer) {
       const uint32_t page = r.page;
-      const uint32_t slot = t % a.page_tokens;
-      int8_t *row8 = const_cast<int8_t *>(wave == 0 ? a.k : a.v) + page * a.page_bytes +
-                     slot * a.row_bytes + kvh * HD;
-      float *sp = reinterpret_cast<float *>(reinterpret_cast<int8_t *>(const_cast<float *>(wave == 0 ? a.ks : a.vs)) +
-                                            page * a.scale_page_bytes + slot * a.scale_row_bytes) + kvh;
+      const uint32_t slot = t % h.page_tokens;
+      int8_t *row8 = const_cast<int8_t *>(wave == 0 ? h.k : h.v) + page * h.page_bytes +
+                     slot * h.row_bytes + kvh * HD;
+      float *sp = reinterpret_cast<float *>(reinterpret_cast<int8_t *>(const_cast<float *>(wave == 0 ? h.ks : h.vs)) +
+                                            page * h.scale_page_bytes + slot * h.scale_row_bytes) + kvh;
       row8[lane] = q0;
       row8[lane + 64] = q1;
       if (lane == 0) *sp = scale;
@@ -217,10 +281,19 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
   static_assert(!OFUSE || (FUSE && QPW == 1), "O projection fusion: one head per workgroup");
   __shared__ __align__(16) Smem<QPW, CB> sm;
   __shared__ __align__(16) SmemO<OFUSE> smo;
-  if (static_cast<int>(blockIdx.x) >= a.heads / QPW) {  // prefetch workgroups
+  // prefetch workgroups: grid rows y >= 1 of the fused (b = 1) variants, so
+  // that telling them apart needs no kernel argument; else x >= heads / QPW
+  if constexpr (FUSE) {
+    if (blockIdx.y > 0) {
+      const int w = static_cast<int>((blockIdx.y - 1) * gridDim.x + blockIdx.x);
+      if (w < a.pf_wgs) prefetch_ranges(a, w);
+      return;
+    }
+  } else if (static_cast<int>(blockIdx.x) >= a.heads / QPW) {
     prefetch_ranges(a, static_cast<int>(blockIdx.x) - a.heads / QPW);
     return;
   }
+  const HotArgs h = hot_args<FUSE, OFUSE>(a);
   // a batch of independent sequences: sequence blockIdx.y's length, pages
   // and rows of q8/qs/o8/os
   // Batches whose row count is a multiple of 8: workgroup i runs on XCD
@@ -250,7 +323,7 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
   const int qh0 = bx * QPW;
   const int kvh = qh0 / grp;
   const bool kv_writer = (qh0 % grp) == 0;
-  const uint32_t kv_len = batch ? static_cast<uint32_t>(a.row_pos[brow]) + 1 : a.kv_len;
+  const uint32_t kv_len = batch ? static_cast<uint32_t>(a.row_pos[brow]) + 1 : h.kv_len;
   // one query row: pos0 = kv_len - 1, so kv_end = kv_len and the causal mask
   // only removes keys >= kv_len (attention_gqa.h:454-458)
   const int pos0 = static_cast<int>(kv_len) - 1;
@@ -277,7 +350,7 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
 #pragma unroll
   for (int i = 0; i < BPW; ++i) {
     const int jblk = __builtin_amdgcn_readfirstlane(min(wave + NW * i, nblocks - 1));
-    pgs0[i] = FUSE ? a.blk_page[jblk] : table[static_cast<uint32_t>(jblk * 32) / a.page_tokens];
+    pgs0[i] = FUSE ? a.blk_page[jblk] : table[static_cast<uint32_t>(jblk * 32) / h.page_tokens];
   }
   FusedRegs fr{};
   int8_t q8a = 0, q8b = 0;
@@ -285,10 +358,10 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
   constexpr int kWosPerThread = (kORowsMax + NW * 64 - 1) / (NW * 64);
   float wosr[OFUSE ? kWosPerThread : 1];
   if constexpr (FUSE) {
-    fused_load<QPW>(a, kvh, qh0, wave, lane, fr);
+    fused_load<QPW>(h, kvh, qh0, wave, lane, fr);
     if constexpr (OFUSE) {
 #pragma unroll
-      for (int i = 0; i < kWosPerThread; ++i) wosr[i] = a.wos[min(tid + i * NW * 64, a.o_rows - 1)];
+      for (int i = 0; i < kWosPerThread; ++i) wosr[i] = h.wos[min(tid + i * NW * 64, h.o_rows - 1)];
     }
   } else {
     const int qh = qh0 + min(wave, QPW - 1);  // every wave loads (fixed count)
@@ -311,7 +384,7 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
     const int64_t col = live ? static_cast<int64_t>(qh0) * HD + 16 * (tid & 7) : 0;
 #pragma unroll
     for (int i = i0; i < i1; ++i) {
-      const int n = live ? min(i * NW * 8 + tid / 8, a.o_rows - 1) : 0;
+      const int n = live ? min(i * NW * 8 + tid / 8, h.o_rows - 1) : 0;
       wov[i] = *reinterpret_cast<const int4 *>(a.wo + n * a.ldwo + col);
     }
   };
@@ -325,7 +398,7 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < BPW; ++i) {
       const int jblk = min(b0 + wave + NW * i, nblocks - 1);
-      pgs[i] = table[static_cast<uint32_t>(jblk * 32) / a.page_tokens];
+      pgs[i] = table[static_cast<uint32_t>(jblk * 32) / h.page_tokens];
     }
   };
 
@@ -349,15 +422,15 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
       const int j = min(b0 + wave + NW * i, nblocks - 1) * 32;
       const int last = kv_end - 1 - j;  // >= 0: the block holds key kv_end - 1 or is full
       const uint32_t page = pgs[i];
-      const uint32_t slot0 = static_cast<uint32_t>(j) % a.page_tokens;
-      const int8_t *kb = a.k + page * a.page_bytes + slot0 * a.row_bytes + kvh * HD;
-      const int8_t *vb = a.v + page * a.page_bytes + slot0 * a.row_bytes + kvh * HD;
-      const int8_t *ksb = reinterpret_cast<const int8_t *>(a.ks) + page * a.scale_page_bytes +
-                          slot0 * a.scale_row_bytes;
-      const int8_t *vsb = reinterpret_cast<const int8_t *>(a.vs) + page * a.scale_page_bytes +
-                          slot0 * a.scale_row_bytes;
+      const uint32_t slot0 = static_cast<uint32_t>(j) % h.page_tokens;
+      const int8_t *kb = h.k + page * h.page_bytes + slot0 * h.row_bytes + kvh * HD;
+      const int8_t *vb = h.v + page * h.page_bytes + slot0 * h.row_bytes + kvh * HD;
+      const int8_t *ksb = reinterpret_cast<const int8_t *>(h.ks) + page * h.scale_page_bytes +
+                          slot0 * h.scale_row_bytes;
+      const int8_t *vsb = reinterpret_cast<const int8_t *>(h.vs) + page * h.scale_page_bytes +
+                          slot0 * h.scale_row_bytes;
       const int kr = min(kc, last);
-      const int4 *kp = reinterpret_cast<const int4 *>(kb + kr * a.row_bytes + half * 64);
+      const int4 *kp = reinterpret_cast<const int4 *>(kb + kr * h.row_bytes + half * 64);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int4 v = kp[e];
@@ -366,11 +439,11 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
         kw[i][4 * e + 2] = v.z;
         kw[i][4 * e + 3] = v.w;
       }
-      kscale[i] = reinterpret_cast<const float *>(ksb + kr * a.scale_row_bytes)[kvh];
+      kscale[i] = reinterpret_cast<const float *>(ksb + kr * h.scale_row_bytes)[kvh];
 #pragma unroll
       for (int cc = 0; cc < 16; ++cc)
-        vw[i][cc] = *reinterpret_cast<const int *>(vb + min(kh + cc, last) * a.row_bytes + d0);
-      vscale[i] = reinterpret_cast<const float *>(vsb + min(lane & 31, last) * a.scale_row_bytes)[kvh];
+        vw[i][cc] = *reinterpret_cast<const int *>(vb + min(kh + cc, last) * h.row_bytes + d0);
+      vscale[i] = reinterpret_cast<const float *>(vsb + min(lane & 31, last) * h.scale_row_bytes)[kvh];
     };
     // 22 loads per block: the last block is issued after the prologue, so
     // that the prologue does not stall on a full load counter (vmcnt holds
@@ -387,7 +460,7 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
           if (tid + i * NW * 64 < kORowsMax) smo.wos[tid + i * NW * 64] = wosr[i];
       }
       if constexpr (FUSE) {
-        fused_compute<QPW>(a, sm, fr, kvh, qh0, kv_writer, wave, lane);
+        fused_compute<QPW>(a, h, sm, fr, kvh, qh0, kv_writer, wave, lane);
       } else if (wave < QPW) {
         sm.q8[wave][lane] = q8a;
         sm.q8[wave][lane + 64] = q8b;
@@ -573,7 +646,7 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
       acc += lane_xor<2>(acc);
       acc += lane_xor<4>(acc);
       const int n = i * NW * 8 + tid / 8;
-      if ((tid & 7) == 0 && n < a.o_rows) dst[n] = __fmul_rn(__fmul_rn(static_cast<float>(acc), smo.wos[n]), osh);
+      if ((tid & 7) == 0 && n < h.o_rows) dst[n] = __fmul_rn(__fmul_rn(static_cast<float>(acc), smo.wos[n]), osh);
     }
   }
 }
@@ -597,11 +670,13 @@ hipError_t launch_decode(const AttnArgs &a, hipStream_t s) {
   const int extra = a.pf_n > 0 ? a.pf_wgs : 0;
   const int seqs = a.row_pos ? a.rows : 1;
   static_assert(kOPieces * NW * 8 >= kORowsMax, "O projection rows per workgroup");
+  // fused: the prefetch workgroups are grid rows 1.. (ids after the heads')
+  const int hx = a.heads / QPW;
+  const dim3 fgrid(hx, 1 + (extra + hx - 1) / hx);
   if (a.fuse_heads && a.opart)
-    Q3_LAUNCH((attn_decode_kernel<QPW, NW, BPW, true, true>), dim3(a.heads / QPW + extra, seqs), dim3(NW * 64), 0,
-              s, a);
+    Q3_LAUNCH((attn_decode_kernel<QPW, NW, BPW, true, true>), fgrid, dim3(NW * 64), 0, s, a);
   else if (a.fuse_heads)
-    Q3_LAUNCH((attn_decode_kernel<QPW, NW, BPW, true>), dim3(a.heads / QPW + extra, seqs), dim3(NW * 64), 0, s, a);
+    Q3_LAUNCH((attn_decode_kernel<QPW, NW, BPW, true>), fgrid, dim3(NW * 64), 0, s, a);
   else
     Q3_LAUNCH((attn_decode_kernel<QPW, NW, BPW, false>), dim3(a.heads / QPW + extra, seqs), dim3(NW * 64), 0, s, a);
   return hipGetLastError();

@@ -64,27 +64,99 @@ struct ProRow {
   uint32_t e[QW];   // four int8 embedding values (PRO_EMBED)
   float esc;        // embedding row scale
   float4 p[QW][NP > 0 ? NP : 1];  // O projection partials (GemvArgs::part)
+  int npart;
 };
 
-template <int QW, int NP>
-__device__ __forceinline__ void pro_load_row(const GemvArgs &a, int m, ProRow<QW, NP> &r) {
+// The kernel arguments the first loads depend on (prologue sources, O
+// partials, the unfused A operand), read together at the top of the kernel
+// and pinned in SGPRs (pin_src): each read waiting for the one before costs
+// a scalar-cache round trip.
+struct ProSrc {
+  const float *x;
+  int64_t ldx;
+  const float *w;
+  const int8_t *emb;
+  const float *emb_s;
+  const int32_t *ids;
+  int64_t vocab;
+  const float *part;
+  int npart;
+  int64_t ld_part;
+  const int8_t *a;
+  int64_t lda;
+  const float *as;
+  int64_t ldas;
+};
+
+template <int PRO, bool PART>
+__device__ __forceinline__ ProSrc read_src(const GemvArgs &a) {
+  ProSrc p{};
+  if constexpr (PRO == PRO_EMBED) {
+    p.emb = a.emb;
+    p.emb_s = a.emb_s;
+    p.ids = a.ids;
+    p.vocab = a.vocab;
+  } else if constexpr (PRO != PRO_NONE) {
+    p.x = a.x;
+    p.ldx = a.ldx;
+  } else {
+    p.a = a.a;
+    p.lda = a.lda;
+    p.as = a.as;
+    p.ldas = a.ldas;
+  }
+  if constexpr (PRO == PRO_NORM || PRO == PRO_EMBED) p.w = a.w_pre;
+  if constexpr (PART) {
+    p.part = a.part;
+    p.npart = a.npart;
+    p.ld_part = a.ld_part;
+  }
+  return p;
+}
+
+template <int PRO, bool PART>
+__device__ __forceinline__ void pin_src(ProSrc &p) {
+  if constexpr (PRO == PRO_EMBED) {
+    p.emb = pin_sgpr(p.emb);
+    p.emb_s = pin_sgpr(p.emb_s);
+    p.ids = pin_sgpr(p.ids);
+    p.vocab = pin_sgpr(p.vocab);
+  } else if constexpr (PRO != PRO_NONE) {
+    p.x = pin_sgpr(p.x);
+    p.ldx = pin_sgpr(p.ldx);
+  } else {
+    p.a = pin_sgpr(p.a);
+    p.lda = pin_sgpr(p.lda);
+    p.as = pin_sgpr(p.as);
+    p.ldas = pin_sgpr(p.ldas);
+  }
+  if constexpr (PRO == PRO_NORM || PRO == PRO_EMBED) p.w = pin_sgpr(p.w);
+  if constexpr (PART) {
+    p.part = pin_sgpr(p.part);
+    p.npart = pin_sgpr(p.npart);
+    p.ld_part = pin_sgpr(p.ld_part);
+  }
+}
+
+template <int PRO, int QW, int NP>
+__device__ __forceinline__ void pro_load_row(const GemvArgs &a, const ProSrc &ps, int m, ProRow<QW, NP> &r) {
   const int lane = threadIdx.x & 63;
   const int wave = wave_id();
   const int K = a.K;
-  if (a.pro == PRO_EMBED) {
-    const int32_t id = a.ids[m];
-    const bool ok = id >= 0 && id < a.vocab;  // out-of-range ids embed to zero
-    r.esc = ok ? a.emb_s[id] : 0.0f;
+  if constexpr (PRO == PRO_EMBED) {
+    const int32_t id = ps.ids[m];
+    const bool ok = id >= 0 && id < ps.vocab;  // out-of-range ids embed to zero
+    r.esc = ok ? ps.emb_s[id] : 0.0f;
 #pragma unroll
     for (int q = 0; q < QW; ++q) {
       const int c = (wave + 4 * q) * 256 + 4 * lane;
-      r.e[q] = ok ? *reinterpret_cast<const uint32_t *>(a.emb + static_cast<int64_t>(id) * K + c) : 0u;
+      r.e[q] = ok ? *reinterpret_cast<const uint32_t *>(ps.emb + static_cast<int64_t>(id) * K + c) : 0u;
     }
   } else {
 #pragma unroll
     for (int q = 0; q < QW; ++q) {
       const int c = (wave + 4 * q) * 256 + 4 * lane;
-      r.x[q] = *reinterpret_cast<const float4 *>(a.x + static_cast<int64_t>(m) * a.ldx + c);
+      r.x[q] = *reinterpret_cast<const float4 *>(ps.x + static_cast<int64_t>(m) * ps.ldx + c);
     }
     // the O projection partials (row 0 only; every row of the fixed count is
     // loaded, rows past npart repeat the last one and are not added)
@@ -95,19 +167,20 @@ __device__ __forceinline__ void pro_load_row(const GemvArgs &a, int m, ProRow<QW
           const int c = (wave + 4 * q) * 256 + 4 * lane;
 #pragma unroll
           for (int h = 0; h < NP; ++h)
-            r.p[q][h] = *reinterpret_cast<const float4 *>(a.part + min(h, a.npart - 1) * a.ld_part + c);
+            r.p[q][h] = *reinterpret_cast<const float4 *>(ps.part + min(h, ps.npart - 1) * ps.ld_part + c);
         }
+        r.npart = ps.npart;
       }
     }
   }
-  if (a.pro != PRO_QUANT) {
+  if constexpr (PRO != PRO_QUANT) {
 #pragma unroll
     for (int q = 0; q < QW; ++q)
-      r.w[q] = *reinterpret_cast<const float4 *>(a.w_pre + (wave + 4 * q) * 256 + 4 * lane);
+      r.w[q] = *reinterpret_cast<const float4 *>(ps.w + (wave + 4 * q) * 256 + 4 * lane);
   }
 }
 
-template <int QW, int NP>
+template <int PRO, int QW, int NP>
 __device__ void pro_compute_row(const GemvArgs &a, int m, const ProRow<QW, NP> &r, int8_t *a_lds,
                                 float *as_lds, float *blk) {
   const int lane = threadIdx.x & 63;
@@ -119,7 +192,7 @@ __device__ void pro_compute_row(const GemvArgs &a, int m, const ProRow<QW, NP> &
 #pragma unroll
   for (int q = 0; q < QW; ++q) {
     const int c = (wave + 4 * q) * 256 + 4 * lane;
-    if (a.pro == PRO_EMBED) {
+    if constexpr (PRO == PRO_EMBED) {
       const uint32_t e = r.e[q];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -139,7 +212,7 @@ __device__ void pro_compute_row(const GemvArgs &a, int m, const ProRow<QW, NP> &
           float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
           for (int h = 0; h < NP; ++h) {
-            if (h < a.npart) {
+            if (h < r.npart) {
               o[0] = __fadd_rn(o[0], r.p[q][h].x);
               o[1] = __fadd_rn(o[1], r.p[q][h].y);
               o[2] = __fadd_rn(o[2], r.p[q][h].z);
@@ -152,7 +225,7 @@ __device__ void pro_compute_row(const GemvArgs &a, int m, const ProRow<QW, NP> &
       }
     }
   }
-  if (a.pro != PRO_QUANT) {
+  if constexpr (PRO != PRO_QUANT) {
 #pragma unroll
     for (int q = 0; q < QW; ++q) {
       float s = __fadd_rn(__fadd_rn(__fmul_rn(v[q][0], v[q][0]), __fmul_rn(v[q][1], v[q][1])),
@@ -203,7 +276,7 @@ __device__ void pro_compute_row(const GemvArgs &a, int m, const ProRow<QW, NP> &
 // them in the PRO_NORM prologue, PART = kPartEpi in the EPI_ADD epilogue.
 constexpr int kMaxPart = 16;
 constexpr int kPartPro = 1, kPartEpi = 2;
-template <int GPW, int KSTEPS, int NT, int NMAT, int PART>
+template <int GPW, int KSTEPS, int NT, int NMAT, int PRO, int PART>
 __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
   static_assert(PART == 0 || NT == 1, "partials: one item column per thread");
   constexpr int NPRO = PART == kPartPro ? kMaxPart : 0;
@@ -220,8 +293,46 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
   const int G = a.group;
   const int ngroups = K / G;
   const int n_blk = blockIdx.x * NB;
-  int si = 0;
-  while (si + 1 < a.nseg && n_blk >= a.seg[si + 1].n0) ++si;
+  // The workgroup's segment: the fields the weight stream needs are
+  // selected from all three segments' fields, read at once (a search loop or
+  // an indexed read would make each kernel-argument read wait for the one
+  // before it); the epilogue's fields are read by index later, in the shadow
+  // of the weight loads.
+  // (pin_sgpr: the value exists in SGPRs here, so the compiler can neither
+  // turn the selects back into selected addresses nor delay the reads)
+  // (all reads first, then the pins: one wait for the whole batch)
+  ProSrc ps = read_src<PRO, PART != 0>(a);
+  int nseg = a.nseg;
+  int s_n0[3];
+  const int8_t *s_b[3], *s_b2[3];
+  const float *s_bs[3], *s_bs2[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    s_n0[i] = a.seg[i].n0;
+    s_b[i] = a.seg[i].b;
+    s_bs[i] = a.seg[i].bs;
+    s_b2[i] = NMAT == 2 ? a.seg[i].b2 : s_b[i];
+    s_bs2[i] = NMAT == 2 ? a.seg[i].bs2 : s_bs[i];
+  }
+  pin_src<PRO, PART != 0>(ps);
+  nseg = pin_sgpr(nseg);
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    s_n0[i] = pin_sgpr(s_n0[i]);
+    s_b[i] = pin_sgpr(s_b[i]);
+    s_bs[i] = pin_sgpr(s_bs[i]);
+    if constexpr (NMAT == 2) {
+      s_b2[i] = pin_sgpr(s_b2[i]);
+      s_bs2[i] = pin_sgpr(s_bs2[i]);
+    }
+  }
+  const int si = (nseg > 1 && n_blk >= s_n0[1] ? 1 : 0) + (nseg > 2 && n_blk >= s_n0[2] ? 1 : 0);
+  auto pick = [&](const auto (&v)[3]) { return si == 0 ? v[0] : si == 1 ? v[1] : v[2]; };
+  const int sg_n0 = pick(s_n0);
+  const int8_t *const sg_b = pick(s_b);
+  const int8_t *const sg_b2 = pick(s_b2);
+  const float *const sg_bs = pick(s_bs);
+  const float *const sg_bs2 = pick(s_bs2);
   const GemvSeg &sg = a.seg[si];
 
   // LDS: partials [NMAT][ngroups][16][PP] f32, then (prologue) A [M][K] i8
@@ -241,22 +352,22 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
   // waits for those operands alone (vmcnt(#weight loads)) instead of for
   // everything.
   ProRow<QW, NPRO> r0;
-  if (a.pro != PRO_NONE) pro_load_row<QW, NPRO>(a, 0, r0);
+  if constexpr (PRO != PRO_NONE) pro_load_row<PRO, QW, NPRO>(a, ps, 0, r0);
   // EPI_ADD with partials: those of the thread's item column, before the
   // weights (the column j = it % NB is the same for every item it of the
   // thread since 256 is a multiple of NB)
   float pe[NEPI > 0 ? NEPI : 1];
   if constexpr (NEPI > 0) {
-    const float *pc = a.part + (n_blk - sg.n0 + static_cast<int>(threadIdx.x) % NB);
+    const float *pc = ps.part + (n_blk - sg_n0 + static_cast<int>(threadIdx.x) % NB);
 #pragma unroll
-    for (int h = 0; h < NEPI; ++h) pe[h] = pc[min(h, a.npart - 1) * a.ld_part];
+    for (int h = 0; h < NEPI; ++h) pe[h] = pc[min(h, ps.npart - 1) * ps.ld_part];
   }
   // A operand rows and scales of the unfused path, also before the weights
   const bool avalid = lr < M;
   v4i av[GPW][KSTEPS];
   float asv[GPW][4];
-  if (a.pro == PRO_NONE) {
-    const int8_t *arow = a.a + static_cast<int64_t>(avalid ? lr : 0) * a.lda + lg * 16;
+  if constexpr (PRO == PRO_NONE) {
+    const int8_t *arow = ps.a + static_cast<int64_t>(avalid ? lr : 0) * ps.lda + lg * 16;
 #pragma unroll
     for (int gi = 0; gi < GPW; ++gi) {
       const int g = min(wave + 4 * gi, ngroups - 1);
@@ -268,7 +379,7 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int m = min(lg * 4 + i, M - 1);
-        asv[gi][i] = a.as[static_cast<int64_t>(m) * a.ldas + g];
+        asv[gi][i] = ps.as[static_cast<int64_t>(m) * ps.ldas + g];
       }
     }
   }
@@ -277,7 +388,7 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
 #pragma unroll
   for (int mi = 0; mi < NMAT; ++mi)
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) bsv[mi][nt] = (mi == 0 ? sg.bs : sg.bs2)[n_blk - sg.n0 + nt * 16 + lr];
+    for (int nt = 0; nt < NT; ++nt) bsv[mi][nt] = (mi == 0 ? sg_bs : sg_bs2)[n_blk - sg_n0 + nt * 16 + lr];
   v4i bv[NMAT][NT][GPW][KSTEPS];
 #pragma unroll
   for (int gi = 0; gi < GPW; ++gi) {
@@ -289,8 +400,8 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
       for (int mi = 0; mi < NMAT; ++mi)
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
-          const int8_t *b = (mi == 0 ? sg.b : sg.b2) +
-                            static_cast<int64_t>(n_blk - sg.n0 + nt * 16 + lr) * K;
+          const int8_t *b = (mi == 0 ? sg_b : sg_b2) +
+                            static_cast<int64_t>(n_blk - sg_n0 + nt * 16 + lr) * K;
           bv[mi][nt][gi][ks] = *reinterpret_cast<const v4i *>(b + k);
         }
     }
@@ -299,12 +410,12 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
   // weights and waited for with them); first read after barriers
   if (NMAT == 2 && threadIdx.x == 0) stage_exp2_table(exptab);
 
-  if (a.pro != PRO_NONE) {
-    pro_compute_row<QW, NPRO>(a, 0, r0, a_lds, as_lds, blk);
+  if constexpr (PRO != PRO_NONE) {
+    pro_compute_row<PRO, QW, NPRO>(a, 0, r0, a_lds, as_lds, blk);
     for (int m = 1; m < M; ++m) {
       ProRow<QW, 0> r;
-      pro_load_row<QW, 0>(a, m, r);
-      pro_compute_row<QW, 0>(a, m, r, a_lds, as_lds, blk);
+      pro_load_row<PRO, QW, 0>(a, ps, m, r);
+      pro_compute_row<PRO, QW, 0>(a, m, r, a_lds, as_lds, blk);
     }
     const int8_t *arow = a_lds + (avalid ? lr : 0) * K + lg * 16;
 #pragma unroll
@@ -349,7 +460,7 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
       out = __fadd_rn(out, part[(g * 16 + m) * PP + j]);
       if (NMAT == 2) out2 = __fadd_rn(out2, part[((ngroups + g) * 16 + m) * PP + j]);
     }
-    const int ncol = n_blk - sg.n0 + j;
+    const int ncol = n_blk - sg_n0 + j;
     if (sg.epi == EPI_ARGMAX) {
       unsigned long long key = 0ull;
       if (m < M)
@@ -372,7 +483,7 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
         float o = 0.0f;  // the O projection, partials in head order
 #pragma unroll
         for (int h = 0; h < NEPI; ++h)
-          if (h < a.npart) o = __fadd_rn(o, pe[h]);
+          if (h < ps.npart) o = __fadd_rn(o, pe[h]);
         base = __fadd_rn(base, o);
       }
       *dst = __fadd_rn(base, out);
@@ -391,7 +502,7 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
 // is reduced, and EPI_ARGMAX keeps one running key per row, written to slot
 // blockIdx.x at the end.  Items (row m, column j) map to threads so that a
 // row's NB = 64 columns are one wave.
-template <int GPW, int KSTEPS, int NT>
+template <int GPW, int KSTEPS, int NT, int PRO>
 __global__ void __launch_bounds__(256) gemv_stream_kernel(GemvArgs a, int ntiles) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int NB = 16 * NT;
@@ -412,8 +523,10 @@ __global__ void __launch_bounds__(256) gemv_stream_kernel(GemvArgs a, int ntiles
   float *as_lds = reinterpret_cast<float *>(a_lds + ((M * K + 15) & ~15));
   float *blk = as_lds + M * (K / 256);
 
+  ProSrc ps = read_src<PRO, false>(a);
+  pin_src<PRO, false>(ps);
   ProRow<QW, 0> r0;
-  if (a.pro != PRO_NONE) pro_load_row<QW, 0>(a, 0, r0);
+  if constexpr (PRO != PRO_NONE) pro_load_row<PRO, QW, 0>(a, ps, 0, r0);
 
   // a tile's column scales, then its weights: issued together one tile
   // ahead, so that using tile t waits only for loads issued before tile
@@ -439,8 +552,8 @@ __global__ void __launch_bounds__(256) gemv_stream_kernel(GemvArgs a, int ntiles
   // first tile (so that waiting for them does not wait for the tile)
   v4i av[GPW][KSTEPS];
   float asv[GPW][4];
-  if (a.pro == PRO_NONE) {
-    const int8_t *arow = a.a + static_cast<int64_t>(lr < M ? lr : 0) * a.lda + lg * 16;
+  if constexpr (PRO == PRO_NONE) {
+    const int8_t *arow = ps.a + static_cast<int64_t>(lr < M ? lr : 0) * ps.lda + lg * 16;
 #pragma unroll
     for (int gi = 0; gi < GPW; ++gi) {
       const int g = min(wave + 4 * gi, ngroups - 1);
@@ -450,7 +563,7 @@ __global__ void __launch_bounds__(256) gemv_stream_kernel(GemvArgs a, int ntiles
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int m = lg * 4 + i;
-        asv[gi][i] = m < M ? a.as[static_cast<int64_t>(m) * a.ldas + g] : 0.0f;
+        asv[gi][i] = m < M ? ps.as[static_cast<int64_t>(m) * ps.ldas + g] : 0.0f;
       }
     }
   }
@@ -460,12 +573,12 @@ __global__ void __launch_bounds__(256) gemv_stream_kernel(GemvArgs a, int ntiles
   float s0[NT], s1[NT];
   load_tile(b0, s0, t);
 
-  if (a.pro != PRO_NONE) {
-    pro_compute_row<QW, 0>(a, 0, r0, a_lds, as_lds, blk);
+  if constexpr (PRO != PRO_NONE) {
+    pro_compute_row<PRO, QW, 0>(a, 0, r0, a_lds, as_lds, blk);
     for (int m = 1; m < M; ++m) {
       ProRow<QW, 0> r;
-      pro_load_row<QW, 0>(a, m, r);
-      pro_compute_row<QW, 0>(a, m, r, a_lds, as_lds, blk);
+      pro_load_row<PRO, QW, 0>(a, ps, m, r);
+      pro_compute_row<PRO, QW, 0>(a, m, r, a_lds, as_lds, blk);
     }
     const int8_t *arow = a_lds + (lr < M ? lr : 0) * K + lg * 16;
 #pragma unroll
@@ -614,27 +727,47 @@ __global__ void __launch_bounds__(256) qkv_heads_kernel(QkvHeadArgs a) {
   if (lane == 0) *sp = scale;
 }
 
-template <int GPW, int KSTEPS, int NT, int NMAT, int PART>
+template <int GPW, int KSTEPS, int NT, int NMAT, int PRO, int PART>
 hipError_t launch_t(const GemvArgs &a, int ncols, hipStream_t s) {
   constexpr int NB = 16 * NT;
   // the prologue gives each wave GPW * KSTEPS / 4 groups of 256 columns
-  if (a.pro != PRO_NONE && a.K != 256 * GPW * KSTEPS) return hipErrorInvalidValue;
+  if (PRO != PRO_NONE && a.K != 256 * GPW * KSTEPS) return hipErrorInvalidValue;
   const int ngroups = a.K / a.group;
   size_t lds = sizeof(float) * NMAT * ngroups * 16 * (NB + 1);
-  if (a.pro != PRO_NONE)
+  if (PRO != PRO_NONE)
     lds += ((a.M * a.K + 15) & ~15) + sizeof(float) * (a.M * (a.K / 256) + a.K / 32);
   if (lds > 65536) return hipErrorInvalidValue;
-  Q3_LAUNCH((gemv_kernel<GPW, KSTEPS, NT, NMAT, PART>), dim3(ncols / NB), dim3(256), lds, s, a);
+  Q3_LAUNCH((gemv_kernel<GPW, KSTEPS, NT, NMAT, PRO, PART>), dim3(ncols / NB), dim3(256), lds, s, a);
   return hipGetLastError();
+}
+
+// The prologue kinds (a template parameter, so that no branch on a kernel
+// argument precedes the first loads) are built for K = 1024, 2048 and 3072
+// with group 256 and 16-column tiles.
+template <int NMAT, int PRO, int PART>
+hipError_t dispatch_pro(const GemvArgs &a, int ncols, hipStream_t s) {
+  if (a.group != 256) return hipErrorInvalidValue;
+  if (a.K == 1024) return launch_t<1, 4, 1, NMAT, PRO, PART>(a, ncols, s);
+  if (a.K == 2048) return launch_t<2, 4, 1, NMAT, PRO, PART>(a, ncols, s);
+  if (a.K == 3072) return launch_t<3, 4, 1, NMAT, PRO, PART>(a, ncols, s);
+  return hipErrorInvalidValue;
 }
 
 template <int NT, int NMAT>
 hipError_t dispatch_k(const GemvArgs &a, int ncols, hipStream_t s) {
-  if (a.K == 1024 && a.group == 256) return launch_t<1, 4, NT, NMAT, 0>(a, ncols, s);
-  if (a.K == 1024 && a.group == 128) return launch_t<2, 2, NT, NMAT, 0>(a, ncols, s);
-  if (a.K == 2048 && a.group == 128) return launch_t<4, 2, NT, NMAT, 0>(a, ncols, s);
-  if (a.K == 2048 && a.group == 256) return launch_t<2, 4, NT, NMAT, 0>(a, ncols, s);
-  if (a.K == 3072 && a.group == 256) return launch_t<3, 4, NT, NMAT, 0>(a, ncols, s);
+  if (a.pro == PRO_NONE) {
+    if (a.K == 1024 && a.group == 256) return launch_t<1, 4, NT, NMAT, PRO_NONE, 0>(a, ncols, s);
+    if (a.K == 1024 && a.group == 128) return launch_t<2, 2, NT, NMAT, PRO_NONE, 0>(a, ncols, s);
+    if (a.K == 2048 && a.group == 128) return launch_t<4, 2, NT, NMAT, PRO_NONE, 0>(a, ncols, s);
+    if (a.K == 2048 && a.group == 256) return launch_t<2, 4, NT, NMAT, PRO_NONE, 0>(a, ncols, s);
+    if (a.K == 3072 && a.group == 256) return launch_t<3, 4, NT, NMAT, PRO_NONE, 0>(a, ncols, s);
+    return hipErrorInvalidValue;
+  }
+  if constexpr (NT == 1) {
+    if (a.pro == PRO_NORM) return dispatch_pro<NMAT, PRO_NORM, 0>(a, ncols, s);
+    if (a.pro == PRO_EMBED) return dispatch_pro<NMAT, PRO_EMBED, 0>(a, ncols, s);
+    if (a.pro == PRO_QUANT) return dispatch_pro<NMAT, PRO_QUANT, 0>(a, ncols, s);
+  }
   return hipErrorInvalidValue;
 }
 
@@ -648,8 +781,11 @@ hipError_t dispatch_part(const GemvArgs &a, int ncols, hipStream_t s) {
   if (pro == epi || a.ld_part < (pro ? a.K : ncols) ||
       (reinterpret_cast<uintptr_t>(a.part) & 15) != 0 || (a.ld_part % 4) != 0)
     return hipErrorInvalidValue;
-  if (pro && NMAT == 2 && a.K == 1024) return launch_t<1, 4, 1, NMAT, kPartPro>(a, ncols, s);
-  if (epi && NMAT == 1 && a.K == 3072) return launch_t<3, 4, 1, NMAT, kPartEpi>(a, ncols, s);
+  if constexpr (NMAT == 2) {
+    if (pro && a.K == 1024) return launch_t<1, 4, 1, NMAT, PRO_NORM, kPartPro>(a, ncols, s);
+  } else {
+    if (epi && a.K == 3072 && a.pro == PRO_QUANT) return launch_t<3, 4, 1, NMAT, PRO_QUANT, kPartEpi>(a, ncols, s);
+  }
   return hipErrorInvalidValue;
 }
 
@@ -706,7 +842,14 @@ hipError_t launch_gemv(const GemvArgs &a, hipStream_t s) {
     const int ntiles = ncols / 64;
     const size_t lds = sizeof(float) * 4 * 16 * 65 +
                        (a.pro != PRO_NONE ? ((a.M * a.K + 15) & ~15) + sizeof(float) * (a.M * 4 + 32) : 0);
-    Q3_LAUNCH((gemv_stream_kernel<1, 4, 4>), dim3(stream_grid(ntiles)), dim3(256), lds, s, a, ntiles);
+    const dim3 grid(stream_grid(ntiles));
+    switch (a.pro) {
+      case PRO_NONE: Q3_LAUNCH((gemv_stream_kernel<1, 4, 4, PRO_NONE>), grid, dim3(256), lds, s, a, ntiles); break;
+      case PRO_NORM: Q3_LAUNCH((gemv_stream_kernel<1, 4, 4, PRO_NORM>), grid, dim3(256), lds, s, a, ntiles); break;
+      case PRO_EMBED: Q3_LAUNCH((gemv_stream_kernel<1, 4, 4, PRO_EMBED>), grid, dim3(256), lds, s, a, ntiles); break;
+      case PRO_QUANT: Q3_LAUNCH((gemv_stream_kernel<1, 4, 4, PRO_QUANT>), grid, dim3(256), lds, s, a, ntiles); break;
+      default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
   }
   const bool two = a.seg[0].epi == EPI_SWIGLU;

@@ -29,6 +29,27 @@ constexpr int kWave = 64;
 // value.  The compiler cannot prove threadIdx.x / 64 uniform by itself; it
 // would then keep per-lane copies of anything selected by the wave index
 // (argument pointers included) instead of scalar registers.
+// The value in SGPRs at this point (an empty asm that takes and returns it):
+// kernel-argument reads pinned this way are issued together at the top
+// instead of one after another where each is first used.
+template <class T>
+__device__ __forceinline__ T pin_sgpr(T v) {
+  asm volatile("" : "+s"(v));
+  return v;
+}
+// Pointers (kernel arguments point to global memory): the address goes
+// through the asm as an integer and comes back as a global-address-space
+// pointer, so that loads through it stay global loads (a plain pinned
+// pointer would lose its address space and become flat loads, which wait
+// on both counters).
+template <class T>
+__device__ __forceinline__ T *pin_sgpr(T *p) {
+  uint64_t v = reinterpret_cast<uint64_t>(p);
+  asm volatile("" : "+s"(v));
+  typedef __attribute__((address_space(1))) T *global_ptr;
+  return (T *)(global_ptr)v;
+}
+
 __device__ __forceinline__ int wave_id() {
   return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
 }
