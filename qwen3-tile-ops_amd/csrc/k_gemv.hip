@@ -353,6 +353,7 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
   // everything.
   ProRow<QW, NPRO> r0;
   if constexpr (PRO != PRO_NONE) pro_load_row<PRO, QW, NPRO>(a, ps, 0, r0);
+  __builtin_amdgcn_sched_barrier(0);  // (issue order: prologue operands first)
   // EPI_ADD with partials: those of the thread's item column, before the
   // weights (the column j = it % NB is the same for every item it of the
   // thread since 256 is a multiple of NB)
@@ -362,6 +363,7 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int h = 0; h < NEPI; ++h) pe[h] = pc[min(h, ps.npart - 1) * ps.ld_part];
   }
+  __builtin_amdgcn_sched_barrier(0);
   // A operand rows and scales of the unfused path, also before the weights
   const bool avalid = lr < M;
   v4i av[GPW][KSTEPS];
@@ -408,6 +410,10 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
   }
   // the exp table from immediates (a load here would be issued after the
   // weights and waited for with them); first read after barriers
+  // keep every load above issued before the prologue's arithmetic (the
+  // scheduler would otherwise start it first and wait for its operands
+  // before issuing the weights)
+  __builtin_amdgcn_sched_barrier(0);
   if (NMAT == 2 && threadIdx.x == 0) stage_exp2_table(exptab);
 
   if constexpr (PRO != PRO_NONE) {
@@ -572,6 +578,7 @@ __global__ void __launch_bounds__(256) gemv_stream_kernel(GemvArgs a, int ntiles
   v4i b0[NT][GPW][KSTEPS], b1[NT][GPW][KSTEPS];
   float s0[NT], s1[NT];
   load_tile(b0, s0, t);
+  __builtin_amdgcn_sched_barrier(0);
 
   if constexpr (PRO != PRO_NONE) {
     pro_compute_row<PRO, QW, 0>(a, 0, r0, a_lds, as_lds, blk);
