@@ -526,16 +526,29 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
     }
     __syncthreads();
     // ---- phase 2: prefix max (attention_gqa.h:476-477) ----
-    if (tid < QPW) {
-      float run = sm.run[tid];
-      for (int jb = 0; jb < nb; ++jb) {
-        const float bm = sm.bmax[tid][jb];
-        const float nmm = (run > bm) ? run : bm;
-        sm.prev[tid][jb] = run;
-        sm.nmm[tid][jb] = nmm;
-        run = nmm;
+    // nmm_j = max(run, bmax_0, ..., bmax_j): wave h scans head h's block
+    // maxima across its lanes.  Scores are never NaN or -0 (an exact zero
+    // dot product gives +0 after the positive scales), so the select
+    // (a > b ? a : b) is an associative max and the scan equals the
+    // reference's sequential walk.
+    static_assert(CB <= 32, "phase 2 scans one block per lane");
+    if (wave < QPW) {
+      const int h = wave;
+      const float run = sm.run[h];
+      float m = lane < nb ? sm.bmax[h][lane] : -INFINITY;
+#pragma unroll
+      for (int d = 1; d < 32; d <<= 1) {
+        const float o = __shfl_up(m, d);
+        if (lane >= d) m = (o > m) ? o : m;
       }
-      sm.run[tid] = run;
+      const float nmm = (run > m) ? run : m;
+      const float up = __shfl_up(nmm, 1);
+      const float prev = lane == 0 ? run : up;
+      if (lane < nb) {
+        sm.prev[h][lane] = prev;
+        sm.nmm[h][lane] = nmm;
+      }
+      if (lane == nb - 1) sm.run[h] = nmm;
     }
     __syncthreads();
     // ---- phase 3: P, P8 and P8.V per block ----
