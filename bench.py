@@ -127,36 +127,41 @@ def kernel_rooflines(stream) -> dict:
 
 # Algorithmic HBM bytes of one launch of each decode kernel class (model
 # shape of the workload): every operand read once, every result written once.
-def decode_class_bytes(name: str, kv_len: int) -> int:
+# ofused: the O projection runs inside the attention kernel (per-head f32
+# partials, NH x H, written there and read by the gate/up and down GEMVs).
+def decode_class_bytes(name: str, kv_len: int, ofused: bool = True) -> int:
     H, QW, KW, KVH, NH, I, V = 1024, 2048, 1024, 8, 16, 3072, 151936
+    part = NH * H * 4 if ofused else 0
     if name == "attn_decode":
         kv_rows = kv_len * (2 * KW + 2 * KVH * 4)       # K, V rows + per-head scales
         ins = (QW + 2 * KW) * 4 + 2 * 128 * 4 + 2 * 64 * 4  # f32 q|k|v rows, q/k gains, cos/sin
         outs = (QW + NH * 4) * 2 + 2 * (KW + KVH * 4)  # q8/qs + o8/os, new K/V rows + scales
-        return kv_rows + ins + outs
+        o = (H * QW + 4 * H) + part if ofused else 0   # Wo and its scales, the partials
+        return kv_rows + ins + outs + o
     if name == "gemv_qkv":     # RMSNorm prologue (x, gain) + Q|K|V weights, f32 outputs
         N = QW + 2 * KW
         return N * H + 4 * N + 2 * 4 * H + 4 * N + (H + 4 * H + 16)
     if name == "gemv_o":       # o8/os + Wo + residual read/write
         return H * QW + 4 * H + QW + 4 * NH + 2 * 4 * H
-    if name == "gemv_gate_up":  # prologue (x, gain) + Wg, Wu + f32 SwiGLU row
-        return 2 * I * H + 8 * I + 2 * 4 * H + 4 * I + (H + 4 * H + 16)
-    if name == "gemv_down":    # f32 SwiGLU row + Wd + residual read/write (+ s8/ss stage)
-        return 4 * I + H * I + 4 * H + 2 * 4 * H + I + 4 * (I // 256)
+    if name == "gemv_gate_up":  # prologue (x, gain, O partials) + Wg, Wu + f32 SwiGLU row
+        return 2 * I * H + 8 * I + 2 * 4 * H + 4 * I + (H + 4 * H + 16) + part
+    if name == "gemv_down":    # f32 SwiGLU row + Wd + residual read/write (+ s8/ss stage, O partials)
+        return 4 * I + H * I + 4 * H + 2 * 4 * H + I + 4 * (I // 256) + part
     if name == "lm_head":      # prologue + lm weights and scales (+ keys)
         return V * H + 4 * V + 2 * 4 * H + 8 * 1024
     raise KeyError(name)
 
 
-def attn_prefetch_bytes(kv_len: int, last_layer: bool) -> int:
+def attn_prefetch_bytes(kv_len: int, last_layer: bool, ofused: bool = True) -> int:
     """Bytes the attention kernel's prefetch workgroups read per launch
-    (q3_model.hip): this layer's O, gate, up, down weights, the next layer's
-    Q, K, V weights (not after the last layer), and the K/V pages and scales
-    of the next attention."""
+    (q3_model.hip): this layer's gate, up, down weights (and O unless the
+    attention computes the O projection itself), the next layer's Q, K, V
+    (and O when fused) weights (not after the last layer), and the K/V pages
+    and scales of the next attention."""
     H, QW, KW, KVH, I = 1024, 2048, 1024, 8, 3072
-    b = H * QW + 2 * I * H + H * I
+    b = 2 * I * H + H * I + (0 if ofused else H * QW)
     if not last_layer:
-        b += (QW + 2 * KW) * H
+        b += (QW + 2 * KW) * H + (H * QW if ofused else 0)
     pages = (kv_len + (1 if last_layer else 0) + 31) // 32
     return b + pages * (2 * 32 * KW + 2 * 32 * KVH * 4)
 
@@ -469,6 +474,7 @@ def main() -> int:
         # decode step i (0-based) attends over kv_len = N_PROMPT + 1 + i keys
         n_steps = max(1, kt["attn_decode"][1] // layers)
         kv_lens = [N_PROMPT + 1 + i for i in range(n_steps)]
+        ofused = kt.get("gemv_o", (0.0, 0))[1] == 0  # no O GEMV launches: fused
         classes = {}
         for name, (tot_ms, n) in kt.items():
             if n == 0:
@@ -476,7 +482,7 @@ def main() -> int:
             if name == "lm_head":
                 byts = decode_class_bytes(name, 0)
             else:
-                byts = sum(decode_class_bytes(name, kv) for kv in kv_lens) / len(kv_lens)
+                byts = sum(decode_class_bytes(name, kv, ofused) for kv in kv_lens) / len(kv_lens)
             avg = tot_ms / n
             classes[name] = {"launches": n, "avg_us": avg * 1e3, "total_ms": tot_ms,
                              "bytes_per_launch": int(byts), "GBs": byts / avg / 1e6}
@@ -489,7 +495,7 @@ def main() -> int:
         pmc = load_pmc_traffic().get(dom_name)
         pf = None
         if dom_name == "attn_decode":
-            pf = sum(attn_prefetch_bytes(kv, l == layers - 1)
+            pf = sum(attn_prefetch_bytes(kv, l == layers - 1, ofused)
                      for kv in kv_lens for l in range(layers)) / (len(kv_lens) * layers)
         out["roofline"] = {"kernel": dom_name, "bound": "hbm", "achieved": dom["GBs"],
                            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": dom["GBs"] / HBM_PEAK_GBS,

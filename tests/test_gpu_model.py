@@ -86,6 +86,29 @@ def test_cfg0_generate(cuda, mode, gold_meta):
     assert not probs, probs
 
 
+@pytest.mark.parametrize("fuse_oproj", ["0", "1"])
+def test_cfg0_generate_oproj_modes(cuda, gold_meta, fuse_oproj, monkeypatch):
+    """Decode with the O projection inside the attention kernel (default) and
+    as its own GEMV (Q3_DECODE_FUSE_OPROJ=0, read when the model opens): the
+    generated ids, logits and the last forward's stages match the goldens
+    either way."""
+    note(f"cfg0 generate fuse_oproj={fuse_oproj}")
+    monkeypatch.setenv("Q3_DECODE_FUSE_OPROJ", fuse_oproj)
+    lay, blob = host_blob("cfg0")
+    g = load_cfg("cfg0")
+    m = Model(lay, blob)
+    m.set_ctrl(40, 2, 1)
+    m.generate()
+    ids = m.ids()
+    assert np.array_equal(ids[40:42], g["generated"]), (ids[40:42], g["generated"])
+    got = m.stage("logits", 1)[0]
+    assert bits_equal(got, g["logits"]), describe_diff(got, g["logits"])
+    last = int(g["n_forwards_with_logits"]) - 1
+    probs = stage_problems(g, f"f{last}_", m, 1, 42, 0, last_row_only=False)
+    m.close()
+    assert not probs, probs
+
+
 def test_cfg0_each_forward(cuda):
     """forward_chunk step by step, non-fused (all rows of the last layer):
     every recorded stage of every forward, bit for bit.  Chunk 0 runs with
