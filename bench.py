@@ -379,6 +379,72 @@ def cpu_baseline(threads: int) -> dict:
             "generated_head": [int(v) for v in np.asarray(gen)[:8]]}
 
 
+ENGINE_REQS, ENGINE_PROMPT, ENGINE_GEN = 32, 256, 64
+
+
+def run_engine(args) -> dict:
+    """The continuous-batching engine (q3ops.engine, tools/engine.py) on the
+    28-layer shape: ENGINE_REQS requests of ENGINE_PROMPT uniform prompt ids,
+    ENGINE_GEN greedy ids each, batches of at most 32 rows (prefill chunks of
+    32 first, then one row per decoding request), one shared page pool.  One
+    bench step = admitting every request and running the engine until all
+    have finished; the host scheduler and page bookkeeping are inside the
+    timed region."""
+    import numpy as np
+    import torch
+    from q3ops.engine import SamplingParams, make_gpu_engine
+    from q3ops.layout import InitConfig, Layout, ModelShape, init_random_blob
+    from q3ops.model import Model
+
+    per_req = -(-(ENGINE_PROMPT + ENGINE_GEN) // 32)
+    shape = ModelShape(seq=32, max_seq=ENGINE_REQS * per_req * 32)
+    lay = Layout(shape)
+    log(f"engine: writing random-init blob ({lay.size / 1e9:.2f} GB) ...")
+    blob = init_random_blob(lay, InitConfig(n_prompt=1, n_gen=0, mode=0))
+    m = Model(lay, blob)
+    rng = np.random.default_rng(0x5EED0005)
+    prompts = [[int(t) for t in rng.integers(0, lay.vocab, size=ENGINE_PROMPT)]
+               for _ in range(ENGINE_REQS)]
+
+    def one_step():
+        eng = make_gpu_engine(m)
+        for p in prompts:
+            eng.add_request(p, SamplingParams(max_new=ENGINE_GEN))
+        eng.run(max_steps=100000)
+        return eng
+
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        one_step()
+    torch.cuda.synchronize()
+    log(f"engine: timing {args.steps} steps ...")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        eng = one_step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    outs = eng.outputs()
+    assert all(len(v) == ENGINE_GEN for v in outs.values())
+    assert eng.pool.free_pages == eng.pool.num_pages
+    fed = ENGINE_REQS * (ENGINE_PROMPT + ENGINE_GEN - 1)
+    gen = ENGINE_REQS * ENGINE_GEN
+    return {
+        "metric": "tok/s continuous-batching engine (32 req x 256 prompt + 64 greedy), "
+                  "Qwen3-0.6B W8A8, 1 MI355X",
+        "value": fed / dt, "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": dt * 1e3, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic (random-init weights N(0,0.02) int8 per-row; uniform prompt ids)",
+        "config": {"workload": "engine: q3ops.engine over q3_forward_chunk (32-row prefill "
+                               "chunks) and q3_decode_batch (greedy rows), 28-layer shape",
+                   "requests": ENGINE_REQS, "prompt": ENGINE_PROMPT, "generated": ENGINE_GEN,
+                   "max_rows": 32, "pages": eng.pool.num_pages},
+        "generated_tok_s": gen / dt, "engine_batches": eng.steps,
+        "launches": dict(eng.guest_step.launches),
+        "first_ids": outs[0][:8],
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -389,19 +455,20 @@ def main() -> int:
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="finish with 3 device-to-device copies of MIB MiB (PMC calibration)")
-    ap.add_argument("--workload", choices=("cfg3", "cfg4"), default="cfg3",
+    ap.add_argument("--workload", choices=("cfg3", "cfg4", "engine"), default="cfg3",
                     help="cfg3: 512-token prefill + 64 b=1 decode steps (the headline line); "
-                         "cfg4: 64-sequence batched paged decode")
+                         "cfg4: 64-sequence batched paged decode; engine: continuous batching")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (this build has no multi-GPU path); "
               f"got --gpus {args.gpus}", file=sys.stderr)
         return 2
-    if args.workload == "cfg4":
+    if args.workload in ("cfg4", "engine"):
         import torch
         assert torch.cuda.is_available(), "bench.py needs a ROCm device"
         torch.cuda.set_device(0)
-        print(json.dumps(run_cfg4(args)), flush=True)
+        run = run_cfg4 if args.workload == "cfg4" else run_engine
+        print(json.dumps(run(args)), flush=True)
         return 0
 
     import numpy as np
