@@ -5,7 +5,7 @@ tensor names, one layer, a 1024-row vocabulary.
 Pinned by: a numpy restatement of pqwf.py:344-360's per-row quantiser (its
 numpy operations, independent of the C++ quantiser the converter calls), the
 quantiser's closed-form properties (|q| <= 127 with 127 reached, error within
-most half a step, zero rows, ties to even), the placement of every tensor in
+half a step plus the quotient rounding, zero rows, ties to even), the placement of every tensor in
 the blob (through the layout's typed views, byte offsets pinned by the
 layout tests), the RoPE tables' closed form, and on the GPU a generation on
 the converted blob equal to the oracle's."""
