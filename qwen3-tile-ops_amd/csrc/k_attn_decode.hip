@@ -93,10 +93,8 @@ struct Smem {
   float ksnew, vsnew;
   float s[QPW][CB * 32];  // scores of the chunk
   float bmax[QPW][CB];
-  float prev[QPW][CB], nmm[QPW][CB];
   float corr[QPW][CB], psum[QPW][CB];
   float pv[QPW][CB][HD];  // f32(P8.V) * pmax per block
-  float run[QPW];
   float absmax[QPW][2];
   int8_t o8[HD];  // OFUSE: the head's quantised output and its scale
   float os;
@@ -116,6 +114,16 @@ constexpr int kOPieces = 11;
 // pieces loaded after phase 1 of a chunk; the rest after its phase 3 (V rows
 // consumed): all of them at once do not fit the register file
 constexpr int kOPiecesEarly = 6;
+
+// One step of an inclusive max-scan within rows of 16 lanes (DPP
+// row_shr:D): lanes D.. of a row combine the value D lanes down, the first D
+// keep their own (the disabled lanes of the move return the old value).
+template <int D>
+__device__ __forceinline__ float row_shr_max(float m) {
+  const float o = __int_as_float(
+      __builtin_amdgcn_update_dpp(__float_as_int(m), __float_as_int(m), 0x110 + D, 0xf, 0xf, false));
+  return (o > m) ? o : m;
+}
 
 // The kernel arguments the first K/V loads depend on, read together and
 // pinned in SGPRs in the fused variants: otherwise the K/V addresses wait on
@@ -337,6 +345,8 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
   const int ph = tid / HD;  // phase-4 ownership: (head, dim)
   const int pd = tid % HD;
   float res = 0.0f, den = 0.0f;
+  // the running max of each head across chunks, from -FLT_MAX (attention_gqa.h:418)
+  float run0 = -3.402823466e38f, run1 = -3.402823466e38f;
   int qv[QPW][16];
   float qscale[QPW];
 
@@ -453,7 +463,6 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
     if constexpr (FIRST) __builtin_amdgcn_sched_barrier(0);
     if constexpr (FIRST) {
       // ---- prologue (overlaps the loads above) ----
-      if (tid < QPW) sm.run[tid] = -3.402823466e38f;
       if constexpr (OFUSE) {
 #pragma unroll
         for (int i = 0; i < kWosPerThread; ++i)
@@ -526,31 +535,31 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
     }
     __syncthreads();
     // ---- phase 2: prefix max (attention_gqa.h:476-477) ----
-    // nmm_j = max(run, bmax_0, ..., bmax_j): wave h scans head h's block
-    // maxima across its lanes.  Scores are never NaN or -0 (an exact zero
-    // dot product gives +0 after the positive scales), so the select
-    // (a > b ? a : b) is an associative max and the scan equals the
-    // reference's sequential walk.
+    // nmm_j = max(run, bmax_0, ..., bmax_j), prev_j = nmm_{j-1} (run for
+    // j = 0): every wave scans the block maxima itself (lanes 32 h + j hold
+    // head h's block j), in registers, so no barrier follows.  Scores are
+    // never NaN or -0 (an exact zero dot product gives +0 after the positive
+    // scales), so the select (a > b ? a : b) is an associative max and the
+    // scan equals the reference's sequential walk.
     static_assert(CB <= 32, "phase 2 scans one block per lane");
-    if (wave < QPW) {
-      const int h = wave;
-      const float run = sm.run[h];
-      float m = lane < nb ? sm.bmax[h][lane] : -INFINITY;
-#pragma unroll
-      for (int d = 1; d < 32; d <<= 1) {
-        const float o = __shfl_up(m, d);
-        if (lane >= d) m = (o > m) ? o : m;
-      }
-      const float nmm = (run > m) ? run : m;
+    float nmm, prev;
+    {
+      const int hh = lane >> 5, cc = lane & 31;
+      float m = (hh < QPW && cc < nb) ? sm.bmax[hh][cc] : -INFINITY;
+      m = row_shr_max<1>(m);
+      m = row_shr_max<2>(m);
+      m = row_shr_max<4>(m);
+      m = row_shr_max<8>(m);
+      const float r15 = lane_read(m, 15), r47 = lane_read(m, 47);
+      const float cross = (lane & 32) ? r47 : r15;
+      if (lane & 16) m = (cross > m) ? cross : m;
+      const float runh = hh ? run1 : run0;
+      nmm = (runh > m) ? runh : m;
       const float up = __shfl_up(nmm, 1);
-      const float prev = lane == 0 ? run : up;
-      if (lane < nb) {
-        sm.prev[h][lane] = prev;
-        sm.nmm[h][lane] = nmm;
-      }
-      if (lane == nb - 1) sm.run[h] = nmm;
+      prev = cc == 0 ? runh : up;
+      run0 = lane_read(nmm, nb - 1);
+      if constexpr (QPW > 1) run1 = lane_read(nmm, 32 + nb - 1);
     }
-    __syncthreads();
     // ---- phase 3: P, P8 and P8.V per block ----
 #pragma unroll
     for (int i = 0; i < BPW; ++i) {
@@ -563,9 +572,14 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
       for (int hp = 0; hp < QPW; hp += 2) {
         const int h = hp + (lane >> 5);
         const bool hok = h < QPW;
+        // this block's nmm / prev of the lane's head (lanes jb and 32 + jb)
+        const float nm0 = lane_read(nmm, jb), pr0 = lane_read(prev, jb);
+        const float nm1 = QPW > 1 ? lane_read(nmm, 32 + jb) : nm0;
+        const float pr1 = QPW > 1 ? lane_read(prev, 32 + jb) : pr0;
+        const float nmb = (lane & 32) ? nm1 : nm0, prb = (lane & 32) ? pr1 : pr0;
         float p = 0.0f, pv = 0.0f;
         if (hok && valid) {
-          p = exp_f32_le0_tab(__fsub_rn(sm.s[h][jb * 32 + c], sm.nmm[h][jb]), sm.tab);
+          p = exp_f32_le0_tab(__fsub_rn(sm.s[h][jb * 32 + c], nmb), sm.tab);
           pv = __fmul_rn(p, vscale[i]);
         }
         const float psum = tree_sum32(p);
@@ -573,7 +587,7 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
         const int p8 = hok ? quant1(pv, pm) : 0;
         if (hok && c == 0) {
           sm.psum[h][jb] = psum;
-          sm.corr[h][jb] = exp_f32_le0_tab(__fsub_rn(sm.prev[h][jb], sm.nmm[h][jb]), sm.tab);
+          sm.corr[h][jb] = exp_f32_le0_tab(__fsub_rn(prb, nmb), sm.tab);
         }
         int acc[2][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
         pv_dot<(QPW > 1 ? 2 : 1)>(vw[i], p8, lane, reinterpret_cast<int(&)[(QPW > 1 ? 2 : 1)][4]>(acc));

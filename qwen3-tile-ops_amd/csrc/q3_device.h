@@ -285,6 +285,11 @@ __device__ __forceinline__ float lane_bcast(float x) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), L));
 }
 
+// Value of lane l (wave-uniform, a runtime value) in every lane.
+__device__ __forceinline__ float lane_read(float x, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l));
+}
+
 // ---- wave reductions --------------------------------------------------
 // Pairwise tree over 32 consecutive lanes: level k adds lanes i and i^2^k.
 // For 32 leaves this is exactly ref_qwen3.py:41-50's tree (pairs (0,1),
