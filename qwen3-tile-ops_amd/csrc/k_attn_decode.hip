@@ -621,14 +621,39 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
     }
     __syncthreads();
     // ---- phase 4: the sequential den/res chain (attention_gqa.h:476-519) ----
-    if (tid < QPW * HD) {
-      for (int jb = 0; jb < nb; ++jb) {
-        const float corr = sm.corr[ph][jb];
-        den = __fadd_rn(__fmul_rn(den, corr), sm.psum[ph][jb]);
-        res = __fadd_rn(__fmul_rn(res, corr), sm.pv[ph][jb][pd]);
+    // Batches: operands of 8 blocks are read before their 8 chain steps
+    // (entries past nb are read, in bounds, and not used); at b = 1 (up to
+    // 24 blocks on 16 CUs) the plain loop measured faster.  No barrier
+    // follows: the LDS this reads (corr, psum, pv) is next written in the
+    // next chunk's phase 3, behind that chunk's first barrier, and the
+    // epilogue writes other arrays.
+    if constexpr (FUSE) {
+      if (tid < QPW * HD) {
+        for (int jb = 0; jb < nb; ++jb) {
+          const float corr = sm.corr[ph][jb];
+          den = __fadd_rn(__fmul_rn(den, corr), sm.psum[ph][jb]);
+          res = __fadd_rn(__fmul_rn(res, corr), sm.pv[ph][jb][pd]);
+        }
+      }
+    } else if (tid < QPW * HD) {
+      for (int j0 = 0; j0 < nb; j0 += 8) {
+        float cr[8], ps[8], pw[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int jb = min(j0 + u, CB - 1);
+          cr[u] = sm.corr[ph][jb];
+          ps[u] = sm.psum[ph][jb];
+          pw[u] = sm.pv[ph][jb][pd];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (j0 + u < nb) {
+            den = __fadd_rn(__fmul_rn(den, cr[u]), ps[u]);
+            res = __fadd_rn(__fmul_rn(res, cr[u]), pw[u]);
+          }
+        }
       }
     }
-    __syncthreads();
   };
   chunk(0, std::true_type{});
   for (int b0 = CB; b0 < nblocks; b0 += CB) chunk(b0, std::false_type{});
