@@ -20,12 +20,21 @@
 // through the global address each lane reads: LDS row r keeps its 16-byte
 // chunk c in slot c ^ ((r / RPC) % CH) (CH chunks per row, RPC rows per
 // 256-byte bank cycle), which spreads the 16 rows of a fragment read over
-// all banks.  Steps are coarse (KS = 256 B: one barrier pair per 4 MFMA
-// k-slices) because a k-step's fixed cost (barriers, LDS latency) is
-// comparable to a 64-byte step's MFMA work.  The per-group dequantisation
-// runs when a group's last slice is done, one thread per output element, in
-// group order.
+// all banks.  Steps are coarse (KS = 128 or 256 B: one barrier per 2-4 MFMA
+// k-slices) because a k-step's fixed cost (barrier, LDS latency) is
+// comparable to a 64-byte step's MFMA work; the copies of step t + STAGES - 1
+// are issued right after step t's barrier, into the stage step t - 1 read.
+//
+// The per-group dequantisation (one thread per output element, groups in
+// order) costs 4 VALU operations per element and group (cvt, two RN
+// multiplies, add): as much issue time as the group's MFMAs at g = 256 and
+// twice as much at g = 128.  The int32 group sums are therefore double
+// buffered by group parity: group g is dequantised after the first MFMAs of
+// group g + 1 are issued, so the two run side by side instead of
+// MFMA -> dequant -> MFMA on one set of registers.
 #include <algorithm>
+#include <type_traits>
+#include <utility>
 
 #include "q3_device.h"
 #include "q3_kernels.h"
@@ -37,6 +46,16 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ v4i zero4() {
   v4i z = {0, 0, 0, 0};
   return z;
+}
+
+// f(std::integral_constant<int, 0>{}), ..., f(std::integral_constant<int, N - 1>{})
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
 
@@ -96,7 +115,7 @@ struct TileShape {
   __device__ static int swz(int r, int c) { return c ^ ((r / RPC) & (CH - 1)); }
 };
 
-template <int BM, int BN, int WGM, int NMAT, int STAGES, int KS, int EPI>
+template <int BM, int BN, int WGM, int NMAT, int STAGES, int KS, int EPI, int GROUP>
 __global__ void __launch_bounds__(512) gemm_tile_kernel(TileArgs a) {
   using S = TileShape<BM, BN, WGM, NMAT, STAGES, KS>;
   constexpr int MT = S::MT, NT = S::NT;
@@ -130,7 +149,6 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(TileArgs a) {
   }
   const int M = a.M;
   const int T = a.K / KS;            // k-steps
-  const int SPG = a.group / 64;      // k-slices per group
   const int ngroups = a.K / a.group;
   float *as_lds = reinterpret_cast<float *>(smem + STAGES * S::STAGE);  // [BM][ngroups]
   uint64_t *tab = reinterpret_cast<uint64_t *>(as_lds + BM * ngroups);  // exp table (SwiGLU)
@@ -179,79 +197,127 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(TileArgs a) {
     if (p < T) issue(p, p);
 
   float acc[NMAT][MT][NT][4];
-  v4i c[NMAT][MT][NT];
 #pragma unroll
   for (int mi = 0; mi < NMAT; ++mi)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
+      for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[mi][mt][nt][i] = 0.0f;
-        c[mi][mt][nt] = zero4();
-      }
 
-  for (int t = 0; t < T; ++t) {
-    const int tn = t + STAGES - 1;
-    if (tn < T) {
-      issue(tn, tn % STAGES);
-      // steps t+1 .. t+STAGES-1 of this wave may stay in flight
+  // Exact int32 group sums, double-buffered by group parity (GROUP > 0):
+  // group g is dequantised (and its buffer cleared) right after the first
+  // MFMAs of group g + 1 are issued, so its VALU work runs while they
+  // execute (the two buffers share no register).  GROUP == 0 (group size
+  // known only at run time): one buffer, dequantised as soon as the group's
+  // last slice is done.
+  v4i c[2][NMAT][MT][NT];
+#pragma unroll
+  for (int mi = 0; mi < NMAT; ++mi)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) c[0][mi][mt][nt] = c[1][mi][mt][nt] = zero4();
+
+  // acc += RN(RN(f32(c) * bs[n]) * as[m][g]) (groups in ascending order),
+  // then c = 0 for the buffer's next group
+  auto dequant = [&](auto PAR, int g) {
+    constexpr int b = decltype(PAR)::value;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float asv = as_lds[(wm * S::WM + mt * 16 + lg * 4 + i) * ngroups + g];
+#pragma unroll
+        for (int mi = 0; mi < NMAT; ++mi)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) {
+            const float p = __fmul_rn(__fmul_rn(static_cast<float>(c[b][mi][mt][nt][i]), bsv[mi][nt]), asv);
+            acc[mi][mt][nt][i] = __fadd_rn(acc[mi][mt][nt][i], p);
+          }
+      }
+#pragma unroll
+    for (int mi = 0; mi < NMAT; ++mi)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) c[b][mi][mt][nt] = zero4();
+  };
+
+  constexpr int SPG = GROUP > 0 ? GROUP / 64 : 1;        // k-slices per group
+  constexpr bool WHOLE = GROUP > 0 && SPG >= S::SLICES;  // a group is whole steps
+  // One k-step.  WHOLE: every slice goes to buffer PAR (the group's parity)
+  // and gfirst marks the group's first step; otherwise a step holds an even
+  // number of groups and the buffer follows the slice.  Stage t % STAGES is
+  // refilled STAGES - 1 steps later, by the copies issued after the barrier
+  // of step t + 1, when every wave is past step t.
+  auto step = [&](int t, auto PAR, bool gfirst) {
+    if (t + STAGES - 2 < T) {
+      // steps t+1 .. t+STAGES-2 of this wave may stay in flight
       if (wave < S::INSTR % S::NW || S::INSTR % S::NW == 0)
-        wait_vmcnt<S::IPW_HI * (STAGES - 1)>();
+        wait_vmcnt<S::IPW_HI * (STAGES - 2)>();
       else
-        wait_vmcnt<S::IPW_LO * (STAGES - 1)>();
+        wait_vmcnt<S::IPW_LO * (STAGES - 2)>();
     } else {
       wait_vmcnt<0>();
     }
     lds_barrier();
+    if (t + STAGES - 1 < T) issue(t + STAGES - 1, (t + STAGES - 1) % STAGES);
     const int8_t *st = smem + (t % STAGES) * S::STAGE;
+    static_for<S::SLICES>([&](auto KK) {
+      constexpr int kk = decltype(KK)::value;
+      v4i af[MT], bf[NMAT][NT];
 #pragma unroll
-    for (int kk = 0; kk < S::SLICES; ++kk) {
-    v4i af[MT], bf[NMAT][NT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int r = wm * S::WM + mt * 16 + lr;
-      af[mt] = *reinterpret_cast<const v4i *>(st + r * KS + 16 * S::swz(r, 4 * kk + lg));
-    }
-#pragma unroll
-    for (int mi = 0; mi < NMAT; ++mi)
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const int r = BM + mi * BN + wn * S::WN + nt * 16 + lr;
-        bf[mi][nt] = *reinterpret_cast<const v4i *>(st + r * KS + 16 * S::swz(r, 4 * kk + lg));
+      for (int mt = 0; mt < MT; ++mt) {
+        const int r = wm * S::WM + mt * 16 + lr;
+        af[mt] = *reinterpret_cast<const v4i *>(st + r * KS + 16 * S::swz(r, 4 * kk + lg));
       }
 #pragma unroll
-    for (int mi = 0; mi < NMAT; ++mi)
+      for (int mi = 0; mi < NMAT; ++mi)
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
-          c[mi][mt][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[mt], bf[mi][nt], c[mi][mt][nt], 0, 0, 0);
-    const int slice = t * S::SLICES + kk;
-    if ((slice + 1) % SPG == 0) {  // group g done: dequant and accumulate in order
-      const int g = slice / SPG;
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float asv = as_lds[(wm * S::WM + mt * 16 + lg * 4 + i) * ngroups + g];
-#pragma unroll
-          for (int mi = 0; mi < NMAT; ++mi)
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-              const float p = __fmul_rn(__fmul_rn(static_cast<float>(c[mi][mt][nt][i]), bsv[mi][nt]), asv);
-              acc[mi][mt][nt][i] = __fadd_rn(acc[mi][mt][nt][i], p);
-            }
+        for (int nt = 0; nt < NT; ++nt) {
+          const int r = BM + mi * BN + wn * S::WN + nt * 16 + lr;
+          bf[mi][nt] = *reinterpret_cast<const v4i *>(st + r * KS + 16 * S::swz(r, 4 * kk + lg));
         }
+      const int slice = t * S::SLICES + kk;
+      constexpr int par = GROUP == 0 ? 0 : WHOLE ? decltype(PAR)::value : (kk / SPG) & 1;
 #pragma unroll
       for (int mi = 0; mi < NMAT; ++mi)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-          for (int nt = 0; nt < NT; ++nt) c[mi][mt][nt] = zero4();
+          for (int nt = 0; nt < NT; ++nt)
+            c[par][mi][mt][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[mt], bf[mi][nt], c[par][mi][mt][nt], 0, 0, 0);
+      if constexpr (GROUP == 0) {
+        const int spg = a.group / 64;
+        if ((slice + 1) % spg == 0) dequant(std::integral_constant<int, 0>{}, slice / spg);
+      } else if constexpr (WHOLE) {
+        if (kk == 0 && gfirst && slice > 0) dequant(std::integral_constant<int, par ^ 1>{}, slice / SPG - 1);
+      } else if constexpr (kk % SPG == 0) {
+        if (slice > 0) dequant(std::integral_constant<int, par ^ 1>{}, slice / SPG - 1);
+      }
+    });
+  };
+
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
+  if constexpr (WHOLE) {
+    constexpr int SPS = SPG / S::SLICES;  // k-steps per group
+    int t = 0;
+    for (int g = 0; g < ngroups; g += 2) {
+      for (int q = 0; q < SPS; ++q, ++t) step(t, P0{}, q == 0);
+      if (g + 1 < ngroups)
+        for (int q = 0; q < SPS; ++q, ++t) step(t, P1{}, q == 0);
     }
-    }  // k-slices
-    lds_barrier();  // stage t % STAGES is refilled by the next iteration
+  } else {
+    for (int t = 0; t < T; ++t) step(t, P0{}, false);
+  }
+  if constexpr (GROUP > 0) {  // the last group
+    if ((ngroups - 1) & 1)
+      dequant(P1{}, ngroups - 1);
+    else
+      dequant(P0{}, ngroups - 1);
   }
   __syncthreads();
 
@@ -348,7 +414,7 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(TileArgs a) {
   }
 }
 
-template <int BM, int BN, int WGM, int NMAT, int STAGES, int KS, int EPI>
+template <int BM, int BN, int WGM, int NMAT, int STAGES, int KS, int EPI, int GROUP>
 hipError_t launch_shape(const TileArgs &a, hipStream_t s) {
   using S = TileShape<BM, BN, WGM, NMAT, STAGES, KS>;
   if (a.K % KS) return hipErrorInvalidValue;
@@ -360,14 +426,24 @@ hipError_t launch_shape(const TileArgs &a, hipStream_t s) {
   static bool attr_set = false;  // more than 64 KiB of dynamic LDS must be allowed once
   if (!attr_set) {
     const hipError_t e =
-        hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_tile_kernel<BM, BN, WGM, NMAT, STAGES, KS, EPI>),
+        hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_tile_kernel<BM, BN, WGM, NMAT, STAGES, KS, EPI, GROUP>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
   const dim3 grid(a.N / BN, (a.M + BM - 1) / BM);
-  Q3_LAUNCH((gemm_tile_kernel<BM, BN, WGM, NMAT, STAGES, KS, EPI>), grid, dim3(S::NTHR), lds, s, a);
+  Q3_LAUNCH((gemm_tile_kernel<BM, BN, WGM, NMAT, STAGES, KS, EPI, GROUP>), grid, dim3(S::NTHR), lds, s, a);
   return hipGetLastError();
+}
+
+// The group size as a template argument where the model uses it (256, and
+// 128 for the O projection), so that the group-sum buffers alternate at
+// compile time; any other group size takes the run-time path.
+template <int BM, int BN, int WGM, int NMAT, int STAGES, int KS, int EPI>
+hipError_t launch_tile(const TileArgs &a, hipStream_t s) {
+  if (a.group == 256) return launch_shape<BM, BN, WGM, NMAT, STAGES, KS, EPI, 256>(a, s);
+  if (a.group == 128) return launch_shape<BM, BN, WGM, NMAT, STAGES, KS, EPI, 128>(a, s);
+  return launch_shape<BM, BN, WGM, NMAT, STAGES, KS, EPI, 0>(a, s);
 }
 
 }  // namespace
@@ -386,25 +462,25 @@ hipError_t launch_gemm_tile(const TileArgs &a, int epi, hipStream_t s) {
   if (!gemm_tile_supported(a, epi)) return hipErrorInvalidValue;
   // a batch of sequences (M <= 64): 32-column tiles, for 4x the workgroups
   if (a.M <= 64 && (epi == EPI_STORE || epi == EPI_ADD)) {
-    if (epi == EPI_STORE) return launch_shape<64, 32, 4, 1, 3, 256, EPI_STORE>(a, s);
-    return launch_shape<64, 32, 4, 1, 3, 256, EPI_ADD>(a, s);
+    if (epi == EPI_STORE) return launch_tile<64, 32, 4, 1, 3, 256, EPI_STORE>(a, s);
+    return launch_tile<64, 32, 4, 1, 3, 256, EPI_ADD>(a, s);
   }
   switch (epi) {
-    case EPI_STORE: return launch_shape<64, 128, 2, 1, 3, 256, EPI_STORE>(a, s);
-    case EPI_ADD: return launch_shape<32, 64, 2, 1, 5, 256, EPI_ADD>(a, s);
-    case EPI_HEADQ: return launch_shape<64, 128, 2, 1, 3, 256, EPI_HEADQ>(a, s);
-    case EPI_NRQ: return launch_shape<64, 128, 2, 1, 3, 256, EPI_NRQ>(a, s);
+    case EPI_STORE: return launch_tile<64, 128, 2, 1, 4, 128, EPI_STORE>(a, s);
+    case EPI_ADD: return launch_tile<32, 64, 2, 1, 6, 256, EPI_ADD>(a, s);
+    case EPI_HEADQ: return launch_tile<64, 128, 2, 1, 4, 128, EPI_HEADQ>(a, s);
+    case EPI_NRQ: return launch_tile<64, 128, 2, 1, 4, 128, EPI_NRQ>(a, s);
     case EPI_QKV:
       if (a.nseg < 1 || a.nseg > 3 || a.seg[0].n0 != 0 || a.seg[a.nseg - 1].n1 != a.N) return hipErrorInvalidValue;
       for (int i = 0; i < a.nseg; ++i)
         if (a.seg[i].n0 % 128 || a.seg[i].n1 % 128 || a.seg[i].n1 <= a.seg[i].n0 ||
             (i > 0 && a.seg[i].n0 != a.seg[i - 1].n1) || (reinterpret_cast<uintptr_t>(a.seg[i].b) & 15))
           return hipErrorInvalidValue;
-      return launch_shape<64, 128, 2, 1, 3, 256, EPI_QKV>(a, s);
-    case EPI_SWIGLUQ: return launch_shape<32, 256, 2, 2, 2, 128, EPI_SWIGLUQ>(a, s);
+      return launch_tile<64, 128, 2, 1, 4, 128, EPI_QKV>(a, s);
+    case EPI_SWIGLUQ: return launch_tile<32, 256, 1, 2, 2, 128, EPI_SWIGLUQ>(a, s);
     case EPI_ARGMAX:  // rows of a batch of sequences (M <= 64): the weights are read once
       if (!a.keys || a.keys_ld < a.N / 128) return hipErrorInvalidValue;
-      return launch_shape<64, 128, 2, 1, 3, 256, EPI_ARGMAX>(a, s);
+      return launch_tile<64, 128, 2, 1, 3, 256, EPI_ARGMAX>(a, s);
     default: return hipErrorInvalidValue;
   }
 }
