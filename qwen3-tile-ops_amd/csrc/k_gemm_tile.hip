@@ -322,6 +322,21 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(TileArgs a) {
   __syncthreads();
 
   if constexpr (EPI == EPI_STORE || EPI == EPI_ADD) {
+    // EPI_ADD: every residual element of the lane is loaded before the first
+    // store (a load after a store to the same array would wait for it, one
+    // memory latency per element); rows past M read row M - 1, unused
+    float xr[MT][4][NT];
+    if constexpr (EPI == EPI_ADD) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = min(m0 + wm * S::WM + mt * 16 + lg * 4 + i, M - 1);
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt)
+            xr[mt][i][nt] = a.out[static_cast<int64_t>(m) * a.ldo + n0 + wn * S::WN + nt * 16 + lr];
+        }
+    }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -332,7 +347,7 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(TileArgs a) {
         for (int nt = 0; nt < NT; ++nt) {
           float *dst = a.out + static_cast<int64_t>(m) * a.ldo + n0 + wn * S::WN + nt * 16 + lr;
           if constexpr (EPI == EPI_ADD)
-            *dst = __fadd_rn(*dst, acc[0][mt][nt][i]);
+            *dst = __fadd_rn(xr[mt][i][nt], acc[0][mt][nt][i]);
           else
             *dst = acc[0][mt][nt][i];
         }
@@ -351,6 +366,56 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(TileArgs a) {
           tile[(wm * S::WM + mt * 16 + lg * 4 + i) * S::LDT + wn * S::WN + nt * 16 + lr] = v;
         }
     __syncthreads();
+    if constexpr (EPI == EPI_HEADQ || EPI == EPI_NRQ || EPI == EPI_QKV) {
+      // group_gemm.h:173-193 / norm_rope_quant.h:17-86 per (row, head).
+      // Pass 1 loads every operand of the wave's rows (gains, cos/sin rows,
+      // destination slots through the page table) as independent loads
+      // issued together; pass 2 computes and stores.  Walking rows with
+      // their loads inside would wait for a chain of dependent loads per
+      // row.  Rows past M load row M - 1's operands and store nothing.
+      static_assert(BN == 128, "one head (128 columns) per tile");
+      constexpr int RPW = (BM + S::NW - 1) / S::NW;  // rows per wave
+      float w0 = 0.0f, w1 = 0.0f, cr[RPW], sr[RPW];
+      int8_t *row8[RPW];
+      float *sp[RPW];
+      int64_t cs_off = 0;
+      if (do_norm) {
+        w0 = nw[static_cast<int64_t>(lane) * a.nw_stride];
+        w1 = nw[static_cast<int64_t>(lane + 64) * a.nw_stride];
+        if (a.cs_row_dev) cs_off = *a.cs_row_dev;
+      }
+#pragma unroll
+      for (int q = 0; q < RPW; ++q) {
+        const int mm = min(m0 + min(wave + S::NW * q, BM - 1), M - 1);
+        cr[q] = sr[q] = 0.0f;
+        if (do_norm) {
+          const int64_t crow = a.cs_row_pos ? static_cast<int64_t>(a.cs_row_pos[mm]) : mm + cs_off;
+          cr[q] = a.cos_t[crow * a.ld_cs + lane];
+          sr[q] = a.sin_t[crow * a.ld_cs + lane];
+        }
+        qdest_row(qd, mm, nb / 128, &row8[q], &sp[q]);
+      }
+      // every row is computed (a row past M holds zeros: finite, unused)
+      // and only the stores are predicated, so the rows' independent
+      // reduction chains can interleave
+#pragma unroll
+      for (int q = 0; q < RPW; ++q) {
+        const int rr = min(wave + S::NW * q, BM - 1);
+        const bool store = wave + S::NW * q < BM && m0 + rr < M;
+        float t0 = tile[rr * S::LDT + lane];
+        float t1 = tile[rr * S::LDT + lane + 64];
+        if (do_norm) head_norm_rope_regs(t0, t1, w0, w1, cr[q], sr[q], a.inv_hd, true);
+        const float mx = max64(fmaxf(fabsf(t0), fabsf(t1)));
+        const float scale = __fmul_rn(mx, inv127());
+        const int8_t q0 = static_cast<int8_t>(quant1(t0, scale));
+        const int8_t q1 = static_cast<int8_t>(quant1(t1, scale));
+        if (store) {
+          row8[q][lane] = q0;
+          row8[q][lane + 64] = q1;
+          if (lane == 0) *sp[q] = scale;
+        }
+      }
+    } else {
     for (int rr = wave; rr < BM; rr += S::NW) {
       const int m = m0 + rr;
       if (m >= M) break;
@@ -390,27 +455,9 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(TileArgs a) {
           for (int j = 0; j < 4; ++j) dst[lane + 64 * j] = static_cast<int8_t>(quant1(v[j], scale));
           if (lane == 0) a.ss[static_cast<int64_t>(m) * a.ldss + ((n0 + q * 256) / 256) * a.ss_col] = scale;
         }
-      } else {
-        static_assert(EPI == EPI_SWIGLUQ || EPI == EPI_ARGMAX || BN == 128, "one head (128 columns) per tile");
-        float t0 = tile[rr * S::LDT + lane];
-        float t1 = tile[rr * S::LDT + lane + 64];
-        if (do_norm) {
-          int64_t crow = m;
-          if (a.cs_row_dev) crow += *a.cs_row_dev;
-          if (a.cs_row_pos) crow = a.cs_row_pos[m];
-          head_norm_rope(t0, t1, lane, nw, a.nw_stride, a.cos_t + crow * a.ld_cs, a.sin_t + crow * a.ld_cs,
-                         a.inv_hd, true);
-        }
-        const float mx = max64(fmaxf(fabsf(t0), fabsf(t1)));
-        const float scale = __fmul_rn(mx, inv127());
-        int8_t *row8;
-        float *sp;
-        qdest_row(qd, m, nb / 128, &row8, &sp);
-        row8[lane] = static_cast<int8_t>(quant1(t0, scale));
-        row8[lane + 64] = static_cast<int8_t>(quant1(t1, scale));
-        if (lane == 0) *sp = scale;
       }
     }
+    }  // EPI_ARGMAX / EPI_SWIGLUQ
   }
 }
 
@@ -466,17 +513,17 @@ hipError_t launch_gemm_tile(const TileArgs &a, int epi, hipStream_t s) {
     return launch_tile<64, 32, 4, 1, 3, 256, EPI_ADD>(a, s);
   }
   switch (epi) {
-    case EPI_STORE: return launch_tile<64, 128, 2, 1, 4, 128, EPI_STORE>(a, s);
+    case EPI_STORE: return launch_tile<64, 128, 2, 1, 3, 128, EPI_STORE>(a, s);
     case EPI_ADD: return launch_tile<32, 64, 2, 1, 6, 256, EPI_ADD>(a, s);
-    case EPI_HEADQ: return launch_tile<64, 128, 2, 1, 4, 128, EPI_HEADQ>(a, s);
-    case EPI_NRQ: return launch_tile<64, 128, 2, 1, 4, 128, EPI_NRQ>(a, s);
+    case EPI_HEADQ: return launch_tile<32, 128, 2, 1, 3, 128, EPI_HEADQ>(a, s);
+    case EPI_NRQ: return launch_tile<32, 128, 2, 1, 3, 128, EPI_NRQ>(a, s);
     case EPI_QKV:
       if (a.nseg < 1 || a.nseg > 3 || a.seg[0].n0 != 0 || a.seg[a.nseg - 1].n1 != a.N) return hipErrorInvalidValue;
       for (int i = 0; i < a.nseg; ++i)
         if (a.seg[i].n0 % 128 || a.seg[i].n1 % 128 || a.seg[i].n1 <= a.seg[i].n0 ||
             (i > 0 && a.seg[i].n0 != a.seg[i - 1].n1) || (reinterpret_cast<uintptr_t>(a.seg[i].b) & 15))
           return hipErrorInvalidValue;
-      return launch_tile<64, 128, 2, 1, 4, 128, EPI_QKV>(a, s);
+      return launch_tile<32, 128, 2, 1, 3, 128, EPI_QKV>(a, s);
     case EPI_SWIGLUQ: return launch_tile<32, 256, 1, 2, 2, 128, EPI_SWIGLUQ>(a, s);
     case EPI_ARGMAX:  // rows of a batch of sequences (M <= 64): the weights are read once
       if (!a.keys || a.keys_ld < a.N / 128) return hipErrorInvalidValue;
