@@ -668,6 +668,115 @@ __global__ void __launch_bounds__(256) gemv_stream_kernel(GemvArgs a, int ntiles
   }
 }
 
+// M = 1 (decode, and the last row of a prefill chunk): the lm_head GEMV on
+// v_dot4 instead of MFMA tiles.  The MFMA operand layout makes every load
+// instruction gather 16 weight rows x 64 B at a 1 KB stride, and that
+// pattern alone streams at ~4.2 TB/s on this GPU, against ~6.3 TB/s for
+// contiguous 16-byte-per-lane reads (probe); with one activation row the
+// MFMA's other 15 rows are idle anyway.  Here a wave reads whole 1 KB
+// weight rows, lane l holding k = 16 l .. 16 l + 15, R rows per step with
+// the next step's loads in flight.  Per row: v_dot4 partials (exact int32),
+// the 16 lanes of each 256-column group summed with DPP (exact), then the
+// group GEMM's arithmetic (kernels/lm_argmax.h:72-182, ref_qwen3.py:145-158):
+// p_g = RN(RN(f32(I_g) * bs[n]) * as_g), out = (((0 + p_0) + p_1) + p_2) + p_3.
+// One argmax key per workgroup, as the tile kernels write.
+__device__ __forceinline__ int sdot4(int x, int y, int acc) { return __builtin_amdgcn_sdot4(x, y, acc, false); }
+
+template <int PRO, int R>
+__global__ void __launch_bounds__(256) gemv_row_kernel(GemvArgs a, int N) {
+  __shared__ float blk[32];
+  __shared__ __align__(16) int8_t a_lds[1024];
+  __shared__ float as_lds[4];
+  __shared__ unsigned long long wkey[4];
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_id();
+  const GemvSeg &sg = a.seg[0];
+
+  ProSrc ps = read_src<PRO, false>(a);
+  pin_src<PRO, false>(ps);
+  ProRow<1, 0> r0;
+  if constexpr (PRO != PRO_NONE) pro_load_row<PRO, 1, 0>(a, ps, 0, r0);
+
+  // rows of a wave's step: R consecutive rows; a workgroup step covers 4 R
+  // (N is a multiple of 64, so every wave of a workgroup runs the same steps)
+  const int stride = static_cast<int>(gridDim.x) * 4 * R;
+  int b = (static_cast<int>(blockIdx.x) * 4 + wave) * R;
+  auto load = [&](int4 (&w)[R], float (&bs)[R], int b0) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int n = min(b0 + r, N - 1);  // past N: reloaded, never used
+      bs[r] = sg.bs[n];
+      w[r] = *reinterpret_cast<const int4 *>(sg.b + static_cast<int64_t>(n) * 1024 + 16 * lane);
+    }
+  };
+  int4 w0[R], w1[R];
+  float bs0[R], bs1[R];
+  load(w0, bs0, b);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // the activation's 16 bytes at k = 16 lane and the lane's group scale
+  int4 av;
+  float asg;
+  if constexpr (PRO == PRO_NONE) {
+    av = *reinterpret_cast<const int4 *>(ps.a + 16 * lane);
+    asg = ps.as[lane / 16];
+  } else {
+    pro_compute_row<PRO, 1, 0>(a, 0, r0, a_lds, as_lds, blk);  // ends with a barrier
+    av = *reinterpret_cast<const int4 *>(a_lds + 16 * lane);
+    asg = as_lds[lane / 16];
+  }
+
+  unsigned long long best = 0ull;
+  auto rows = [&](const int4 (&w)[R], const float (&bs)[R], int b0) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      int acc = sdot4(w[r].x, av.x, 0);
+      acc = sdot4(w[r].y, av.y, acc);
+      acc = sdot4(w[r].z, av.z, acc);
+      acc = sdot4(w[r].w, av.w, acc);
+      acc += lane_xor<1>(acc);
+      acc += lane_xor<2>(acc);
+      acc += lane_xor<4>(acc);
+      acc += lane_xor<8>(acc);
+      const float p = __fmul_rn(__fmul_rn(static_cast<float>(acc), bs[r]), asg);
+      float out = 0.0f;
+      out = __fadd_rn(out, lane_bcast<0>(p));
+      out = __fadd_rn(out, lane_bcast<16>(p));
+      out = __fadd_rn(out, lane_bcast<32>(p));
+      out = __fadd_rn(out, lane_bcast<48>(p));
+      const int n = b0 + r;
+      if (n < N) {
+        if (sg.epi == EPI_ARGMAX) {
+          const unsigned long long key = (static_cast<unsigned long long>(ordered_key(out)) << 32) |
+                                         (0xFFFFFFFFu - static_cast<uint32_t>(n));
+          best = key > best ? key : best;
+        } else if (lane == 0) {
+          sg.out[n] = out;
+        }
+      }
+    }
+  };
+  while (b < N) {
+    load(w1, bs1, b + stride);
+    rows(w0, bs0, b);
+    b += stride;
+    if (b >= N) break;
+    load(w0, bs0, b + stride);
+    rows(w1, bs1, b);
+    b += stride;
+  }
+  if (sg.epi == EPI_ARGMAX) {
+    if (lane == 0) wkey[wave] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      unsigned long long k = wkey[0];
+#pragma unroll
+      for (int i = 1; i < 4; ++i) k = wkey[i] > k ? wkey[i] : k;
+      a.keys[blockIdx.x] = k;
+    }
+  }
+}
+
 // Per (row, head) wave: the head epilogues of the Q/K/V projections
 // (kernels/norm_rope_quant.h:17-86, group_gemm.h:173-193), from f32 rows.
 __global__ void __launch_bounds__(256) qkv_heads_kernel(QkvHeadArgs a) {
@@ -845,6 +954,18 @@ hipError_t launch_gemv(const GemvArgs &a, hipStream_t s) {
   if (a.M <= 0) return hipSuccess;
   if (a.pro != PRO_NONE && (a.K % 1024 != 0 || a.M > 16)) return hipErrorInvalidValue;
   const int ncols = ncols_of(a);
+  if (use_stream(a) && a.M == 1) {  // one row: whole-row v_dot4 streaming
+    const dim3 grid(stream_grid(ncols / 64));
+    constexpr int R = 4;
+    switch (a.pro) {
+      case PRO_NONE: Q3_LAUNCH((gemv_row_kernel<PRO_NONE, R>), grid, dim3(256), 0, s, a, ncols); break;
+      case PRO_NORM: Q3_LAUNCH((gemv_row_kernel<PRO_NORM, R>), grid, dim3(256), 0, s, a, ncols); break;
+      case PRO_EMBED: Q3_LAUNCH((gemv_row_kernel<PRO_EMBED, R>), grid, dim3(256), 0, s, a, ncols); break;
+      case PRO_QUANT: Q3_LAUNCH((gemv_row_kernel<PRO_QUANT, R>), grid, dim3(256), 0, s, a, ncols); break;
+      default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+  }
   if (use_stream(a)) {
     const int ntiles = ncols / 64;
     const size_t lds = sizeof(float) * 4 * 16 * 65 +
