@@ -152,6 +152,34 @@ def decode_class_bytes(name: str, kv_len: int, ofused: bool = True) -> int:
     raise KeyError(name)
 
 
+def path_roofline(prefill_ms: float, decode_ms: float) -> dict:
+    """The whole prefill and decode against their bounds (model shape of the
+    workload).  Prefill: int8 MACs of the 28 layers' GEMMs per token
+    (Q 2048x1024, K and V 1024x1024, O 1024x2048, gate/up 2x3072x1024,
+    down 1024x3072: 15,728,640 x 28), the causal attention (16 heads x
+    (QK + PV) x 128 x 512*513/2 per layer) and one lm_head row, x2 ops per
+    MAC, at the dense int8 MFMA peak.  Decode: weights and row scales of the
+    28 layers, the lm_head and its scales, and K, V rows plus per-head scales
+    (2112 B per layer and position) of every cached position, averaged over
+    the generated tokens, at the HBM peak."""
+    H, L, V, NH, HD = 1024, 28, 151936, 16, 128
+    layer_macs = 2048 * H + 2 * 1024 * H + H * 2048 + 2 * 3072 * H + H * 3072
+    attn_macs = L * NH * 2 * HD * (N_PROMPT * (N_PROMPT + 1) // 2)
+    prefill_ops = 2 * (N_PROMPT * L * layer_macs + attn_macs + V * H)
+    prefill_bound_ms = prefill_ops / (INT8_PEAK_TOPS * 1e9)
+    layer_scale_bytes = 4 * (2048 + 1024 + 1024 + 1024 + 2 * 3072 + 1024)
+    weights = L * (layer_macs + layer_scale_bytes) + V * H + 4 * V
+    kv = [L * 2112 * (N_PROMPT + i + 1) for i in range(N_GEN)]
+    decode_bytes = weights + sum(kv) / len(kv)
+    decode_bound_ms = decode_bytes / (HBM_PEAK_GBS * 1e6)
+    return {
+        "prefill": {"bound": "mfma", "ops": prefill_ops, "bound_ms": prefill_bound_ms,
+                    "frac": prefill_bound_ms / prefill_ms},
+        "decode": {"bound": "hbm", "bytes_per_token": decode_bytes, "bound_ms_per_token": decode_bound_ms,
+                   "frac": decode_bound_ms / decode_ms},
+    }
+
+
 def attn_prefetch_bytes(kv_len: int, last_layer: bool, ofused: bool = True) -> int:
     """Bytes the attention kernel's prefetch workgroups read per launch
     (q3_model.hip): this layer's gate, up, down weights (and O unless the
@@ -527,6 +555,7 @@ def main() -> int:
         "prefill_tok_s": N_PROMPT / (prefill_ms / 1e3),
         "decode_ms_per_token": decode_ms,
         "decode_tok_s": 1e3 / decode_ms,
+        "path_roofline": path_roofline(prefill_ms, decode_ms),
         "generated_head": [int(v) for v in gen_ids[:8]],
     }
     # in-situ kernel timing: one more (untimed) generation with every decode
