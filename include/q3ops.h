@@ -14,7 +14,9 @@
  *    on the current device).  Columns must be dense (col_bytes == element
  *    size); rows may be strided (row_bytes >= cols * element size).
  *  - `stream` is a hipStream_t passed as void* (NULL = default stream).  All
- *    ops are asynchronous and stream-ordered; none allocates or synchronises.
+ *    ops are asynchronous and stream-ordered and none synchronises.  None
+ *    allocates, except that the first q3_gemm_nt_group_argmax call on a
+ *    stream allocates that stream's key workspace.
  *  - Every function returns an int status: Q3_OK (0) or a negative Q3_ERR_*.
  *    The reference silently returns on unsupported shapes
  *    (kernels/group_gemm.h:47-49, kernels/lm_argmax.h:82); that behaviour is
@@ -185,7 +187,11 @@ int q3_gemm_gate_up_swiglu_quant(const q3_view *a, const q3_view *a_scale,
  * best, bidx, group_k): per row m, merges the logits row D[m,:] into the
  * running (best[m], bidx[m]) with the reference's strict `best < value`
  * rule, so the first index of the maximum wins and an initial best that is
- * not beaten is kept.  best f32 [M][1], bidx i32 [M][1] (read and written). */
+ * not beaten is kept.  best f32 [M][1], bidx i32 [M][1] (read and written).
+ * M <= 256.  The partial maxima between the GEMM and the final merge live in
+ * a 4 MiB key workspace per (device, stream): the first call on a stream
+ * allocates it (hipMalloc) and it is kept until the process ends, so calls
+ * on different streams never share keys. */
 int q3_gemm_nt_group_argmax(const q3_view *a, const q3_view *a_scale,
                             const q3_view *b, const q3_view *b_scale,
                             const q3_view *best, const q3_view *bidx,

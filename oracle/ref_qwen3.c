@@ -10,7 +10,8 @@
  * function is restated here from its published algorithm (ARM
  * optimized-routines exp2f, adopted by glibc 2.28: 32-entry table of
  * 2^(i/32) and a degree-3 polynomial evaluated in double) and pinned against
- * glibc exp2f over every float in [-151, 129] by tests/test_exp2.py.
+ * glibc exp2f over every float in [-151, 129] by oracle/exp2_check.c, which
+ * tests/test_oracle_prims.py runs.
  */
 #include "ref_qwen3.h"
 

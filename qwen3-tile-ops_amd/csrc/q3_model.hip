@@ -875,6 +875,7 @@ extern "C" int q3_model_open(void *blob, const q3_layout *lay, void *stream, q3_
   if (!blob || !lay || !out) return Q3_ERR_ARG;
   *out = nullptr;
   // Shapes the kernels are written for (hd128 heads, 256-column groups).
+  if (lay->kv_heads == 0 || lay->heads == 0) return Q3_ERR_UNSUPPORTED;
   if (lay->head_dim != 128 || lay->hidden % 256 || lay->inter % 256 || lay->vocab % 128 ||
       lay->max_seq % kPageTokens || lay->heads % lay->kv_heads || lay->seq == 0)
     return Q3_ERR_UNSUPPORTED;

@@ -2,6 +2,8 @@
 // dispatch to the kernels.  Mirrors kernels/*.h one function per op.
 #include <atomic>
 #include <cstring>
+#include <mutex>
+#include <vector>
 
 #include "q3_kernels.h"
 #include "q3ops.h"
@@ -38,6 +40,20 @@ int check_vec(const q3_view *v, uint32_t n, int64_t *stride) {
     return Q3_OK;
   }
   return Q3_ERR_VIEW;
+}
+
+// An f32 scale matrix [rows][cols] whose columns may be strided
+// (col_bytes a multiple of 4): at least `rows` x `cols`, and each row long
+// enough for its last column.
+int check_scales(const q3_view *v, uint32_t rows, uint32_t cols) {
+  if (!v || !v->data) return Q3_ERR_ARG;
+  if (v->dtype != Q3_DT_F32) return Q3_ERR_DTYPE;
+  if (v->row_bytes % 4 || v->col_bytes % 4 || v->col_bytes <= 0) return Q3_ERR_VIEW;
+  if (v->rows < rows || v->cols < cols) return Q3_ERR_VIEW;
+  if (rows > 1 && cols > 0 &&
+      v->row_bytes < static_cast<int64_t>(cols - 1) * v->col_bytes + 4)
+    return Q3_ERR_VIEW;
+  return Q3_OK;
 }
 
 inline int64_t ld(const q3_view *v) { return v->row_bytes / elem_size(v->dtype); }
@@ -272,10 +288,8 @@ int q3_gemm_nt_group_store(const q3_view *a, const q3_view *a_scale,
   if (skip) return Q3_OK;
   if (q8) {  // group_gemm.h:168-193 (nw selects norm+RoPE)
     Q3_TRY(check_view(q8, Q3_DT_I8));
-    if (!qs || !qs->data) return Q3_ERR_ARG;
-    if (qs->dtype != Q3_DT_F32) return Q3_ERR_DTYPE;
     if (q8->rows < a->rows || q8->cols < b->rows) return Q3_ERR_VIEW;
-    if (qs->row_bytes % 4 || qs->col_bytes % 4 || qs->col_bytes == 0) return Q3_ERR_VIEW;
+    Q3_TRY(check_scales(qs, a->rows, b->rows / 128));
     g.qd.q8 = static_cast<int8_t *>(q8->data);
     g.qd.ldq8 = q8->row_bytes;
     g.qd.qs = static_cast<float *>(qs->data);
@@ -316,7 +330,7 @@ int q3_gemm_nt_group_kv_paged(const q3_view *a, const q3_view *a_scale,
   Q3_TRY(gemm_common(a, a_scale, b, b_scale, group_k, g, &skip));
   if (skip) return Q3_OK;
   Q3_TRY(check_paged(kv));
-  if (kv->row_bytes < b->rows) return Q3_ERR_VIEW;
+  if (kv->row_bytes < b->rows || kv->scale_row_bytes < b->rows / 128 * 4) return Q3_ERR_VIEW;
   g.qd.q8 = static_cast<int8_t *>(is_v ? kv->v : kv->k);
   g.qd.qs = static_cast<float *>(is_v ? kv->vs : kv->ks);
   g.qd.table = kv->table;
@@ -344,9 +358,7 @@ int q3_norm_rope_quant_heads(const q3_view *x, const q3_view *w,
   Q3_TRY(check_view(q8, Q3_DT_I8));
   if (heads <= 0 || x->cols != static_cast<uint32_t>(heads) * 128) return unsupported();
   if (q8->rows < x->rows || q8->cols < x->cols) return Q3_ERR_VIEW;
-  if (!scale || !scale->data) return Q3_ERR_ARG;
-  if (scale->dtype != Q3_DT_F32) return Q3_ERR_DTYPE;
-  if (scale->row_bytes % 4 || scale->col_bytes % 4 || scale->col_bytes == 0) return Q3_ERR_VIEW;
+  Q3_TRY(check_scales(scale, x->rows, static_cast<uint32_t>(heads)));
   q3::NrqArgs r{};
   int64_t nws = 1;
   Q3_TRY(check_vec(w, 128, &nws));
@@ -398,6 +410,8 @@ int q3_attention_heads_gqa_tokscale_paged(const q3_view *q8,
   const uint32_t rows = q8->rows;
   if (q8->cols < static_cast<uint32_t>(heads) * 128 || o8->cols < q8->cols || o8->rows < rows)
     return Q3_ERR_VIEW;
+  Q3_TRY(check_scales(q_scale, rows, static_cast<uint32_t>(heads)));
+  Q3_TRY(check_scales(os, rows, static_cast<uint32_t>(heads)));
   if (causal && kv_len < rows) return Q3_ERR_RANGE;
   if (kv->row_bytes < static_cast<uint32_t>(kv_heads) * 128 ||
       kv->scale_row_bytes < static_cast<uint32_t>(kv_heads) * 4)
@@ -451,12 +465,10 @@ int q3_gemm_gate_up_swiglu_quant(const q3_view *a, const q3_view *a_scale,
   Q3_TRY(check_vec(wus, wu->rows, &wus_stride));
   if (wus_stride != g.bs_stride) return Q3_ERR_VIEW;
   Q3_TRY(check_view(s8, Q3_DT_I8));
-  if (!ss || !ss->data) return Q3_ERR_ARG;
-  if (ss->dtype != Q3_DT_F32) return Q3_ERR_DTYPE;
   const uint32_t N = wg->rows;
   if (N % 256 != 0) return unsupported();  // swiglu_quant.h:197 (256-column groups)
   if (s8->rows < a->rows || s8->cols < N) return Q3_ERR_VIEW;
-  if (ss->rows < a->rows || ss->cols < N / 256 || ss->row_bytes % 4 || ss->col_bytes % 4) return Q3_ERR_VIEW;
+  Q3_TRY(check_scales(ss, a->rows, N / 256));
   q3::GateUpArgs u{};
   u.M = g.M;
   u.N = g.N;
@@ -482,65 +494,95 @@ int q3_gemm_gate_up_swiglu_quant(const q3_view *a, const q3_view *a_scale,
 
 }  // extern "C"
 
-// ---- lm_head + argmax: per-device key workspace ---------------------------
+// ---- lm_head + argmax: key workspaces --------------------------------------
+// The argmax GEMM writes one 64-bit key per (row, column block) and
+// argmax_finish_kernel merges them, so a call needs M * slots keys of device
+// memory between its two launches.  Every key is written before it is read:
+// nothing has to start at zero.
 namespace {
-// One key per (row, column block): 4 MiB of slots (e.g. 256 rows x 1187
-// lm_head blocks of 128 columns).
 constexpr int kMaxArgmaxRows = 256;
+// 4 MiB of keys, e.g. 256 rows x 1187 lm_head blocks of 128 columns.
 constexpr int64_t kArgmaxSlots = int64_t(1) << 19;
-__device__ unsigned long long g_argmax_keys[kArgmaxSlots];
-}  // namespace
 
-namespace q3 {
-// Device address of the op-level argmax key workspace of the current device.
-unsigned long long *op_argmax_keys() {
-  static thread_local int cached_dev = -1;
-  static thread_local unsigned long long *cached = nullptr;
+// q3_gemm_nt_group_argmax: one workspace per (device, stream), allocated by
+// the first call on that stream and kept until the process ends, so calls on
+// different streams never share keys.
+struct StreamKeys {
+  int dev;
+  hipStream_t stream;
+  unsigned long long *keys;
+};
+std::mutex g_stream_keys_mu;
+std::vector<StreamKeys> g_stream_keys;
+
+unsigned long long *stream_keys(hipStream_t s) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return nullptr;
-  if (dev != cached_dev) {
-    void *p = nullptr;
-    if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_argmax_keys)) != hipSuccess) return nullptr;
-    cached = static_cast<unsigned long long *>(p);
-    cached_dev = dev;
-  }
-  return cached;
+  std::lock_guard<std::mutex> lock(g_stream_keys_mu);
+  for (const StreamKeys &e : g_stream_keys)
+    if (e.dev == dev && e.stream == s) return e.keys;
+  void *p = nullptr;
+  if (hipMalloc(&p, sizeof(unsigned long long) * kArgmaxSlots) != hipSuccess) return nullptr;
+  g_stream_keys.push_back({dev, s, static_cast<unsigned long long *>(p)});
+  return static_cast<unsigned long long *>(p);
 }
-}  // namespace q3
+
+// Validation of the argmax entry point; fills g (EPI_ARGMAX) and
+// the best/bidx strides.
+int argmax_common(const q3_view *a, const q3_view *a_scale, const q3_view *b,
+                  const q3_view *b_scale, const q3_view *best, const q3_view *bidx,
+                  uint32_t group_k, q3::GemmArgs &g, int64_t *bst, int64_t *ist, bool *skip) {
+  Q3_TRY(gemm_common(a, a_scale, b, b_scale, group_k, g, skip));
+  if (*skip) return Q3_OK;
+  if (!best || !best->data || !bidx || !bidx->data) return Q3_ERR_ARG;
+  if (best->dtype != Q3_DT_F32) return Q3_ERR_DTYPE;
+  if (bidx->dtype != Q3_DT_I32 && bidx->dtype != Q3_DT_U32) return Q3_ERR_DTYPE;
+  Q3_TRY(check_vec(best, a->rows, bst));
+  {
+    // bidx has the same shape rules as best but an integer dtype
+    q3_view tmp = *bidx;
+    tmp.dtype = Q3_DT_F32;
+    Q3_TRY(check_vec(&tmp, a->rows, ist));
+  }
+  if (a->rows > static_cast<uint32_t>(kMaxArgmaxRows)) {
+    *skip = true;
+    return unsupported();
+  }
+  g.epi = q3::EPI_ARGMAX;
+  const int nslots = argmax_slots(g);
+  if (static_cast<int64_t>(g.M) * nslots > kArgmaxSlots) {
+    *skip = true;
+    return unsupported();
+  }
+  g.keys_ld = nslots;
+  return Q3_OK;
+}
+
+int argmax_launch(q3::GemmArgs &g, unsigned long long *keys, const q3_view *best, int64_t bst,
+                  const q3_view *bidx, int64_t ist, hipStream_t s) {
+  g.keys = keys;
+  Q3_TRY(hip_status(launch_gemm_or_gemv(g, s)));
+  const int nslots = static_cast<int>(g.keys_ld);
+  return hip_status(q3::launch_argmax_finish(keys, nslots, nslots, g.M,
+                                             static_cast<float *>(best->data), bst,
+                                             static_cast<int32_t *>(bidx->data), ist, 0, nullptr,
+                                             nullptr, 0, s));
+}
+}  // namespace
 
 extern "C" int q3_gemm_nt_group_argmax(const q3_view *a, const q3_view *a_scale,
                                        const q3_view *b, const q3_view *b_scale,
                                        const q3_view *best, const q3_view *bidx,
                                        uint32_t group_k, void *stream) {
   q3::GemmArgs g;
-  bool skip = false;
-  Q3_TRY(gemm_common(a, a_scale, b, b_scale, group_k, g, &skip));
-  if (skip) return Q3_OK;
-  if (!best || !best->data || !bidx || !bidx->data) return Q3_ERR_ARG;
-  if (best->dtype != Q3_DT_F32) return Q3_ERR_DTYPE;
-  if (bidx->dtype != Q3_DT_I32 && bidx->dtype != Q3_DT_U32) return Q3_ERR_DTYPE;
-  if (a->rows > static_cast<uint32_t>(kMaxArgmaxRows)) return Q3_ERR_UNSUPPORTED;
   int64_t bst = 1, ist = 1;
-  Q3_TRY(check_vec(best, a->rows, &bst));
-  {
-    // bidx has the same shape rules as best but an integer dtype
-    q3_view tmp = *bidx;
-    tmp.dtype = Q3_DT_F32;
-    Q3_TRY(check_vec(&tmp, a->rows, &ist));
-  }
-  unsigned long long *keys = q3::op_argmax_keys();
-  if (!keys) return Q3_ERR_HIP;
-  g.epi = q3::EPI_ARGMAX;
-  g.keys = keys;
-  const int nslots = argmax_slots(g);
-  if (static_cast<int64_t>(g.M) * nslots > kArgmaxSlots) return Q3_ERR_UNSUPPORTED;
-  g.keys_ld = nslots;
+  bool skip = false;
+  Q3_TRY(argmax_common(a, a_scale, b, b_scale, best, bidx, group_k, g, &bst, &ist, &skip));
+  if (skip) return Q3_OK;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  Q3_TRY(hip_status(launch_gemm_or_gemv(g, s)));
-  return hip_status(q3::launch_argmax_finish(keys, nslots, nslots, g.M,
-                                             static_cast<float *>(best->data), bst,
-                                             static_cast<int32_t *>(bidx->data), ist, 0, nullptr,
-                                             nullptr, 0, s));
+  unsigned long long *keys = stream_keys(s);
+  if (!keys) return Q3_ERR_HIP;
+  return argmax_launch(g, keys, best, bst, bidx, ist, s);
 }
 
 extern "C" int q3_argmax_logits(const q3_view *logits, int32_t *out_id, void *stream) {

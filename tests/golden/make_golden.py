@@ -34,6 +34,7 @@ import hashlib  # noqa: E402
 import json  # noqa: E402
 import platform  # noqa: E402
 import sys  # noqa: E402
+import tempfile  # noqa: E402
 import time  # noqa: E402
 from pathlib import Path  # noqa: E402
 
@@ -287,10 +288,11 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--reference", default="/root/reference")
     ap.add_argument("--skip-full", action="store_true", help="only layout/exp/ops/cfg0")
-    ap.add_argument("--tmp", default=str(REPO / "_work" / "golden_tmp"))
+    ap.add_argument("--tmp", default=None,
+                    help="folder for the scratch blobs (default: a fresh temporary folder)")
     args = ap.parse_args()
     ref, pqwf, convert_pqwf = load_reference(Path(args.reference))
-    tmp = Path(args.tmp)
+    tmp = Path(args.tmp) if args.tmp else Path(tempfile.mkdtemp(prefix="q3_golden_"))
     tmp.mkdir(parents=True, exist_ok=True)
 
     libc_ver = platform.libc_ver()

@@ -1,0 +1,127 @@
+"""Host-side argument validation of the C ABI, without a GPU.
+
+Every case here must be rejected before anything is launched: an undersized
+output or scale view has to come back as Q3_ERR_VIEW (a kernel would
+otherwise write past it on the device), a degenerate layout as
+Q3_ERR_UNSUPPORTED, and the row limit of the argmax ops through the
+reference's silent-unsupported switch.  The data pointers are host
+addresses that are never dereferenced.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from q3ops import _lib
+from q3ops.layout import Layout, ModelShape
+
+OK, ERR_VIEW, ERR_UNSUPPORTED = 0, -3, -4
+DT_I8, DT_I32, DT_F32 = _lib.DT_I8, _lib.DT_I32, _lib.DT_F32
+_ARENA = np.zeros(1 << 16, np.uint8)  # a 16-byte aligned, never-read address
+_ADDR = (_ARENA.ctypes.data + 255) & ~255
+
+
+def V(rows, cols, dt, row_bytes=None, col_bytes=None):
+    es = 1 if dt == DT_I8 else 4
+    rb = cols * es if row_bytes is None else row_bytes
+    cb = es if col_bytes is None else col_bytes
+    return C.byref(_lib.View(_ADDR, rb, cb, rows, cols, dt))
+
+
+def gemm_operands(M, K, N, group=256):
+    return (V(M, K, DT_I8), V(M, K // group, DT_F32), V(N, K, DT_I8), V(N, 1, DT_F32))
+
+
+def paged(row_bytes=1024, scale_row_bytes=32):
+    return _lib.PagedKV(_ADDR, _ADDR, _ADDR, _ADDR, _ADDR, 32, 32 * row_bytes, row_bytes,
+                        32 * scale_row_bytes, scale_row_bytes)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.lib()
+
+
+def test_head_quant_epilogue_scale_shape(lib):
+    M, K, N = 8, 1024, 1024
+    a, as_, b, bs = gemm_operands(M, K, N)
+    q8 = V(M, N, DT_I8)
+    for qs in (V(M - 1, N // 128, DT_F32),        # too few rows
+               V(M, N // 128 - 1, DT_F32),        # too few heads
+               V(M, N // 128, DT_F32, col_bytes=0),
+               V(M, N // 128, DT_F32, row_bytes=16, col_bytes=8)):  # rows overlap
+        assert lib.q3_gemm_nt_group_store(a, as_, b, bs, None, 256, None, q8, qs, None, None,
+                                          None, C.c_float(0), None) == ERR_VIEW
+
+
+def test_attention_scale_shapes(lib):
+    rows, heads, kvh = 4, 16, 8
+    kv = paged()
+    q8, o8 = V(rows, heads * 128, DT_I8), V(rows, heads * 128, DT_I8)
+    good = V(rows, heads, DT_F32)
+    for qsc, osc in ((V(rows - 1, heads, DT_F32), good), (V(rows, heads - 1, DT_F32), good),
+                     (good, V(rows - 1, heads, DT_F32)), (good, V(rows, heads - 2, DT_F32))):
+        assert lib.q3_attention_heads_gqa_tokscale_paged(q8, qsc, C.byref(kv), 64, o8, osc, heads,
+                                                         kvh, 128, 1, C.c_float(0.088),
+                                                         None) == ERR_VIEW
+
+
+def test_kv_paged_scale_row_bytes(lib):
+    M, K, N = 8, 1024, 1024
+    a, as_, b, bs = gemm_operands(M, K, N)
+    kv = paged(scale_row_bytes=16)  # 4 heads' scales for an 8-head projection
+    assert lib.q3_gemm_nt_group_kv_paged(a, as_, b, bs, 256, C.byref(kv), 0, 1, None, None,
+                                         None, C.c_float(0), None) == ERR_VIEW
+
+
+def test_norm_rope_quant_scale_shape(lib):
+    x, q8 = V(6, 1024, DT_F32), V(6, 1024, DT_I8)
+    w = V(128, 1, DT_F32)
+    for sc in (V(6, 7, DT_F32), V(5, 8, DT_F32)):
+        assert lib.q3_norm_rope_quant_heads(x, w, None, None, q8, sc, 8, C.c_float(1 / 128), 0,
+                                            None) == ERR_VIEW
+
+
+def test_gate_up_scale_shape(lib):
+    M, K, N = 8, 1024, 3072
+    a, as_, wg, wgs = gemm_operands(M, K, N)
+    s8 = V(M, N, DT_I8)
+    for ss in (V(M, N // 256 - 1, DT_F32), V(M, N // 256, DT_F32, col_bytes=0)):
+        assert lib.q3_gemm_gate_up_swiglu_quant(a, as_, wg, wgs, wg, wgs, s8, ss, 256,
+                                                None) == ERR_VIEW
+
+
+@pytest.mark.parametrize("fn", ["q3_gemm_nt_group_argmax"])
+def test_argmax_row_limit_is_unsupported(lib, fn):
+    """More than 256 rows: Q3_ERR_UNSUPPORTED, or a silent no-op with the
+    reference's behaviour switched on (kernels/lm_argmax.h:82)."""
+    M, K, N = 300, 1024, 1024
+    a, as_, b, bs = gemm_operands(M, K, N)
+    best, bidx = V(M, 1, DT_F32), V(M, 1, DT_I32)
+    f = getattr(lib, fn)
+    assert f(a, as_, b, bs, best, bidx, 256, None) == ERR_UNSUPPORTED
+    prev = lib.q3_set_silent_unsupported(1)
+    try:
+        assert f(a, as_, b, bs, best, bidx, 256, None) == OK
+    finally:
+        lib.q3_set_silent_unsupported(prev)
+
+
+def test_model_open_rejects_zero_kv_heads(lib):
+    lay = Layout(ModelShape(layers=1, vocab=1024))
+    c = _lib.CLayout.from_buffer_copy(lay.c)
+    c.kv_heads = 0
+    h = C.c_void_p()
+    assert lib.q3_model_open(C.c_void_p(_ADDR), C.byref(c), None, C.byref(h)) == ERR_UNSUPPORTED
+    assert not h.value
+
+
+def test_argmax_key_limit(lib):
+    """More keys than the 2^19-slot workspace (256 rows x 2374 column blocks
+    of 128): rejected before launch."""
+    M, K, N = 256, 1024, 2374 * 128
+    a, as_, b, bs = gemm_operands(M, K, N)
+    best, bidx = V(M, 1, DT_F32), V(M, 1, DT_I32)
+    assert lib.q3_gemm_nt_group_argmax(a, as_, b, bs, best, bidx, 256, None) == ERR_UNSUPPORTED

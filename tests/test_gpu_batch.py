@@ -31,7 +31,13 @@ from q3ops.model import Model  # noqa: E402
 PAGE = 32
 Q3_ERR_RANGE = -7  # include/q3ops.h
 LD_TABLE = 8  # pages per sequence table (contexts up to 254 tokens + 2 steps)
-SHAPE = ModelShape(layers=2, vocab=1024, seq=64, max_seq=16384)
+# Contexts around the batched attention's chunk of 12 blocks of 32 keys
+# (384 keys): one short of a chunk, exactly one, one over, two chunks +- 1,
+# and config 4's 2048-token contexts (6 chunks, the last one partial after
+# the steps); the longest needs 65 table entries.
+LONG_CTX = [383, 384, 385, 767, 768, 769, 1535, 2046, 2047, 2048]
+LD_TABLE_LONG = 66
+SHAPE = ModelShape(layers=2, vocab=1024, seq=64, max_seq=32768)
 INIT = InitConfig(n_prompt=1, n_gen=0, mode=0)
 _cache = {}
 
@@ -55,21 +61,26 @@ def pool_views(lay: Layout, raw: np.ndarray) -> dict[str, np.ndarray]:
     }
 
 
-def make_case(n: int, seed: int):
+def make_case(n: int, seed: int, edge: list[int] | None = None, ld_table: int = LD_TABLE):
     """Blob with n random contexts in disjoint random pages; per-row positions
     and tables; the contexts in dense form for the oracle."""
-    key = (n, seed)
+    key = (n, seed, tuple(edge or ()), ld_table)
     if key in _cache:
         return _cache[key]
     lay = Layout(SHAPE)
     blob = init_random_blob(lay, INIT)
     rng = np.random.default_rng(seed)
     # edge contexts first: empty, one short of a page, exactly one page, one over
-    edge = [0, 31, 32, 33, 62, 63, 64, 254]
-    ctx = np.array((edge + list(rng.integers(1, 255, size=max(0, n - len(edge)))))[:n], np.int32)
+    top = 255
+    if edge is None:
+        edge = [0, 31, 32, 33, 62, 63, 64, 254]
+    else:  # the other rows: random contexts up to the longest edge context
+        top = max(edge) + 1
+    ctx = np.array((edge + list(rng.integers(1, top, size=max(0, n - len(edge)))))[:n], np.int32)
+    assert int(ctx.max()) + 2 <= ld_table * PAGE
     n_pages = lay.max_seq // PAGE
     perm = rng.permutation(n_pages).astype(np.uint16)
-    tables = np.full((n, LD_TABLE), 0xFFFF, np.uint16)  # unused slots: out of range on purpose
+    tables = np.full((n, ld_table), 0xFFFF, np.uint16)  # unused slots: out of range on purpose
     need = [(int(c) + 2 + PAGE - 1) // PAGE for c in ctx]
     nxt = 0
     for r in range(n):
@@ -137,10 +148,7 @@ def gpu_new_rows(m: Model, lay: Layout, tables, pos) -> list[dict]:
     return per_layer
 
 
-@pytest.mark.parametrize("n", [1, 5, 20, 64])
-def test_decode_batch_matches_oracle(cuda, n):
-    note(f"decode_batch n={n}")
-    lay, blob, ctx, tables, dense, ids0 = make_case(n, seed=100 + n)
+def run_batch_case(cuda, n, lay, blob, ctx, tables, dense, ids0):
     steps = 2
     ref = oracle_steps(lay, blob, ctx, dense, ids0, steps)
     m = Model(lay, blob)
@@ -170,6 +178,24 @@ def test_decode_batch_matches_oracle(cuda, n):
         ids = out.clone()
     m.close()
     assert not probs, probs
+
+
+@pytest.mark.parametrize("n", [1, 5, 20, 64])
+def test_decode_batch_matches_oracle(cuda, n):
+    note(f"decode_batch n={n}")
+    run_batch_case(cuda, n, *make_case(n, seed=100 + n))
+
+
+@pytest.mark.parametrize("n", [len(LONG_CTX), 24])
+def test_decode_batch_long_contexts(cuda, n):
+    """Contexts that cross the batched attention's 384-key chunks, up to
+    config 4's 2048 tokens: the (maximum, denominator, result) state of both
+    query heads of a GQA group carried from chunk to chunk (attention_gqa.h:
+    404-547 walks the blocks in one recurrence; the kernel splits it into
+    chunks of 12 blocks)."""
+    note(f"decode_batch long contexts n={n}")
+    run_batch_case(cuda, n, *make_case(n, seed=300 + n, edge=list(LONG_CTX),
+                                       ld_table=LD_TABLE_LONG))
 
 
 def test_decode_batch_rejects_bad_rows(cuda):

@@ -198,3 +198,76 @@ def test_cfg3_greedy(cuda, gold_meta):
     probs = stage_problems(g, f"f{last}_", m, 1, 21, lay.layers - 1, last_row_only=True)
     m.close()
     assert not probs, probs
+
+
+# Config 3's perf prefill as one 512-row chunk (layout seq = 512) on a
+# 2-layer, vocab-1024 model with the same seeds; the oracle runs the same
+# prompt as sixteen 32-row chunks (a row's arithmetic does not depend on the
+# chunk it is computed in: ref_qwen3.py:366-444 is row-wise except for the
+# causal attention, which walks the row's keys in the same 32-key blocks).
+SHAPE_512 = ModelShape(layers=2, vocab=1024, seq=512, max_seq=640)
+INIT_512 = InitConfig(n_prompt=512, n_gen=4, mode=0)
+
+
+def oracle_512(blob, lay):
+    import oracle
+    dims = dict(SHAPE_512.__dict__)
+    dims["seq"] = 32
+    return oracle.OracleModel(blob, lay.offsets, dims)
+
+
+def test_cfg3_prefill_512_chunk_stages(cuda):
+    """One 512-row q3_forward_chunk against the oracle's 16 chunks of 32:
+    every recorded stage of the last layer for all 512 rows, both layers'
+    K/V pages (all 16 pages, through a shuffled page table) and the logits."""
+    note("512-row prefill chunk, 2 layers, stages + K/V pages + logits")
+    lay, blob = host_blob("cfg3_perf", shape=SHAPE_512, init=INIT_512)
+    om = oracle_512(blob, lay)
+    ids = lay.global_views(blob)["ids"][:512].copy()
+    recs, logits = [], None
+    for c in range(16):
+        lg, rec = om.forward_chunk(ids[32 * c:32 * (c + 1)], 32 * c, 32, c == 15, record=True)
+        recs.append(rec)
+        logits = lg
+    ref = {k: np.concatenate([r[k] for r in recs]) for k in recs[0]}
+    m = Model(lay, blob)
+    tab = np.arange(lay.max_seq // 32, dtype=np.uint16)
+    np.random.default_rng(5).shuffle(tab)
+    m.set_page_table(tab)
+    m.forward_chunk(0, 512, LM_LOGITS, optimize_tail=False)
+    probs = []
+    got = m.stage("logits", 1)[0]
+    if not bits_equal(got, logits):
+        probs.append(f"logits: {describe_diff(got, logits)}")
+    for st in ("h", "h8", "hs", "q8", "qs", "o8", "os", "s8", "ss", "x"):
+        g = m.stage(st, 512)
+        e = ref[st]
+        if st in ("q8", "qs"):  # row 0 doubles as the final-norm scratch (compare.py:197-205)
+            g, e = g[1:], e[1:]
+        if not bits_equal(g, e):
+            probs.append(f"{st}: {describe_diff(g, e)}")
+    for li in range(lay.layers):
+        caches = m.kv_cache(li, 512)
+        for st, arr in (("kc", om.k8), ("ks", om.k_s), ("vc", om.v8), ("vs", om.v_s)):
+            e = arr[li, :512]
+            if not bits_equal(caches[st], e):
+                probs.append(f"layer {li} {st}: {describe_diff(caches[st], e)}")
+    m.close()
+    assert not probs, probs
+
+
+def test_cfg3_prefill_512_generate(cuda):
+    """q3_generate with CTRL [512, 4, mode 0]: one 512-row prefill chunk, then
+    four greedy decode steps; ids and the fused argmax equal the oracle's."""
+    note("512-row prefill + 4 greedy tokens, 2 layers")
+    lay, blob = host_blob("cfg3_perf", shape=SHAPE_512, init=INIT_512)
+    om = oracle_512(blob, lay)
+    logits, gen, _, _ = om.generate(lay.global_views(blob)["ids"], 512, 4, record=False)
+    m = Model(lay, blob)
+    m.set_ctrl(512, 4, 0)
+    m.generate()
+    got = m.ids()[512:516]
+    best, idx = m.argmax()
+    m.close()
+    assert np.array_equal(got, gen), (got, gen)
+    assert idx == int(np.argmax(logits)) and bits_equal(np.float32(best), logits.max())

@@ -59,13 +59,15 @@ def test_gemm_store(cuda, M, K, N, group):
     assert bits_equal(got, ref), describe_diff(got, ref)
 
 
-def test_gemm_2048_rows(cuda):
-    note("gemm store M=2048 K=3072 N=1024")
-    rng = np.random.default_rng(99)
-    a, as_, b, bs = rand_gemm(rng, 2048, 3072, 1024, 256)
-    out = torch.zeros((2048, 1024), dtype=torch.float32, device=cuda)
-    ops.gemm_nt_group_store(dev(a), dev(as_), dev(b), dev(bs), out, 256)
-    ref = oracle.gemm_nt_group(a, as_, b, bs, 256)
+@pytest.mark.parametrize("K,N,group", SHAPES)
+def test_gemm_2048_rows(cuda, K, N, group):
+    """BASELINE config 1's largest M on each of its five (K, N) shapes."""
+    note(f"gemm store M=2048 K={K} N={N} g={group}")
+    rng = np.random.default_rng(99 + K + N)
+    a, as_, b, bs = rand_gemm(rng, 2048, K, N, group)
+    out = torch.zeros((2048, N), dtype=torch.float32, device=cuda)
+    ops.gemm_nt_group_store(dev(a), dev(as_), dev(b), dev(bs), out, group)
+    ref = oracle.gemm_nt_group(a, as_, b, bs, group)
     got = host(out)
     assert bits_equal(got, ref), describe_diff(got, ref)
 
@@ -88,6 +90,22 @@ def test_gemm_residual_add(cuda, M):
     xt = dev(x)
     ops.gemm_nt_group_store(dev(a), dev(as_), dev(b), dev(bs), None, 128, add=xt)
     ref = (x + oracle.gemm_nt_group(a, as_, b, bs, 128)).astype(F)
+    got = host(xt)
+    assert bits_equal(got, ref), describe_diff(got, ref)
+
+
+@pytest.mark.parametrize("M", [1, 32, 512, 2048])
+@pytest.mark.parametrize("K,N,group", SHAPES)
+def test_gemm_residual_config1_grid(cuda, M, K, N, group):
+    """f32 output with residual add (group_gemm.h:194-214)
+    over its whole M x (K, N) grid: x = D + x."""
+    note(f"gemm residual M={M} K={K} N={N} g={group}")
+    rng = np.random.default_rng(7 * M + K + 3 * N)
+    a, as_, b, bs = rand_gemm(rng, M, K, N, group)
+    x = rng.normal(size=(M, N)).astype(F)
+    xt = dev(x)
+    ops.gemm_nt_group_store(dev(a), dev(as_), dev(b), dev(bs), None, group, add=xt)
+    ref = (oracle.gemm_nt_group(a, as_, b, bs, group) + x).astype(F)
     got = host(xt)
     assert bits_equal(got, ref), describe_diff(got, ref)
 
@@ -305,6 +323,30 @@ def test_lm_argmax(cuda, N):
     bidx2 = torch.tensor([-5], dtype=torch.int32, device=cuda)
     ops.gemm_nt_group_argmax(dev(a), dev(as_), dev(b), dev(bs), best2, bidx2, 256)
     assert int(host(bidx2)[0]) == -5 and host(best2)[0] == np.float32(1e30)
+
+
+def test_lm_argmax_two_streams(cuda):
+    """Two argmax calls in flight at once on two streams (each stream has its
+    own key workspace): both results equal the oracle's."""
+    rng = np.random.default_rng(123)
+    cases = [rand_gemm(rng, M, 1024, 151936, 256) for M in (24, 7)]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    ins = [tuple(dev(t) for t in c) for c in cases]
+    outs = []
+    torch.cuda.synchronize()
+    for (ta, tas, tb, tbs), st in zip(ins, streams):
+        M = ta.shape[0]
+        with torch.cuda.stream(st):
+            best = torch.full((M,), -3.0e38, dtype=torch.float32, device=cuda)
+            bidx = torch.zeros(M, dtype=torch.int32, device=cuda)
+            for _ in range(3):  # repeated, so the two streams' launches interleave
+                ops.gemm_nt_group_argmax(ta, tas, tb, tbs, best, bidx, 256, stream=st)
+            outs.append((best, bidx))
+    torch.cuda.synchronize()
+    for (a, as_, b, bs), (best, bidx) in zip(cases, outs):
+        logits = oracle.gemm_nt_group(a, as_, b, bs, 256)
+        assert bidx.cpu().numpy().tolist() == [int(i) for i in np.argmax(logits, axis=1)]
+        assert bits_equal(best.cpu().numpy(), logits.max(axis=1))
 
 
 @pytest.mark.parametrize("M", [2, 5, 16, 33, 64, 100])
