@@ -197,6 +197,20 @@ int q3_gemm_nt_group_argmax(const q3_view *a, const q3_view *a_scale,
                             const q3_view *best, const q3_view *bidx,
                             uint32_t group_k, void *stream);
 
+/* No counterpart in the reference.  q3_gemm_nt_group_argmax for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops
+ * that forbid hipMalloc): same arguments, results and limits, but its keys
+ * live in one fixed 4 MiB array of the library's device image (each device
+ * holds its own copy until the process ends) and the call never allocates.
+ * Shapes needing more than 2^19 keys (M x column blocks) are rejected with
+ * Q3_ERR_UNSUPPORTED.  Every call on a device shares that device's array:
+ * calls that overlap on one GPU (other streams, other host threads) race and
+ * must be serialised by the caller. */
+int q3_gemm_nt_group_argmax_noalloc(const q3_view *a, const q3_view *a_scale,
+                                    const q3_view *b, const q3_view *b_scale,
+                                    const q3_view *best, const q3_view *bidx,
+                                    uint32_t group_k, void *stream);
+
 /* main_big.cpp:300-322 argmax_logits: greedy pick over row 0 of logits
  * (per 32-column block, ordered-key comparison across blocks); the id is
  * written to *out_id (device i32). */

@@ -503,6 +503,7 @@ namespace {
 constexpr int kMaxArgmaxRows = 256;
 // 4 MiB of keys, e.g. 256 rows x 1187 lm_head blocks of 128 columns.
 constexpr int64_t kArgmaxSlots = int64_t(1) << 19;
+constexpr int kMaxDevices = 64;
 
 // q3_gemm_nt_group_argmax: one workspace per (device, stream), allocated by
 // the first call on that stream and kept until the process ends, so calls on
@@ -527,7 +528,43 @@ unsigned long long *stream_keys(hipStream_t s) {
   return static_cast<unsigned long long *>(p);
 }
 
-// Validation of the argmax entry point; fills g (EPI_ARGMAX) and
+// q3_gemm_nt_group_argmax_noalloc: a fixed key array in the library's own
+// device image (each device holds its own copy until the process ends).  In
+// host code `scratch` names a host-side stand-in, never device memory: its
+// device address comes from hipGetSymbolAddress, taken once per device with
+// that device current, and only that address is handed to kernels.
+constexpr int64_t kScratchSlots = int64_t(1) << 19;  // 4 MiB
+static __device__ __align__(256) unsigned long long scratch[kScratchSlots];
+std::mutex g_scratch_mu;
+std::atomic<unsigned long long *> g_scratch_ptr[kMaxDevices];
+
+unsigned long long *device_scratch(int *status) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    *status = Q3_ERR_HIP;
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    *status = Q3_ERR_UNSUPPORTED;
+    return nullptr;
+  }
+  unsigned long long *p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p) return p;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+  if (!p) {
+    void *addr = nullptr;
+    if (hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)) != hipSuccess || !addr) {
+      *status = Q3_ERR_HIP;
+      return nullptr;
+    }
+    p = static_cast<unsigned long long *>(addr);
+    g_scratch_ptr[dev].store(p, std::memory_order_release);
+  }
+  return p;
+}
+
+// Validation shared by both argmax entry points; fills g (EPI_ARGMAX) and
 // the best/bidx strides.
 int argmax_common(const q3_view *a, const q3_view *a_scale, const q3_view *b,
                   const q3_view *b_scale, const q3_view *best, const q3_view *bidx,
@@ -583,6 +620,22 @@ extern "C" int q3_gemm_nt_group_argmax(const q3_view *a, const q3_view *a_scale,
   unsigned long long *keys = stream_keys(s);
   if (!keys) return Q3_ERR_HIP;
   return argmax_launch(g, keys, best, bst, bidx, ist, s);
+}
+
+extern "C" int q3_gemm_nt_group_argmax_noalloc(const q3_view *a, const q3_view *a_scale,
+                                               const q3_view *b, const q3_view *b_scale,
+                                               const q3_view *best, const q3_view *bidx,
+                                               uint32_t group_k, void *stream) {
+  q3::GemmArgs g;
+  int64_t bst = 1, ist = 1;
+  bool skip = false;
+  Q3_TRY(argmax_common(a, a_scale, b, b_scale, best, bidx, group_k, g, &bst, &ist, &skip));
+  if (skip) return Q3_OK;
+  if (g.keys_ld * static_cast<int64_t>(g.M) > kScratchSlots) return unsupported();
+  int status = Q3_OK;
+  unsigned long long *keys = device_scratch(&status);
+  if (!keys) return status;
+  return argmax_launch(g, keys, best, bst, bidx, ist, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int q3_argmax_logits(const q3_view *logits, int32_t *out_id, void *stream) {

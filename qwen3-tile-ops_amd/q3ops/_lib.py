@@ -88,6 +88,7 @@ SIGNATURES = {
                                                    _F, _VP]),
     "q3_gemm_gate_up_swiglu_quant": (_I, [_PV, _PV, _PV, _PV, _PV, _PV, _PV, _PV, _U, _VP]),
     "q3_gemm_nt_group_argmax": (_I, [_PV, _PV, _PV, _PV, _PV, _PV, _U, _VP]),
+    "q3_gemm_nt_group_argmax_noalloc": (_I, [_PV, _PV, _PV, _PV, _PV, _PV, _U, _VP]),
     "q3_argmax_logits": (_I, [_PV, _VP, _VP]),
     "q3_layout_compute": (_I, [_U] * 9 + [C.POINTER(CLayout)]),
     "q3_layout_header_text": (_I, [C.POINTER(CLayout), C.c_char_p, C.c_size_t]),

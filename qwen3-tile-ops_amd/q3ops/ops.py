@@ -152,6 +152,16 @@ def gemm_nt_group_argmax(a, a_scale, b, b_scale, best, bidx, group_k=128, stream
           "gemm_nt_group_argmax")
 
 
+def gemm_nt_group_argmax_noalloc(a, a_scale, b, b_scale, best, bidx, group_k=128, stream=None):
+    """gemm_nt_group_argmax with the library's fixed device key array instead
+    of an allocated workspace (no reference counterpart; for callers that
+    cannot allocate).  Calls that overlap on one GPU race."""
+    check(lib().q3_gemm_nt_group_argmax_noalloc(view(a), view(a_scale), view(b), view(b_scale),
+                                                view(best), view(bidx), group_k,
+                                                _stream(stream)),
+          "gemm_nt_group_argmax_noalloc")
+
+
 def argmax_logits(logits, out_id, stream=None):
     """main_big.cpp:300-322 (out_id: int32 device tensor, element 0)."""
     check(lib().q3_argmax_logits(view(logits), C.c_void_p(out_id.data_ptr()), _stream(stream)),
@@ -161,4 +171,4 @@ def argmax_logits(logits, out_id, stream=None):
 __all__ = ["view", "paged_kv", "embedding_rmsnorm_rows", "rmsnorm_rows", "quant_rows_heads",
            "gemm_nt_group_store", "gemm_nt_group_kv_paged", "norm_rope_quant_heads",
            "attention_heads_gqa_tokscale_paged", "gemm_gate_up_swiglu_quant",
-           "gemm_nt_group_argmax", "argmax_logits", "LM_ARGMAX"]
+           "gemm_nt_group_argmax", "gemm_nt_group_argmax_noalloc", "argmax_logits", "LM_ARGMAX"]

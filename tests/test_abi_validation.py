@@ -93,7 +93,7 @@ def test_gate_up_scale_shape(lib):
                                                 None) == ERR_VIEW
 
 
-@pytest.mark.parametrize("fn", ["q3_gemm_nt_group_argmax"])
+@pytest.mark.parametrize("fn", ["q3_gemm_nt_group_argmax", "q3_gemm_nt_group_argmax_noalloc"])
 def test_argmax_row_limit_is_unsupported(lib, fn):
     """More than 256 rows: Q3_ERR_UNSUPPORTED, or a silent no-op with the
     reference's behaviour switched on (kernels/lm_argmax.h:82)."""
@@ -118,10 +118,12 @@ def test_model_open_rejects_zero_kv_heads(lib):
     assert not h.value
 
 
-def test_argmax_key_limit(lib):
-    """More keys than the 2^19-slot workspace (256 rows x 2374 column blocks
-    of 128): rejected before launch."""
+def test_argmax_noalloc_key_limit(lib):
+    """More keys than the fixed 2^19-slot array (256 rows x 2374 column
+    blocks of 128): rejected before launch, like the allocating entry point,
+    whose per-stream workspace has the same size."""
     M, K, N = 256, 1024, 2374 * 128
     a, as_, b, bs = gemm_operands(M, K, N)
     best, bidx = V(M, 1, DT_F32), V(M, 1, DT_I32)
-    assert lib.q3_gemm_nt_group_argmax(a, as_, b, bs, best, bidx, 256, None) == ERR_UNSUPPORTED
+    for fn in (lib.q3_gemm_nt_group_argmax_noalloc, lib.q3_gemm_nt_group_argmax):
+        assert fn(a, as_, b, bs, best, bidx, 256, None) == ERR_UNSUPPORTED
