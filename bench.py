@@ -56,6 +56,36 @@ def time_events(fn, reps: int, stream) -> float:
     return start.elapsed_time(end) / reps
 
 
+def time_graph(launch, count: int, stream, replays: int = 3) -> float:
+    """Average milliseconds per launch of `count` back-to-back launches
+    (launch(i), i = 0..count-1) captured into one HIP graph on `stream` and
+    replayed: the launches reach the GPU without host submission gaps, which
+    at a few microseconds per kernel would otherwise dominate (each ctypes
+    call through the C ABI costs the host about 10 us).  One eager pass
+    first sets up everything a first call does (function attributes,
+    workspaces); HIP events on `stream` time the replays."""
+    import torch
+    for i in range(min(count, 2)):
+        launch(i)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for i in range(count):
+            launch(i)
+    g.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(replays):
+        g.replay()
+    end.record(stream)
+    end.synchronize()
+    ms = start.elapsed_time(end) / (replays * count)
+    del g
+    return ms
+
+
 def kernel_rooflines(stream) -> dict:
     """Times single-kernel shapes of the path through the C ABI, on the
     stream they are launched on, and derives achieved bandwidth / ops."""
@@ -84,14 +114,12 @@ def kernel_rooflines(stream) -> dict:
     a, as_ = t8(1, H), tf(1, H // 256)
     best = torch.empty(1, dtype=torch.float32, device=dev)
     bidx = torch.empty(1, dtype=torch.int32, device=dev)
-    it = [0]
 
-    def lm():
-        w, s = ws[it[0] % len(ws)]
-        it[0] += 1
+    def lm(i):
+        w, s = ws[i % len(ws)]
         ops.gemm_nt_group_argmax(a, as_, w, s, best, bidx, 256, stream=stream)
 
-    ms = time_events(lm, 20, stream)
+    ms = time_graph(lm, 24, stream)
     byts = V * H + 4 * V + H + 4 * (H // 256) + 8
     res["lm_argmax_gemv"] = {"ms": ms, "bytes": byts, "GBs": byts / ms / 1e6, "bound": "hbm"}
     del ws
@@ -102,12 +130,11 @@ def kernel_rooflines(stream) -> dict:
     s8 = torch.empty((1, I), dtype=torch.int8, device=dev)
     ss = torch.empty((1, I // 256), dtype=torch.float32, device=dev)
 
-    def gu1():
-        wg, wgs, wu, wus = ws[it[0] % len(ws)]
-        it[0] += 1
+    def gu1(i):
+        wg, wgs, wu, wus = ws[i % len(ws)]
         ops.gemm_gate_up_swiglu_quant(a, as_, wg, wgs, wu, wus, s8, ss, 256, stream=stream)
 
-    ms = time_events(gu1, 50, stream)
+    ms = time_graph(gu1, 64, stream)
     byts = 2 * I * H + 8 * I + H + 16 + I + 4 * (I // 256)
     res["gate_up_gemv_m1"] = {"ms": ms, "bytes": byts, "GBs": byts / ms / 1e6, "bound": "hbm"}
     del ws
@@ -118,11 +145,84 @@ def kernel_rooflines(stream) -> dict:
     wg, wgs, wu, wus = t8(I, H), tf(I), t8(I, H), tf(I)
     s85 = torch.empty((M, I), dtype=torch.int8, device=dev)
     ss5 = torch.empty((M, I // 256), dtype=torch.float32, device=dev)
-    ms = time_events(lambda: ops.gemm_gate_up_swiglu_quant(a5, as5, wg, wgs, wu, wus, s85, ss5, 256,
-                                                           stream=stream), 20, stream)
+    ms = time_graph(lambda i: ops.gemm_gate_up_swiglu_quant(a5, as5, wg, wgs, wu, wus, s85, ss5, 256,
+                                                            stream=stream), 32, stream)
     flops = 2 * M * (2 * I) * H
     res["gate_up_gemm_m512"] = {"ms": ms, "ops": flops, "TOPs": flops / ms / 1e9, "bound": "mfma"}
     return res
+
+
+# the per-group int8 GEMM with f32 output and residual add
+# over M x (K, N, group) (Q, K+V, gate+up, down, O).
+CFG1_SHAPES = [(1024, 2048, 256, "Q"), (1024, 1024, 256, "K+V"), (1024, 6144, 256, "gate+up"),
+               (3072, 1024, 256, "down"), (2048, 1024, 128, "O")]
+CFG1_M = [1, 32, 512, 2048]
+CFG1_ROTATE_BYTES = 1 << 30  # every launch reads operands the 256 MB MALL does not hold
+
+
+def cfg1_bytes(M: int, K: int, N: int, group: int, per_group: bool) -> int:
+    """Algorithmic HBM bytes of one launch: weights and their scales, the A
+    operand and its per-group scales, the residual read and the result
+    written (f32)."""
+    ng = K // group
+    return N * K + 4 * N * (ng if per_group else 1) + M * K + 4 * M * ng + 8 * M * N
+
+
+def run_cfg1(stream, reps_min: int = 64) -> dict:
+    """Times q3_gemm_nt_group_store with the residual epilogue on every
+    config-1 shape, with per-row and with per-(row, group) B scales.  Each
+    (shape, M) rotates over enough operand sets (weights, scales, A, x) that
+    the launches stream >= 1 GiB of distinct data, so the last-level cache
+    cannot serve repeated reads; HIP events on the launch stream give the
+    average launch time (the launches replayed from one HIP graph, so that
+    host submission does not pace them).  Reported against the attainable bound
+    min(int8 peak, arithmetic intensity x HBM peak)."""
+    import torch
+    from q3ops import ops
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0x5EED0001)
+    rows = []
+    for K, N, group, name in CFG1_SHAPES:
+        ng = K // group
+        for M in CFG1_M:
+            per_set = cfg1_bytes(M, K, N, group, True)
+            R = max(2, min(1024, -(-CFG1_ROTATE_BYTES // per_set)))
+            with torch.cuda.stream(stream):
+                B = torch.randint(-127, 128, (R, N, K), dtype=torch.int8, device=dev, generator=gen)
+                A = torch.randint(-127, 128, (R, M, K), dtype=torch.int8, device=dev, generator=gen)
+                AS = torch.rand((R, M, ng), device=dev, generator=gen) * 0.099 + 1e-3
+                BS = torch.rand((R, N, 1), device=dev, generator=gen) * 0.099 + 1e-3
+                BSG = torch.rand((R, N, ng), device=dev, generator=gen) * 0.099 + 1e-3
+                X = torch.randn((R, M, N), device=dev, generator=gen)
+            stream.synchronize()
+            for per_group in (False, True):
+                scales = BSG if per_group else BS
+
+                def launch(j):
+                    i = j % R
+                    ops.gemm_nt_group_store(A[i], AS[i], B[i], scales[i], None, group, add=X[i],
+                                            stream=stream)
+
+                ms = time_graph(launch, max(reps_min, R), stream)
+                byts = cfg1_bytes(M, K, N, group, per_group)
+                ops_n = 2 * M * N * K
+                tops = ops_n / ms / 1e9
+                gbs = byts / ms / 1e6
+                bound_tops = min(INT8_PEAK_TOPS, ops_n / byts * HBM_PEAK_GBS / 1e3)
+                rows.append({"shape": name, "M": M, "K": K, "N": N, "group": group,
+                             "b_scale": "row+group" if per_group else "row", "us": ms * 1e3,
+                             "TOPs": tops, "GBs": gbs, "bytes": byts,
+                             "bound": "hbm" if bound_tops < INT8_PEAK_TOPS else "mfma",
+                             "frac_of_attainable": tops / bound_tops,
+                             "frac_of_int8_peak": tops / INT8_PEAK_TOPS,
+                             "frac_of_hbm_peak": gbs / HBM_PEAK_GBS, "rotated_sets": R})
+            del A, AS, B, BS, BSG, X
+            torch.cuda.empty_cache()
+    return {"workload": ("config 1: q3_gemm_nt_group_store with residual add, int8 U[-127,127] "
+                         "operands, scales U(1e-3,1e-1), x N(0,1); operand sets rotated over "
+                         ">= 1 GiB"), "shapes": rows}
 
 
 # Algorithmic HBM bytes of one launch of each decode kernel class (model
@@ -366,10 +466,10 @@ def run_cfg4(args) -> dict:
                            "traffic": None, "avg_us": avg * 1e3, "bytes_per_launch": int(byts),
                            "launches": n, "share_of_step": tot_ms / (dt * 1e3)}
     if not args.no_cpu:
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
-        log(f"cfg4: cpu baseline ({threads} threads) ...")
-        out["cpu_baseline"] = cfg4_cpu_check(blob, lay, m, tables, ids0, gpu_ids, CFG4_SEQS, 4,
-                                             threads)
+        threads = args.cpu_threads or host_cores()[0]
+        log(f"cfg4: cpu check ({threads} threads) ...")
+        out["cpu_check"] = cfg4_cpu_check(blob, lay, m, tables, ids0, gpu_ids, CFG4_SEQS, 4,
+                                          threads)
     m.close()
     return out
 
@@ -386,7 +486,19 @@ def load_pmc_traffic() -> dict:
         return {}
 
 
-def cpu_baseline(threads: int) -> dict:
+def host_cores() -> tuple[int, int]:
+    """(threads used, nproc): nproc is the CPUs this process may run on; a
+    GPU box shares its host, and one GPU's share is 16 CPUs, so at most 16
+    OpenMP threads are used there whatever nproc reports."""
+    nproc = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    return min(16, nproc), nproc
+
+
+def cpu_baseline(threads: int, nproc: int, runs: int = 5) -> dict:
+    """The CPU oracle (oracle/, the C port of tools/ref_qwen3.py) on the same
+    workload: the median of `runs` timed generations on `threads` OpenMP
+    threads, and a 1-thread line on a bounded sample (32-token prefill + 4
+    greedy steps, median of 3), both after one untimed warm run."""
     import numpy as np
     import oracle
     from q3ops.layout import CONFIGS, Layout, init_random_blob
@@ -394,17 +506,35 @@ def cpu_baseline(threads: int) -> dict:
     shape, init = CONFIGS["cfg3_perf"]
     lay = Layout(shape)
     blob = init_random_blob(lay, init)
-    oracle.set_threads(threads)
     om = oracle.OracleModel(blob, lay.offsets, dict(shape.__dict__))
     ids = lay.global_views(blob)["ids"]
-    t0 = time.perf_counter()
-    _, gen, _, _ = om.generate(ids, N_PROMPT, N_GEN, record=False)
-    dt = time.perf_counter() - t0
-    return {"value": (N_PROMPT + N_GEN) / dt, "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": (f"the full workload once: oracle/ C port of tools/ref_qwen3.py, "
-                       f"512-token prefill + 64 greedy decode steps, {dt:.1f} s, "
-                       f"{threads} OpenMP threads"),
-            "generated_head": [int(v) for v in np.asarray(gen)[:8]]}
+
+    def timed(n_prompt, n_gen, reps):
+        out, ts = None, []
+        for _ in range(reps + 1):  # the first run warms caches and pages
+            om.reset_cache()
+            t0 = time.perf_counter()
+            _, gen, _, _ = om.generate(ids, n_prompt, n_gen, record=False)
+            ts.append(time.perf_counter() - t0)
+            out = gen
+        return sorted(ts[1:])[len(ts[1:]) // 2], ts[1:], out
+
+    oracle.set_threads(threads)
+    med, ts, gen = timed(N_PROMPT, N_GEN, runs)
+    oracle.set_threads(1)
+    med1, ts1, _ = timed(32, 4, 3)
+    oracle.set_threads(threads)
+    return {"value": (N_PROMPT + N_GEN) / med, "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": (f"the full workload (512-token prefill + 64 greedy decode steps), median of "
+                       f"{runs} runs ({med:.2f} s) after a warm run: oracle/ C port of "
+                       f"tools/ref_qwen3.py on {threads} OpenMP threads (nproc {nproc}; one GPU's "
+                       f"share of the box is 16 CPUs)"),
+            "nproc": nproc, "runs_s": [round(t, 3) for t in ts],
+            "one_thread": {"value": 36 / med1, "unit": "tok/s", "cores": 1,
+                           "sample": (f"32-token prefill + 4 greedy steps of the same model and "
+                                      f"prompt, median of 3 runs ({med1:.2f} s), 1 thread"),
+                           "runs_s": [round(t, 3) for t in ts1]},
+            "generated": [int(v) for v in np.asarray(gen)]}
 
 
 ENGINE_REQS, ENGINE_PROMPT, ENGINE_GEN = 32, 256, 64
@@ -473,6 +603,39 @@ def run_engine(args) -> dict:
     }
 
 
+def run_prefill(args) -> dict:
+    """Config 3's prefill alone: the 512-token chunk through
+    q3_forward_chunk with the fused lm_head+argmax of its last row, as
+    q3_generate runs it; `steps` chunks timed with HIP events on the model's
+    stream (the workload profiled for the prefill kernels' counters)."""
+    import torch
+    from q3ops import LM_ARGMAX
+    from q3ops.layout import CONFIGS, Layout, init_random_blob
+    from q3ops.model import Model
+
+    shape, init = CONFIGS["cfg3_perf"]
+    lay = Layout(shape)
+    blob = init_random_blob(lay, init)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        m = Model(lay, blob, stream=stream)
+    for _ in range(args.warmup):
+        m.forward_chunk(0, N_PROMPT, LM_ARGMAX, True)
+    torch.cuda.synchronize()
+    ms = time_events(lambda: m.forward_chunk(0, N_PROMPT, LM_ARGMAX, True), args.steps, stream)
+    best, idx = m.argmax()
+    m.close()
+    pr = path_roofline(ms, 1.0)["prefill"]
+    return {"metric": "tok/s prefill (one 512-token chunk), Qwen3-0.6B W8A8, 1 MI355X",
+            "value": N_PROMPT / (ms / 1e3), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "int8",
+            "data": "synthetic (random-init weights N(0,0.02) int8 per-row, uniform prompt ids)",
+            "config": {"workload": "cfg3 prefill: 28-layer Qwen3-0.6B shape, one 512-token chunk "
+                                   "with the fused lm_head+argmax of the last row"},
+            "path_roofline": pr, "argmax": [float(best), idx]}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -480,23 +643,29 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-roofline", action="store_true")
+    ap.add_argument("--no-cfg1", action="store_true", help="skip the config 1 GEMM sweep leg")
+    ap.add_argument("--no-cfg4", action="store_true", help="skip the config 4 batched-decode leg")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="finish with 3 device-to-device copies of MIB MiB (PMC calibration)")
-    ap.add_argument("--workload", choices=("cfg3", "cfg4", "engine"), default="cfg3",
+    ap.add_argument("--workload", choices=("cfg3", "cfg4", "engine", "prefill"), default="cfg3",
                     help="cfg3: 512-token prefill + 64 b=1 decode steps (the headline line); "
-                         "cfg4: 64-sequence batched paged decode; engine: continuous batching")
+                         "cfg4: 64-sequence batched paged decode; engine: continuous batching; "
+                         "prefill: the 512-token chunk alone")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (this build has no multi-GPU path); "
               f"got --gpus {args.gpus}", file=sys.stderr)
         return 2
-    if args.workload in ("cfg4", "engine"):
+    if args.workload in ("cfg4", "engine", "prefill"):
         import torch
         assert torch.cuda.is_available(), "bench.py needs a ROCm device"
         torch.cuda.set_device(0)
-        run = run_cfg4 if args.workload == "cfg4" else run_engine
-        print(json.dumps(run(args)), flush=True)
+        run = {"cfg4": run_cfg4, "engine": run_engine, "prefill": run_prefill}[args.workload]
+        res = run(args)
+        if "cpu_check" in res:  # the standalone cfg4 line reports it as its CPU baseline
+            res["cpu_baseline"] = res.pop("cpu_check")
+        print(json.dumps(res), flush=True)
         return 0
 
     import numpy as np
@@ -556,7 +725,7 @@ def main() -> int:
         "decode_ms_per_token": decode_ms,
         "decode_tok_s": 1e3 / decode_ms,
         "path_roofline": path_roofline(prefill_ms, decode_ms),
-        "generated_head": [int(v) for v in gen_ids[:8]],
+        "generated": [int(v) for v in gen_ids],
     }
     # in-situ kernel timing: one more (untimed) generation with every decode
     # launch bracketed by HIP events on the model's stream
@@ -608,12 +777,26 @@ def main() -> int:
     if not args.no_roofline:
         log("kernel rooflines ...")
         out["kernels"] = kernel_rooflines(stream)
+    if not args.no_cfg1:
+        log("config 1 GEMM sweep ...")
+        out["cfg1"] = run_cfg1(stream)
+    if not args.no_cfg4:
+        log("config 4 batched decode ...")
+        c4 = run_cfg4(args)
+        out["cfg4"] = {k: c4[k] for k in ("value", "unit", "ms_per_step", "ms_per_decode_step",
+                                          "hbm_bound_ms_per_decode_step", "step_frac_of_hbm_bound",
+                                          "config", "first_ids") if k in c4}
+        for k in ("roofline", "cpu_check"):
+            if k in c4:
+                out["cfg4"][k] = c4[k]
     if not args.no_cpu:
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        threads, nproc = host_cores()
+        threads = args.cpu_threads or threads
         log(f"cpu baseline ({threads} threads) ...")
-        cb = cpu_baseline(threads)
-        cb_ok = cb.pop("generated_head") == out["generated_head"]
-        cb["matches_gpu_ids"] = bool(cb_ok)
+        cb = cpu_baseline(threads, nproc)
+        cb_gen = cb.pop("generated")
+        cb["matches_gpu_ids"] = cb_gen == [int(v) for v in gen_ids]
+        cb["ids_compared"] = len(cb_gen)
         out["cpu_baseline"] = cb
     if args.calib_copy > 0:
         n = args.calib_copy << 20

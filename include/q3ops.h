@@ -122,7 +122,12 @@ int q3_quant_rows_heads(const q3_view *x, const q3_view *qi8,
  *   D[m,n] = sum_g RN(RN(f32(I32_g[m,n]) * b_scale[n]) * a_scale[m,g]),
  *   summed in group order from +0.0f, where I32_g is the exact int32 dot
  *   product over K-group g.  a i8 [M][K], a_scale f32 [M][K/group_k],
- *   b i8 [N][K], b_scale f32 [N][1].  Epilogue (same precedence as the
+ *   b i8 [N][K], b_scale f32 [N][1].  b_scale may instead be [N][K/group_k]
+ *   (K/group_k > 1), one scale per weight row and K-group (BASELINE config 1's
+ *   form; not in the reference): the term is then
+ *   RN(RN(f32(I32_g[m,n]) * b_scale[n,g]) * a_scale[m,g]), and only the
+ *   plain and residual stores accept it (other epilogues and the other GEMM
+ *   ops return Q3_ERR_UNSUPPORTED).  Epilogue (same precedence as the
  *   reference): nw != NULL -> per-128-column head RMSNorm (gain nw, factor
  *   inv_hd), rotate-half RoPE with cos/sin rows [M][64], per-head int8 quant
  *   into q8 [M][N] / qs [M][N/128]; else q8 != NULL -> per-head int8 quant;

@@ -145,6 +145,22 @@ def gemm_nt_group(a8, a_scale, w8, w_scale, group: int) -> np.ndarray:
     return out
 
 
+def gemm_nt_group_bg(a8, a_scale, w8, w_scale, group: int) -> np.ndarray:
+    """ref_qwen3.py:145-158 with per-(row, group) weight scales
+    w_scale [n][k // group] (BASELINE config 1; not a reference function)."""
+    a8 = np.ascontiguousarray(a8, np.int8)
+    w8 = np.ascontiguousarray(w8, np.int8)
+    a_scale = np.ascontiguousarray(a_scale, np.float32)
+    w_scale = np.ascontiguousarray(w_scale, np.float32)
+    rows, k = a8.shape
+    n = w8.shape[0]
+    assert w_scale.shape == (n, k // group), w_scale.shape
+    out = np.empty((rows, n), np.float32)
+    lib().orc_gemm_nt_group_bg(_p(a8), _p(a_scale), rows, k, _p(w8), _p(w_scale), n, group,
+                               _p(out))
+    return out
+
+
 def gemm_nt_group_i32(a8, w8, group: int) -> np.ndarray:
     """Per-group exact int32 partials, [rows][groups][n]."""
     a8 = np.ascontiguousarray(a8, np.int8)

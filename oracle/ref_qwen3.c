@@ -244,6 +244,36 @@ void orc_gemm_nt_group(const int8_t *a8, const float *a_scale, int rows, int k,
   }
 }
 
+/* BASELINE config 1's per-(row, group) B scales: ref_qwen3.py:145-158 with
+ * w_scale[n] replaced by w_scale[n][g] (row stride `groups`), i.e.
+ *   part = RN(RN(f32(i32) * w_scale[n, g]) * a_scale[m, g]); out = RN(out + part)
+ * in group order from +0.0f.  Not a reference function (the reference scales
+ * weights per row only, group_gemm.h:98-101); pinned by what the arithmetic
+ * fixes: equal group scales reduce it to orc_gemm_nt_group bit for bit, unit
+ * scales to the integer sum, and tiny shapes to the f64 sum within rounding. */
+void orc_gemm_nt_group_bg(const int8_t *a8, const float *a_scale, int rows, int k,
+                          const int8_t *w8, const float *w_scale, int n,
+                          int group, float *out) {
+  const int groups = k / group;
+#pragma omp parallel for schedule(static)
+  for (int j = 0; j < n; ++j) {
+    const int8_t *wj = w8 + (size_t)j * k;
+    const float *wsj = w_scale + (size_t)j * groups;
+    for (int r = 0; r < rows; ++r) {
+      const int8_t *ar = a8 + (size_t)r * k;
+      float acc = 0.0f;
+      for (int g = 0; g < groups; ++g) {
+        const int32_t p = idot(ar + (size_t)g * group, wj + (size_t)g * group, group);
+        float part = (float)p;
+        part = part * wsj[g];
+        part = part * a_scale[(size_t)r * groups + g];
+        acc = acc + part;
+      }
+      out[(size_t)r * n + j] = acc;
+    }
+  }
+}
+
 /* ref_qwen3.py:161-173 rmsnorm_from_values. */
 void orc_rmsnorm_rows(const float *x, int rows, int cols, int x_stride,
                       const float *w, float inv, float *out, int out_stride) {

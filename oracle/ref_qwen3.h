@@ -36,6 +36,10 @@ void orc_quant_rows_heads(const float *x, int rows, int cols, int group,
 void orc_gemm_nt_group(const int8_t *a8, const float *a_scale, int rows, int k,
                        const int8_t *w8, const float *w_scale, int n,
                        int group, float *out);
+/* Per-(row, group) weight scales w_scale[n][k / group]. */
+void orc_gemm_nt_group_bg(const int8_t *a8, const float *a_scale, int rows, int k,
+                          const int8_t *w8, const float *w_scale, int n,
+                          int group, float *out);
 void orc_gemm_nt_group_i32(const int8_t *a8, int rows, int k,
                            const int8_t *w8, int n, int group, int32_t *out);
 void orc_rmsnorm_rows(const float *x, int rows, int cols, int x_stride,

@@ -96,7 +96,7 @@ __global__ void __launch_bounds__(256) gemm_group_kernel(GemmArgs a) {
   for (int nt = 0; nt < 2; ++nt) {
     const int n = nw0 + nt * 16 + lr;
     brow[nt] = a.b + static_cast<int64_t>(n) * a.ldb + lg * 16;
-    bscale[nt] = a.bs[static_cast<int64_t>(n) * a.bs_stride];
+    bscale[nt] = a.bs_ld ? 0.0f : a.bs[static_cast<int64_t>(n) * a.bs_stride];
   }
 
   const int G = a.group;
@@ -122,6 +122,10 @@ __global__ void __launch_bounds__(256) gemm_group_kernel(GemmArgs a) {
           c[mt][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[mt], bv[nt], c[mt][nt], 0, 0, 0);
     }
     // per-group dequant and ordered f32 accumulation
+    float bsg[2];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+      bsg[nt] = a.bs_ld ? a.bs[static_cast<int64_t>(nw0 + nt * 16 + lr) * a.bs_ld + g] : bscale[nt];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -130,7 +134,7 @@ __global__ void __launch_bounds__(256) gemm_group_kernel(GemmArgs a) {
         const float asv = (r < M) ? a.as[static_cast<int64_t>(r) * a.ldas + g] : 0.0f;
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
-          float p = __fmul_rn(static_cast<float>(c[mt][nt][i]), bscale[nt]);
+          float p = __fmul_rn(static_cast<float>(c[mt][nt][i]), bsg[nt]);
           p = __fmul_rn(p, asv);
           acc[mt][nt][i] = __fadd_rn(acc[mt][nt][i], p);
         }
@@ -318,6 +322,7 @@ __global__ void __launch_bounds__(64) argmax_logits_kernel(const float *logits, 
 
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t s) {
   if (a.M <= 0) return hipSuccess;
+  if (a.bs_ld && a.epi != EPI_STORE && a.epi != EPI_ADD) return hipErrorInvalidValue;
   // prefill shapes and batches of sequences: the LDS-staged tile kernel
   // (ARGMAX over at most 64 rows, so that one row tile reads the weights once)
   if (a.M > 16 && (a.epi != EPI_ARGMAX || a.M <= 64)) {
@@ -334,6 +339,7 @@ hipError_t launch_gemm(const GemmArgs &a, hipStream_t s) {
     t.ldb = a.ldb;
     t.bs0 = a.bs;
     t.bs_stride = a.bs_stride;
+    t.bs_ld = a.bs_ld;
     t.out = a.out;
     t.ldo = a.ldo;
     t.qd = a.qd;

@@ -115,7 +115,9 @@ struct TileShape {
   __device__ static int swz(int r, int c) { return c ^ ((r / RPC) & (CH - 1)); }
 };
 
-template <int BM, int BN, int WGM, int NMAT, int STAGES, int KS, int EPI, int GROUP>
+// BSG: per-(row, K-group) B scales bs0[n * bs_ld + g] (staged in LDS with
+// the A scales) instead of one scale per weight row.
+template <int BM, int BN, int WGM, int NMAT, int STAGES, int KS, int EPI, int GROUP, bool BSG>
 __global__ void __launch_bounds__(512) gemm_tile_kernel(TileArgs a) {
   using S = TileShape<BM, BN, WGM, NMAT, STAGES, KS>;
   constexpr int MT = S::MT, NT = S::NT;
@@ -151,7 +153,8 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(TileArgs a) {
   const int T = a.K / KS;            // k-steps
   const int ngroups = a.K / a.group;
   float *as_lds = reinterpret_cast<float *>(smem + STAGES * S::STAGE);  // [BM][ngroups]
-  uint64_t *tab = reinterpret_cast<uint64_t *>(as_lds + BM * ngroups);  // exp table (SwiGLU)
+  float *bs_lds = as_lds + BM * ngroups;                                 // BSG: [BN][ngroups]
+  uint64_t *tab = reinterpret_cast<uint64_t *>(bs_lds + (BSG ? BN * ngroups : 0));  // exp table (SwiGLU)
 
   // k-step t -> stage s; instruction j copies LDS rows [RPI j, RPI (j + 1))
   auto issue = [&](int t, int s) {
@@ -182,13 +185,19 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(TileArgs a) {
   }
   if (EPI == EPI_SWIGLUQ && threadIdx.x == 0) stage_exp2_table(tab);
   float bsv[NMAT][NT];
+  if constexpr (BSG) {
+    static_assert(!BSG || NMAT == 1, "per-group B scales: one weight matrix");
+    for (int i = threadIdx.x; i < BN * ngroups; i += S::NTHR)
+      bs_lds[i] = BS0[static_cast<int64_t>(nb + i / ngroups) * a.bs_ld + i % ngroups];
+  } else {
 #pragma unroll
-  for (int mi = 0; mi < NMAT; ++mi)
+    for (int mi = 0; mi < NMAT; ++mi)
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      const float *bs = mi == 0 ? BS0 : a.bs1;
-      bsv[mi][nt] = bs[static_cast<int64_t>(nb + wn * S::WN + nt * 16 + lr) * a.bs_stride];
-    }
+      for (int nt = 0; nt < NT; ++nt) {
+        const float *bs = mi == 0 ? BS0 : a.bs1;
+        bsv[mi][nt] = bs[static_cast<int64_t>(nb + wn * S::WN + nt * 16 + lr) * a.bs_stride];
+      }
+  }
 
   // scales first, then the first STAGES-1 copies: vector loads complete in
   // order, so waiting for the scales does not wait for the copies
@@ -224,6 +233,10 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(TileArgs a) {
   // then c = 0 for the buffer's next group
   auto dequant = [&](auto PAR, int g) {
     constexpr int b = decltype(PAR)::value;
+    if constexpr (BSG) {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) bsv[0][nt] = bs_lds[(wn * S::WN + nt * 16 + lr) * ngroups + g];
+    }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -461,36 +474,37 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(TileArgs a) {
   }
 }
 
-template <int BM, int BN, int WGM, int NMAT, int STAGES, int KS, int EPI, int GROUP>
+template <int BM, int BN, int WGM, int NMAT, int STAGES, int KS, int EPI, int GROUP, bool BSG>
 hipError_t launch_shape(const TileArgs &a, hipStream_t s) {
   using S = TileShape<BM, BN, WGM, NMAT, STAGES, KS>;
   if (a.K % KS) return hipErrorInvalidValue;
   const int ngroups = a.K / a.group;
-  size_t lds = static_cast<size_t>(STAGES) * S::STAGE + sizeof(float) * BM * ngroups + 32 * sizeof(uint64_t);
+  size_t lds = static_cast<size_t>(STAGES) * S::STAGE + sizeof(float) * (BM + (BSG ? BN : 0)) * ngroups +
+               32 * sizeof(uint64_t);
   if (EPI != EPI_STORE && EPI != EPI_ADD)
     lds = std::max(lds, sizeof(float) * BM * S::LDT);
   if (lds > 160 * 1024) return hipErrorInvalidValue;
   static bool attr_set = false;  // more than 64 KiB of dynamic LDS must be allowed once
   if (!attr_set) {
     const hipError_t e =
-        hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_tile_kernel<BM, BN, WGM, NMAT, STAGES, KS, EPI, GROUP>),
+        hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_tile_kernel<BM, BN, WGM, NMAT, STAGES, KS, EPI, GROUP, BSG>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
   const dim3 grid(a.N / BN, (a.M + BM - 1) / BM);
-  Q3_LAUNCH((gemm_tile_kernel<BM, BN, WGM, NMAT, STAGES, KS, EPI, GROUP>), grid, dim3(S::NTHR), lds, s, a);
+  Q3_LAUNCH((gemm_tile_kernel<BM, BN, WGM, NMAT, STAGES, KS, EPI, GROUP, BSG>), grid, dim3(S::NTHR), lds, s, a);
   return hipGetLastError();
 }
 
 // The group size as a template argument where the model uses it (256, and
 // 128 for the O projection), so that the group-sum buffers alternate at
 // compile time; any other group size takes the run-time path.
-template <int BM, int BN, int WGM, int NMAT, int STAGES, int KS, int EPI>
+template <int BM, int BN, int WGM, int NMAT, int STAGES, int KS, int EPI, bool BSG = false>
 hipError_t launch_tile(const TileArgs &a, hipStream_t s) {
-  if (a.group == 256) return launch_shape<BM, BN, WGM, NMAT, STAGES, KS, EPI, 256>(a, s);
-  if (a.group == 128) return launch_shape<BM, BN, WGM, NMAT, STAGES, KS, EPI, 128>(a, s);
-  return launch_shape<BM, BN, WGM, NMAT, STAGES, KS, EPI, 0>(a, s);
+  if (a.group == 256) return launch_shape<BM, BN, WGM, NMAT, STAGES, KS, EPI, 256, BSG>(a, s);
+  if (a.group == 128) return launch_shape<BM, BN, WGM, NMAT, STAGES, KS, EPI, 128, BSG>(a, s);
+  return launch_shape<BM, BN, WGM, NMAT, STAGES, KS, EPI, 0, BSG>(a, s);
 }
 
 }  // namespace
@@ -507,6 +521,14 @@ bool gemm_tile_supported(const TileArgs &a, int epi) {
 hipError_t launch_gemm_tile(const TileArgs &a, int epi, hipStream_t s) {
   if (a.M <= 0) return hipSuccess;
   if (!gemm_tile_supported(a, epi)) return hipErrorInvalidValue;
+  if (a.bs_ld) {  // per-(row, K-group) B scales: plain and residual stores only
+    if (epi != EPI_STORE && epi != EPI_ADD) return hipErrorInvalidValue;
+    if (a.M <= 64)
+      return epi == EPI_STORE ? launch_tile<64, 32, 4, 1, 3, 256, EPI_STORE, true>(a, s)
+                              : launch_tile<64, 32, 4, 1, 3, 256, EPI_ADD, true>(a, s);
+    return epi == EPI_STORE ? launch_tile<64, 128, 2, 1, 3, 128, EPI_STORE, true>(a, s)
+                            : launch_tile<32, 64, 2, 1, 6, 256, EPI_ADD, true>(a, s);
+  }
   // a batch of sequences (M <= 64): 32-column tiles, for 4x the workgroups
   if (a.M <= 64 && (epi == EPI_STORE || epi == EPI_ADD)) {
     if (epi == EPI_STORE) return launch_tile<64, 32, 4, 1, 3, 256, EPI_STORE>(a, s);

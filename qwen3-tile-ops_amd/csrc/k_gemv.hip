@@ -276,9 +276,12 @@ __device__ void pro_compute_row(const GemvArgs &a, int m, const ProRow<QW, NP> &
 // them in the PRO_NORM prologue, PART = kPartEpi in the EPI_ADD epilogue.
 constexpr int kMaxPart = 16;
 constexpr int kPartPro = 1, kPartEpi = 2;
-template <int GPW, int KSTEPS, int NT, int NMAT, int PRO, int PART>
+// BSG: per-(row, K-group) B scales seg[0].bs[n * bs_ld + g], loaded with
+// the other scales before the weight stream (PRO_NONE, one matrix).
+template <int GPW, int KSTEPS, int NT, int NMAT, int PRO, int PART, bool BSG = false>
 __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
   static_assert(PART == 0 || NT == 1, "partials: one item column per thread");
+  static_assert(!BSG || (NMAT == 1 && PRO == PRO_NONE && PART == 0), "per-group B scales: plain GEMV");
   constexpr int NPRO = PART == kPartPro ? kMaxPart : 0;
   constexpr int NEPI = PART == kPartEpi ? kMaxPart : 0;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -387,10 +390,22 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
   }
   // the weight rows' scales, then the weights
   float bsv[NMAT][NT];
+  float bsg[BSG ? GPW : 1][NT];
+  if constexpr (BSG) {
+    const int64_t bs_ld = a.bs_ld;
 #pragma unroll
-  for (int mi = 0; mi < NMAT; ++mi)
+    for (int gi = 0; gi < GPW; ++gi) {
+      const int g = min(wave + 4 * gi, ngroups - 1);
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) bsv[mi][nt] = (mi == 0 ? sg_bs : sg_bs2)[n_blk - sg_n0 + nt * 16 + lr];
+      for (int nt = 0; nt < NT; ++nt)
+        bsg[gi][nt] = sg_bs[static_cast<int64_t>(n_blk - sg_n0 + nt * 16 + lr) * bs_ld + g];
+    }
+  } else {
+#pragma unroll
+    for (int mi = 0; mi < NMAT; ++mi)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) bsv[mi][nt] = (mi == 0 ? sg_bs : sg_bs2)[n_blk - sg_n0 + nt * 16 + lr];
+  }
   v4i bv[NMAT][NT][GPW][KSTEPS];
 #pragma unroll
   for (int gi = 0; gi < GPW; ++gi) {
@@ -450,9 +465,10 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
         for (int ks = 0; ks < KSTEPS; ++ks)
           acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[gi][ks], bv[mi][nt][gi][ks], acc, 0, 0, 0);
         float *pt = part + ((mi * ngroups + g) * 16) * PP + nt * 16 + lr;
+        const float bsc = BSG ? bsg[BSG ? gi : 0][nt] : bsv[mi][nt];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          pt[(lg * 4 + i) * PP] = __fmul_rn(__fmul_rn(static_cast<float>(acc[i]), bsv[mi][nt]), asv_[i]);
+          pt[(lg * 4 + i) * PP] = __fmul_rn(__fmul_rn(static_cast<float>(acc[i]), bsc), asv_[i]);
       }
   }
   __syncthreads();
@@ -843,7 +859,7 @@ __global__ void __launch_bounds__(256) qkv_heads_kernel(QkvHeadArgs a) {
   if (lane == 0) *sp = scale;
 }
 
-template <int GPW, int KSTEPS, int NT, int NMAT, int PRO, int PART>
+template <int GPW, int KSTEPS, int NT, int NMAT, int PRO, int PART, bool BSG = false>
 hipError_t launch_t(const GemvArgs &a, int ncols, hipStream_t s) {
   constexpr int NB = 16 * NT;
   // the prologue gives each wave GPW * KSTEPS / 4 groups of 256 columns
@@ -853,7 +869,7 @@ hipError_t launch_t(const GemvArgs &a, int ncols, hipStream_t s) {
   if (PRO != PRO_NONE)
     lds += ((a.M * a.K + 15) & ~15) + sizeof(float) * (a.M * (a.K / 256) + a.K / 32);
   if (lds > 65536) return hipErrorInvalidValue;
-  Q3_LAUNCH((gemv_kernel<GPW, KSTEPS, NT, NMAT, PRO, PART>), dim3(ncols / NB), dim3(256), lds, s, a);
+  Q3_LAUNCH((gemv_kernel<GPW, KSTEPS, NT, NMAT, PRO, PART, BSG>), dim3(ncols / NB), dim3(256), lds, s, a);
   return hipGetLastError();
 }
 
@@ -871,6 +887,16 @@ hipError_t dispatch_pro(const GemvArgs &a, int ncols, hipStream_t s) {
 
 template <int NT, int NMAT>
 hipError_t dispatch_k(const GemvArgs &a, int ncols, hipStream_t s) {
+  if constexpr (NMAT == 1) {
+    if (a.bs_ld) {  // per-(row, K-group) B scales
+      if (a.K == 1024 && a.group == 256) return launch_t<1, 4, NT, 1, PRO_NONE, 0, true>(a, ncols, s);
+      if (a.K == 1024 && a.group == 128) return launch_t<2, 2, NT, 1, PRO_NONE, 0, true>(a, ncols, s);
+      if (a.K == 2048 && a.group == 128) return launch_t<4, 2, NT, 1, PRO_NONE, 0, true>(a, ncols, s);
+      if (a.K == 2048 && a.group == 256) return launch_t<2, 4, NT, 1, PRO_NONE, 0, true>(a, ncols, s);
+      if (a.K == 3072 && a.group == 256) return launch_t<3, 4, NT, 1, PRO_NONE, 0, true>(a, ncols, s);
+      return hipErrorInvalidValue;
+    }
+  }
   if (a.pro == PRO_NONE) {
     if (a.K == 1024 && a.group == 256) return launch_t<1, 4, NT, NMAT, PRO_NONE, 0>(a, ncols, s);
     if (a.K == 1024 && a.group == 128) return launch_t<2, 2, NT, NMAT, PRO_NONE, 0>(a, ncols, s);
@@ -944,6 +970,12 @@ int stream_grid(int ntiles) {
 
 }  // namespace
 
+bool gemv_group_bscale_supported(const GemvArgs &a) {
+  const int epi = a.seg[0].epi;
+  return a.pro == PRO_NONE && a.nseg == 1 && !a.part && (epi == EPI_STORE || epi == EPI_ADD) &&
+         !use_stream(a) && gemv_supported(a.M, a.K, a.group);
+}
+
 int gemv_argmax_slots(const GemvArgs &a) {
   const int ncols = ncols_of(a);
   if (use_stream(a)) return stream_grid(ncols / 64);
@@ -952,6 +984,7 @@ int gemv_argmax_slots(const GemvArgs &a) {
 
 hipError_t launch_gemv(const GemvArgs &a, hipStream_t s) {
   if (a.M <= 0) return hipSuccess;
+  if (a.bs_ld && !gemv_group_bscale_supported(a)) return hipErrorInvalidValue;
   if (a.pro != PRO_NONE && (a.K % 1024 != 0 || a.M > 16)) return hipErrorInvalidValue;
   const int ncols = ncols_of(a);
   if (use_stream(a) && a.M == 1) {  // one row: whole-row v_dot4 streaming

@@ -103,6 +103,9 @@ struct GemmArgs {
   int64_t ldb;
   const float *bs;
   int64_t bs_stride;  // elements between consecutive b_scale entries
+  // per-(row, K-group) B scales bs[n * bs_ld + g] when bs_ld > 0 (EPI_STORE
+  // and EPI_ADD only); 0: one scale per row, bs[n * bs_stride]
+  int64_t bs_ld;
   int epi;
   float *out;
   int64_t ldo;        // EPI_STORE / EPI_ADD target
@@ -145,6 +148,7 @@ struct TileArgs {
   int64_t ldb;
   const float *bs0, *bs1;
   int64_t bs_stride;
+  int64_t bs_ld;  // GemmArgs::bs_ld (EPI_STORE / EPI_ADD)
   float *out;
   int64_t ldo;
   QDest qd;
@@ -330,8 +334,13 @@ struct GemvArgs {
   const float *part;
   int npart;
   int64_t ld_part;
+  // per-(row, K-group) B scales of segment 0 (PRO_NONE, EPI_STORE / EPI_ADD,
+  // one segment): seg[0].bs[n * bs_ld + g]; 0: per-row scales
+  int64_t bs_ld;
 };
 bool gemv_supported(int M, int K, int group);
+// whether launch_gemv takes per-(row, K-group) B scales for this launch
+bool gemv_group_bscale_supported(const GemvArgs &a);
 // key slots per row that an EPI_ARGMAX launch writes (keys_ld must cover it)
 int gemv_argmax_slots(const GemvArgs &a);
 hipError_t launch_gemv(const GemvArgs &a, hipStream_t s);

@@ -89,8 +89,17 @@ int gemm_common(const q3_view *a, const q3_view *a_scale, const q3_view *b,
     return Q3_ERR_VIEW;
   if (a_scale->col_bytes != 4 || a_scale->row_bytes % 4 != 0) return Q3_ERR_VIEW;
   if (a_scale->rows < M || a_scale->cols < K / group_k) return Q3_ERR_VIEW;
-  int64_t bss = 1;
-  Q3_TRY(check_vec(b_scale, N, &bss));
+  // b_scale [N][1] (one scale per weight row, the reference) or
+  // [N][K / group_k] (one per weight row and K-group)
+  int64_t bss = 1, bs_ld = 0;
+  const uint32_t ng = K / group_k;
+  if (ng > 1 && b_scale->cols == ng && b_scale->rows >= N) {
+    Q3_TRY(check_scales(b_scale, N, ng));
+    if (b_scale->col_bytes != 4) return Q3_ERR_VIEW;
+    bs_ld = b_scale->row_bytes / 4;
+  } else {
+    Q3_TRY(check_vec(b_scale, N, &bss));
+  }
   std::memset(&g, 0, sizeof(g));
   g.M = static_cast<int>(M);
   g.N = static_cast<int>(N);
@@ -104,13 +113,17 @@ int gemm_common(const q3_view *a, const q3_view *a_scale, const q3_view *b,
   g.ldb = b->row_bytes;
   g.bs = static_cast<const float *>(b_scale->data);
   g.bs_stride = bss;
+  g.bs_ld = bs_ld;
   return Q3_OK;
 }
 
 // Decode-shaped STORE/ADD/ARGMAX GEMMs go to the whole-chip GEMV kernel.
+q3::GemvArgs to_gemv(const q3::GemmArgs &g);
+
 bool use_gemv(const q3::GemmArgs &g) {
   return q3::gemv_supported(g.M, g.K, g.group) && g.ldb == g.K && g.bs_stride == 1 &&
-         (g.epi == q3::EPI_STORE || g.epi == q3::EPI_ADD || g.epi == q3::EPI_ARGMAX);
+         (g.epi == q3::EPI_STORE || g.epi == q3::EPI_ADD || g.epi == q3::EPI_ARGMAX) &&
+         (!g.bs_ld || q3::gemv_group_bscale_supported(to_gemv(g)));
 }
 
 q3::GemvArgs to_gemv(const q3::GemmArgs &g) {
@@ -134,6 +147,7 @@ q3::GemvArgs to_gemv(const q3::GemmArgs &g) {
   v.seg[0].ldo = g.ldo;
   v.keys = g.keys;
   v.keys_ld = g.keys_ld;
+  v.bs_ld = g.bs_ld;
   return v;
 }
 
@@ -286,6 +300,8 @@ int q3_gemm_nt_group_store(const q3_view *a, const q3_view *a_scale,
   bool skip = false;
   Q3_TRY(gemm_common(a, a_scale, b, b_scale, group_k, g, &skip));
   if (skip) return Q3_OK;
+  // per-group B scales: the plain and residual stores
+  if (g.bs_ld && (q8 || nw)) return unsupported();
   if (q8) {  // group_gemm.h:168-193 (nw selects norm+RoPE)
     Q3_TRY(check_view(q8, Q3_DT_I8));
     if (q8->rows < a->rows || q8->cols < b->rows) return Q3_ERR_VIEW;
@@ -329,6 +345,7 @@ int q3_gemm_nt_group_kv_paged(const q3_view *a, const q3_view *a_scale,
   bool skip = false;
   Q3_TRY(gemm_common(a, a_scale, b, b_scale, group_k, g, &skip));
   if (skip) return Q3_OK;
+  if (g.bs_ld) return unsupported();
   Q3_TRY(check_paged(kv));
   if (kv->row_bytes < b->rows || kv->scale_row_bytes < b->rows / 128 * 4) return Q3_ERR_VIEW;
   g.qd.q8 = static_cast<int8_t *>(is_v ? kv->v : kv->k);
@@ -458,6 +475,7 @@ int q3_gemm_gate_up_swiglu_quant(const q3_view *a, const q3_view *a_scale,
   bool skip = false;
   Q3_TRY(gemm_common(a, a_scale, wg, wgs, group_k, g, &skip));
   if (skip) return Q3_OK;
+  if (g.bs_ld) return unsupported();
   Q3_TRY(check_view(wu, Q3_DT_I8));
   if (wu->rows != wg->rows || wu->cols != wg->cols || wu->row_bytes != wg->row_bytes) return Q3_ERR_VIEW;
   if (reinterpret_cast<uintptr_t>(wu->data) % 16) return Q3_ERR_VIEW;
@@ -571,6 +589,10 @@ int argmax_common(const q3_view *a, const q3_view *a_scale, const q3_view *b,
                   uint32_t group_k, q3::GemmArgs &g, int64_t *bst, int64_t *ist, bool *skip) {
   Q3_TRY(gemm_common(a, a_scale, b, b_scale, group_k, g, skip));
   if (*skip) return Q3_OK;
+  if (g.bs_ld) {
+    *skip = true;
+    return unsupported();
+  }
   if (!best || !best->data || !bidx || !bidx->data) return Q3_ERR_ARG;
   if (best->dtype != Q3_DT_F32) return Q3_ERR_DTYPE;
   if (bidx->dtype != Q3_DT_I32 && bidx->dtype != Q3_DT_U32) return Q3_ERR_DTYPE;

@@ -1,12 +1,19 @@
-"""Summaries of rocprofv3 CSV output for the measurement record.
+"""Summaries of rocprofv3 CSV output for the measurement record
+(profiles/).  Every summary there is produced by this module from the CSV
+files of one of the rocprofv3 commands named in the summary.
 
     python -m q3ops.profiling stats <kernel_stats.csv> --cmd "<command>" [--top N]
         -> markdown table of the per-kernel statistics (stdout)
 
     python -m q3ops.profiling pmc --fetch <counter_collection.csv>
         --write <counter_collection.csv> --calib-bytes N --cmd "<command>"
-        -> JSON: per decode kernel class, FETCH_SIZE / WRITE_SIZE per dispatch
+        -> JSON: per kernel class, FETCH_SIZE / WRITE_SIZE per dispatch
            (KiB, as read) and HBM-side bytes per dispatch after calibration
+
+    python -m q3ops.profiling counters <counter_collection.csv> [...]
+        --cmd "<command>" [--cus 256]
+        -> JSON: per kernel class, the mean of every collected counter per
+           dispatch, plus the derived MFMA and VALU figures (below)
 
 Calibration: the profiled command ends with device-to-device copies of
 N bytes (bench.py --calib-copy); each reads and writes exactly N bytes, so
@@ -14,6 +21,12 @@ factor = N / (counter KiB * 1024) for the copy dispatches of that size, and
 every kernel's counter is scaled by it.  FETCH_SIZE and WRITE_SIZE count
 L2 <-> fabric traffic, i.e. bytes that left the L2 (last-level-cache hits
 included).
+
+Derived figures (when their counters were collected in the same pass):
+  int8 ops per dispatch = SQ_INSTS_VALU_MFMA_MOPS_I8 * 512
+  MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE * CUs * 4 SIMDs)
+  VALU active = SQ_ACTIVE_INST_VALU / (GRBM_GUI_ACTIVE * CUs * 4 SIMDs)
+  L2 hit rate = TCC_HIT_sum / (TCC_HIT_sum + TCC_MISS_sum)
 """
 from __future__ import annotations
 
@@ -24,16 +37,28 @@ import re
 import statistics
 import sys
 
-# decode kernel symbol -> kernel class of q3_model_set_kernel_timing
-# (gemv_kernel<GPW, KSTEPS, NT, NMAT, prologue, partials>: matched on the
-# shape parameters)
+# kernel symbol -> kernel class.  Decode classes are those of
+# q3_model_set_kernel_timing; gemv_kernel<GPW, KSTEPS, NT, NMAT, prologue,
+# partials, ...> and gemm_tile_kernel<BM, BN, WGM, NMAT, STAGES, KS, epilogue,
+# group, ...> are matched on their template arguments (epilogue numbers:
+# 1 residual add, 2 V head quant, 3 Q/K norm+RoPE+quant, 6 SwiGLU+quant,
+# 7 the three-segment Q|K|V launch).
 CLASS_OF = [
-    (r"attn_decode_kernel<", "attn_decode"),
-    (r"gemv_kernel<1, 4, 1, 1,", "gemv_qkv"),
+    (r"attn_decode_kernel<1, ", "attn_decode"),
+    (r"attn_decode_kernel<2, ", "attn_decode_batch"),
+    (r"gemv_kernel<1, 4, 1, 1, [13], 0", "gemv_qkv"),
     (r"gemv_kernel<4, 2, 1, 1,", "gemv_o"),
-    (r"gemv_kernel<1, 4, 1, 2,", "gemv_gate_up"),
-    (r"gemv_kernel<3, 4, 1, 1,", "gemv_down"),
-    (r"gemv_stream_kernel<", "lm_head"),
+    (r"gemv_kernel<1, 4, 1, 2, 1, 1", "gemv_gate_up"),
+    (r"gemv_kernel<3, 4, 1, 1, 2, 2", "gemv_down"),
+    (r"gemv_row_kernel<1, 4", "lm_head"),
+    (r"gemv_stream_kernel<", "lm_head_rows"),
+    (r"gemm_tile_kernel<\d+, \d+, \d+, 2, \d+, \d+, 6,", "prefill_gate_up"),
+    (r"gemm_tile_kernel<\d+, \d+, \d+, 1, \d+, \d+, 7,", "prefill_qkv"),
+    (r"gemm_tile_kernel<\d+, \d+, \d+, 1, \d+, \d+, 1, 128", "prefill_o"),
+    (r"gemm_tile_kernel<\d+, \d+, \d+, 1, \d+, \d+, 1, 256", "prefill_down"),
+    (r"attention_kernel", "prefill_attention"),
+    (r"rows1024_kernel", "norm_quant_rows"),
+    (r"argmax_finish_kernel", "argmax_finish"),
 ]
 
 
@@ -56,7 +81,7 @@ def short_name(name: str, width: int = 90) -> str:
 
 def class_of(name: str) -> str | None:
     for pat, cls in CLASS_OF:
-        if re.search(re.escape(pat), name):
+        if re.search(pat, name):
             return cls
     return None
 
@@ -117,6 +142,39 @@ def pmc_json(fetch: str, write: str, calib_bytes: int, cmd: str) -> dict:
             "kernels": kernels}
 
 
+def counters_json(paths: list[str], cmd: str, cus: int) -> dict:
+    """Per kernel class (and per kernel symbol within it): the mean of every
+    counter over its dispatches, merged over several PMC passes, and the
+    derived MFMA / VALU / L2 figures of the module docstring."""
+    per: dict[str, dict[str, list[float]]] = {}
+    for path in paths:
+        for r in csv.DictReader(open(path)):
+            name = r["Kernel_Name"]
+            per.setdefault(name, {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    kernels = {}
+    for name, cnt in sorted(per.items()):
+        cls = class_of(name)
+        if cls is None:
+            continue
+        mean = {c: statistics.mean(v) for c, v in cnt.items()}
+        d = {"kernel": short_name(name), "dispatches": max(len(v) for v in cnt.values()),
+             "counters": mean}
+        act = mean.get("GRBM_GUI_ACTIVE")
+        if "SQ_INSTS_VALU_MFMA_MOPS_I8" in mean:
+            d["int8_ops_per_dispatch"] = mean["SQ_INSTS_VALU_MFMA_MOPS_I8"] * 512
+        if act:
+            if "SQ_VALU_MFMA_BUSY_CYCLES" in mean:
+                d["mfma_busy"] = mean["SQ_VALU_MFMA_BUSY_CYCLES"] / (act * cus * 4)
+            if "SQ_ACTIVE_INST_VALU" in mean:
+                d["valu_active"] = mean["SQ_ACTIVE_INST_VALU"] / (act * cus * 4)
+        if "TCC_HIT_sum" in mean and "TCC_MISS_sum" in mean:
+            tot = mean["TCC_HIT_sum"] + mean["TCC_MISS_sum"]
+            d["l2_hit_rate"] = mean["TCC_HIT_sum"] / tot if tot else None
+        key = cls if cls not in kernels else f"{cls}:{short_name(name)}"
+        kernels[key] = d
+    return {"command": cmd, "cus": cus, "kernels": kernels}
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(prog="python -m q3ops.profiling")
     sub = ap.add_subparsers(dest="cmd_name", required=True)
@@ -129,9 +187,16 @@ def main(argv=None) -> int:
     p.add_argument("--write", required=True)
     p.add_argument("--calib-bytes", type=int, required=True)
     p.add_argument("--cmd", required=True)
+    c = sub.add_parser("counters")
+    c.add_argument("csv", nargs="+")
+    c.add_argument("--cmd", required=True)
+    c.add_argument("--cus", type=int, default=256)
     a = ap.parse_args(argv)
     if a.cmd_name == "stats":
         sys.stdout.write(stats_md(a.csv, a.cmd, a.top))
+    elif a.cmd_name == "counters":
+        json.dump(counters_json(a.csv, a.cmd, a.cus), sys.stdout, indent=1)
+        sys.stdout.write("\n")
     else:
         json.dump(pmc_json(a.fetch, a.write, a.calib_bytes, a.cmd), sys.stdout, indent=1)
         sys.stdout.write("\n")

@@ -127,3 +127,27 @@ def test_argmax_noalloc_key_limit(lib):
     best, bidx = V(M, 1, DT_F32), V(M, 1, DT_I32)
     for fn in (lib.q3_gemm_nt_group_argmax_noalloc, lib.q3_gemm_nt_group_argmax):
         assert fn(a, as_, b, bs, best, bidx, 256, None) == ERR_UNSUPPORTED
+
+
+def test_group_bscale_only_for_stores(lib):
+    """b_scale [N][K/g] (per row and K-group) is taken by the plain and
+    residual stores only: the head epilogues, the paged K/V GEMM, gate/up and
+    argmax report Q3_ERR_UNSUPPORTED before anything is launched."""
+    M, K, N = 8, 1024, 1024
+    a, as_, b, _ = gemm_operands(M, K, N)
+    bsg = V(N, K // 256, DT_F32)
+    q8, qs = V(M, N, DT_I8), V(M, N // 128, DT_F32)
+    assert lib.q3_gemm_nt_group_store(a, as_, b, bsg, None, 256, None, q8, qs, None, None, None,
+                                      C.c_float(0), None) == ERR_UNSUPPORTED
+    kv = paged()
+    assert lib.q3_gemm_nt_group_kv_paged(a, as_, b, bsg, 256, C.byref(kv), 0, 1, None, None, None,
+                                         C.c_float(0), None) == ERR_UNSUPPORTED
+    s8, ss = V(M, N, DT_I8), V(M, N // 256, DT_F32)
+    assert lib.q3_gemm_gate_up_swiglu_quant(a, as_, b, bsg, b, bsg, s8, ss, 256,
+                                            None) == ERR_UNSUPPORTED
+    best, bidx = V(M, 1, DT_F32), V(M, 1, DT_I32)
+    assert lib.q3_gemm_nt_group_argmax(a, as_, b, bsg, best, bidx, 256, None) == ERR_UNSUPPORTED
+    # a [N][K/g] view with too few rows is an inconsistent view, not per-group
+    assert lib.q3_gemm_nt_group_store(a, as_, b, V(N - 1, K // 256, DT_F32), V(M, N, DT_F32), 256,
+                                      None, None, None, None, None, None, C.c_float(0),
+                                      None) == ERR_VIEW

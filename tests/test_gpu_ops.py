@@ -110,6 +110,39 @@ def test_gemm_residual_config1_grid(cuda, M, K, N, group):
     assert bits_equal(got, ref), describe_diff(got, ref)
 
 
+@pytest.mark.parametrize("M", [1, 32, 512, 2048])
+@pytest.mark.parametrize("K,N,group", SHAPES)
+def test_gemm_group_bscale_residual_config1(cuda, M, K, N, group):
+    """BASELINE config 1 with its per-(row, group) B scales b_scale [N][K/g]:
+    x = D + x over the whole grid, against the oracle's restatement."""
+    note(f"gemm per-group B scales + residual M={M} K={K} N={N} g={group}")
+    rng = np.random.default_rng(11 * M + K + 5 * N)
+    a, as_, b, _ = rand_gemm(rng, M, K, N, group)
+    bsg = rng.uniform(1e-3, 1e-1, (N, K // group)).astype(F)
+    x = rng.normal(size=(M, N)).astype(F)
+    xt = dev(x)
+    ops.gemm_nt_group_store(dev(a), dev(as_), dev(b), dev(bsg), None, group, add=xt)
+    ref = (oracle.gemm_nt_group_bg(a, as_, b, bsg, group) + x).astype(F)
+    got = host(xt)
+    assert bits_equal(got, ref), describe_diff(got, ref)
+
+
+@pytest.mark.parametrize("M", [1, 5, 16, 17, 64, 300])
+def test_gemm_group_bscale_store(cuda, M):
+    """Per-(row, group) B scales with the plain store, on every GEMM path
+    (M <= 16: the GEMV kernel; 17..64: 32-column tiles; above: 128-column
+    tiles), at both group sizes."""
+    for K, N, group in ((1024, 2048, 256), (2048, 1024, 128)):
+        rng = np.random.default_rng(M + K)
+        a, as_, b, _ = rand_gemm(rng, M, K, N, group)
+        bsg = rng.uniform(1e-3, 1e-1, (N, K // group)).astype(F)
+        out = torch.zeros((M, N), dtype=torch.float32, device=cuda)
+        ops.gemm_nt_group_store(dev(a), dev(as_), dev(b), dev(bsg), out, group)
+        ref = oracle.gemm_nt_group_bg(a, as_, b, bsg, group)
+        got = host(out)
+        assert bits_equal(got, ref), (K, N, describe_diff(got, ref))
+
+
 @pytest.mark.parametrize("M", [1, 9, 40, 130])
 def test_gemm_head_quant(cuda, M):
     """V epilogue: per-head int8 quant (group_gemm.h:173-193)."""

@@ -104,6 +104,47 @@ def test_group_gemm_dequant_order():
     assert not bits_equal(out, reversed_)
 
 
+def test_group_gemm_per_group_bscale_pins():
+    """BASELINE config 1's per-(row, group) weight scales (not a reference
+    function), pinned by what the arithmetic fixes: equal scales across a
+    row's groups give the reference's per-row GEMM bit for bit; unit scales
+    give the integer matmul; random scales agree with the f64 sum of the
+    exact products within the rounding bound of its four roundings per term;
+    and the plausible mistakes (one group's scale for every group, the
+    [g][n] index, the scale product in the other order) fail."""
+    rng = np.random.default_rng(12)
+    F = np.float32
+    M, K, N, G = 9, 1024, 256, 256
+    ng = K // G
+    a = rng.integers(-127, 128, (M, K)).astype(np.int8)
+    w = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    as_ = rng.uniform(1e-3, 1e-1, (M, ng)).astype(F)
+    ws = rng.uniform(1e-3, 1e-1, N).astype(F)
+    same = np.repeat(ws[:, None], ng, axis=1)
+    assert bits_equal(oracle.gemm_nt_group_bg(a, as_, w, same, G), oracle.gemm_nt_group(a, as_, w, ws, G))
+    one = oracle.gemm_nt_group_bg(a, np.ones((M, ng), F), w, np.ones((N, ng), F), G)
+    assert np.array_equal(one.astype(np.int64), a.astype(np.int64) @ w.astype(np.int64).T)
+    wsg = rng.uniform(1e-3, 1e-1, (N, ng)).astype(F)
+    out = oracle.gemm_nt_group_bg(a, as_, w, wsg, G)
+    p = oracle.gemm_nt_group_i32(a, w, G).astype(np.float64)      # [M][g][N], exact
+    terms = p * wsg.T[None, :, :].astype(np.float64) * as_[:, :, None].astype(np.float64)
+    exact = terms.sum(axis=1)
+    bound = 4 * 2.0 ** -24 * np.abs(terms).sum(axis=1) * ng + 1e-30
+    assert np.all(np.abs(out - exact) <= bound)
+    p32 = p.astype(F)
+    def acc(scale_of, order_ab=True):
+        r = np.zeros((M, N), F)
+        for g in range(ng):
+            x = (p32[:, g, :] * scale_of(g)).astype(F) if order_ab else (p32[:, g, :] * as_[:, g:g + 1]).astype(F)
+            x = (x * as_[:, g:g + 1]).astype(F) if order_ab else (x * scale_of(g)).astype(F)
+            r = (r + x).astype(F)
+        return r
+    assert bits_equal(out, acc(lambda g: wsg[None, :, g]))
+    assert not bits_equal(out, acc(lambda g: wsg[None, :, 0]))
+    assert not bits_equal(out, acc(lambda g: wsg.reshape(ng, N)[g][None, :]))
+    assert not bits_equal(out, acc(lambda g: wsg[None, :, g], order_ab=False))
+
+
 def test_quant_golden_and_invariants():
     g = golden("ops.npz")
     q, s = oracle.quant_rows_heads(g["qh_x"], 128)
