@@ -335,6 +335,87 @@ int q3_decode_batch(q3_model *m, uint32_t n, const int32_t *ids, const int32_t *
  * (not the blob). */
 int q3_model_close(q3_model *m);
 
+/* The layout, device blob and stream the model was opened with (no
+ * counterpart in the reference, whose model is a set of global views). */
+int q3_model_info(const q3_model *m, q3_layout *lay, void **blob, void **stream);
+
+/* ------------------------------------------------------------------------ */
+/* Host engine: tools/engine.py:81-250 (PagePool, Scheduler, Engine.step)   */
+/* ------------------------------------------------------------------------ */
+
+/* Request states: tools/engine.py:15-19 (State). */
+enum { Q3_REQ_WAITING = 0, Q3_REQ_PREFILL = 1, Q3_REQ_DECODE = 2, Q3_REQ_FINISHED = 3 };
+
+/* A request record (tools/engine.py:33-59 Request: prompt length, n_fed,
+ * len(generated), params.max_new, state, len(pages)). */
+typedef struct q3_sched_req {
+  uint32_t n_prompt, n_fed, n_gen, max_new;
+  int32_t state;
+  uint32_t n_pages;
+} q3_sched_req;
+
+/* One request's rows in a batch (tools/engine.py:62-70 BatchItem; `slot` is
+ * the request's admission index, pos its n_fed when the batch was built). */
+typedef struct q3_sched_item {
+  int32_t slot;
+  uint32_t row_start, rows, pos;
+  int32_t prefill, needs_logits;
+} q3_sched_item;
+
+/* The scheduling core: a pool of num_pages physical pages of page_tokens
+ * tokens (tools/engine.py:81-115: handed out from the top of a free stack,
+ * returned to it) and the requests in admission order
+ * (tools/engine.py:152-200).  Host memory only. */
+typedef struct q3_sched q3_sched;
+int q3_sched_create(uint32_t num_pages, uint32_t page_tokens, q3_sched **out);
+int q3_sched_destroy(q3_sched *s);
+/* Engine.add_request / Scheduler.add: a WAITING record; *slot = its index. */
+int q3_sched_add(q3_sched *s, uint32_t n_prompt, uint32_t max_new, int32_t *slot);
+int q3_sched_get(const q3_sched *s, int32_t slot, q3_sched_req *out);
+/* Overwrites n_prompt, n_fed, n_gen, max_new and state (not the pages). */
+int q3_sched_set(q3_sched *s, int32_t slot, const q3_sched_req *in);
+/* The record's pages (logical order): *n = count, the first min(cap, *n)
+ * copied to out (may be NULL). */
+int q3_sched_pages(const q3_sched *s, int32_t slot, uint32_t *out, uint32_t cap, uint32_t *n);
+/* The free stack, bottom to top (the next page handed out is the last). */
+int q3_sched_free_pages(const q3_sched *s, uint32_t *out, uint32_t cap, uint32_t *n);
+/* PagePool.alloc_page: *page = the top free page, or -1 when none is free.
+ * With slot >= 0 it joins the record's pages; with slot == -1 it belongs to
+ * no record and is never returned to the pool. */
+int q3_sched_alloc_page(q3_sched *s, int32_t slot, int32_t *page);
+/* PagePool.ensure: pages for the record's first n_tokens tokens; *ok = 0
+ * when the pool runs dry (the pages found so far stay with the record). */
+int q3_sched_ensure(q3_sched *s, int32_t slot, uint32_t n_tokens, int32_t *ok);
+/* PagePool.release: the record's pages go back to the free stack. */
+int q3_sched_release(q3_sched *s, int32_t slot);
+/* Scheduler.finish: FINISHED, pages released (no-op when finished). */
+int q3_sched_finish(q3_sched *s, int32_t slot);
+/* Scheduler.build_batch: items in admission order (a prompt chunk of up to
+ * 32 rows, or one decode row), at most max_rows rows; records at their
+ * max_new are finished.  Q3_ERR_RANGE if more than cap items. */
+int q3_sched_build(q3_sched *s, uint32_t max_rows, q3_sched_item *items, uint32_t cap,
+                   uint32_t *n_items, uint32_t *total_rows);
+/* The bookkeeping half of Engine.step after sampling: n_fed += rows; an
+ * item with logits adds one generated id and finishes its request when
+ * stop[i] != 0 or max_new is reached, else the request is DECODE; a prompt
+ * chunk without logits leaves it PREFILL. */
+int q3_sched_commit(q3_sched *s, const q3_sched_item *items, uint32_t n, const int32_t *stop);
+/* Engine.step with an empty batch: finishes every request whose prompt is
+ * fed and whose max_new is reached; *n_finished may be NULL. */
+int q3_sched_finish_exhausted(q3_sched *s, uint32_t *n_finished);
+/* The device side of a batch (the guest step): tokens holds each item's
+ * row ids, concatenated in item order.  A prompt chunk, or a decode row
+ * with on_device[i] == 0, runs q3_forward_chunk over the record's pages
+ * (installed as the model's page table; its ids written to ids[pos..]) and,
+ * when it needs logits, copies the vocab-wide logits row to
+ * logits + i * ld_logits (host); decode rows with on_device[i] != 0 share
+ * q3_decode_batch calls and receive their greedy id in out_ids[i] (-1 for
+ * the others).  page_tokens must be 32 and every page within the model's
+ * pool.  Synchronous. */
+int q3_sched_run(q3_sched *s, q3_model *m, const q3_sched_item *items, uint32_t n,
+                 const int32_t *tokens, const int32_t *on_device, int32_t *out_ids,
+                 float *logits, uint64_t ld_logits);
+
 /* ---- measurement (no counterpart in the reference) ------------------------
  * Decode kernel classes whose launches the model can time with HIP events on
  * its own stream (hipExtLaunchKernel start/stop events: the kernel's own

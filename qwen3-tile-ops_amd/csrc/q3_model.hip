@@ -1187,6 +1187,14 @@ extern "C" int q3_model_set_page_table(q3_model *m, const uint16_t *table, uint3
   return Q3_OK;
 }
 
+extern "C" int q3_model_info(const q3_model *m, q3_layout *lay, void **blob, void **stream) {
+  if (!m) return Q3_ERR_ARG;
+  if (lay) *lay = m->lay;
+  if (blob) *blob = m->blob;
+  if (stream) *stream = m->stream;
+  return Q3_OK;
+}
+
 extern "C" int q3_forward_chunk(q3_model *m, uint32_t pos, uint32_t rows, int lm_out,
                                 int optimize_tail) {
   if (!m) return Q3_ERR_ARG;

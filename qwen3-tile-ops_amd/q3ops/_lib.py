@@ -103,6 +103,22 @@ SIGNATURES = {
     "q3_generate": (_I, [_VP]),
     "q3_model_close": (_I, [_VP]),
     "q3_decode_batch": (_I, [_VP, _U, _VP, _VP, _VP, _U, _VP]),
+    "q3_model_info": (_I, [_VP, C.POINTER(CLayout), C.POINTER(_VP), C.POINTER(_VP)]),
+    "q3_sched_create": (_I, [_U, _U, C.POINTER(_VP)]),
+    "q3_sched_destroy": (_I, [_VP]),
+    "q3_sched_add": (_I, [_VP, _U, _U, _VP]),
+    "q3_sched_get": (_I, [_VP, C.c_int32, _VP]),
+    "q3_sched_set": (_I, [_VP, C.c_int32, _VP]),
+    "q3_sched_pages": (_I, [_VP, C.c_int32, _VP, _U, _VP]),
+    "q3_sched_free_pages": (_I, [_VP, _VP, _U, _VP]),
+    "q3_sched_alloc_page": (_I, [_VP, C.c_int32, _VP]),
+    "q3_sched_ensure": (_I, [_VP, C.c_int32, _U, _VP]),
+    "q3_sched_release": (_I, [_VP, C.c_int32]),
+    "q3_sched_finish": (_I, [_VP, C.c_int32]),
+    "q3_sched_build": (_I, [_VP, _U, _VP, _U, _VP, _VP]),
+    "q3_sched_commit": (_I, [_VP, _VP, _U, _VP]),
+    "q3_sched_finish_exhausted": (_I, [_VP, _VP]),
+    "q3_sched_run": (_I, [_VP, _VP, _VP, _U, _VP, _VP, _VP, _VP, C.c_uint64]),
     "q3_model_set_kernel_timing": (_I, [_VP, _U]),
     "q3_model_kernel_time": (_I, [_VP, _I, C.POINTER(C.c_double), C.POINTER(C.c_uint32)]),
 }

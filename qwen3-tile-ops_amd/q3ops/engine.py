@@ -1,34 +1,44 @@
 """Continuous-batching host engine over the device model (tools/engine.py).
 
-The reference's engine is a host scaffold: a page pool of 32-token KV pages,
-a scheduler that packs prefill chunks (first) and decode rows into one batch
-of at most ``max_rows`` rows, and a sampler (greedy, temperature, top-k,
-top-p, repetition penalty) driven by a ``guest_step(batch)`` callback that
-returns logits per request.  The classes below keep that interface (names,
-fields, argument meaning) so that a caller of the reference can switch:
+The engine's state and decisions live in the host scheduling core of
+libq3ops.so (``q3_sched_*`` in include/q3ops.h): the page pool, one record
+per request (prompt length, tokens fed, ids generated, limit, state, pages),
+batch building, the commit of a batch's ids and the device step.  The
+classes below keep the reference's interface (names, fields, argument
+meaning) as views of that core, so that a caller of the reference can
+switch:
 
-- ``PagePool``   (engine.py:81-115): LIFO free list of physical page ids;
-- ``Sampler``    (engine.py:118-149): float64 host sampling, per-request
-  ``numpy.random.default_rng(seed)`` stream;
-- ``Scheduler``  (engine.py:152-200): admission-ordered batch building;
-- ``Engine``     (engine.py:203-250): step / run / outputs.
+- ``PagePool``  (engine.py:81-115): ``free`` / ``used`` / ``free_pages`` are
+  read from the core's free stack; ``alloc_page`` / ``ensure`` / ``release``
+  act on it;
+- ``Request``   (engine.py:33-59): ``n_fed``, ``pages`` and ``state`` are the
+  core record's once a pool or engine has taken the request; ``generated``
+  (the ids) and the per-request ``rng`` stay in Python;
+- ``Scheduler`` (engine.py:152-200): ``build_batch`` is ``q3_sched_build``;
+- ``Sampler``   (engine.py:118-149): host float64 sampling in the reference's
+  order of numpy operations, so that a seeded request draws the same ids;
+- ``Engine``    (engine.py:203-250): step = build, guest step, sample,
+  ``q3_sched_commit``.
 
-``GpuGuest`` is the device side: prefill chunks and logits rows run through
-``q3_forward_chunk`` with the request's own page table, and greedy decode
-rows of a batch share one ``q3_decode_batch`` launch sequence whose lm_head
-keeps the argmax on the device (only the id comes back).  A guest may answer
-a request with an ``int`` (a token already chosen on the device) instead of
-logits; ``Engine.step`` then uses it as the sample, which is what
-``Sampler.sample`` returns for ``temperature <= 0`` (first index of the
-maximum, engine.py:121-122).
+``GpuGuest`` is the device side (``q3_sched_run``): prefill chunks and rows
+whose logits the host samples run ``q3_forward_chunk`` over the request's own
+page table; greedy decode rows of a batch share ``q3_decode_batch`` launches
+whose lm_head keeps the argmax on the device (only the id comes back).  A
+guest may answer a request with an ``int`` (a token already chosen on the
+device) instead of logits; ``Engine.step`` then uses it as the sample, which
+is what ``Sampler.sample`` returns for ``temperature <= 0`` (first index of
+the maximum, engine.py:121-122).
 """
 from __future__ import annotations
 
+import ctypes as C
 from dataclasses import dataclass, field
 from enum import Enum
 from typing import Callable, Mapping, Sequence, Union
 
 import numpy as np
+
+from ._lib import check, lib
 
 __all__ = ["State", "SamplingParams", "Request", "BatchItem", "Batch", "PagePool",
            "Sampler", "Scheduler", "Engine", "GpuGuest", "make_gpu_engine"]
@@ -37,11 +47,15 @@ PREFILL_CHUNK = 32  # rows of one prefill chunk (engine.py:175)
 
 
 class State(str, Enum):
-    """Request life cycle (engine.py:15-19)."""
+    """Request life cycle (engine.py:15-19); the core's Q3_REQ_* codes are
+    the member positions."""
     WAITING = "waiting"
     PREFILL = "prefill"
     DECODE = "decode"
     FINISHED = "finished"
+
+
+_STATES = list(State)
 
 
 @dataclass
@@ -56,21 +70,131 @@ class SamplingParams:
     stop_tokens: set = field(default_factory=set)
 
 
-@dataclass
-class Request:
-    """engine.py:33-59: ``n_fed`` counts the tokens whose K/V are cached;
-    ``pages`` is the logical -> physical page table."""
-    rid: int
-    prompt: list
-    params: SamplingParams
-    generated: list = field(default_factory=list)
-    n_fed: int = 0
-    pages: list = field(default_factory=list)
-    state: State = State.WAITING
-    rng: np.random.Generator | None = None
+class SchedReq(C.Structure):
+    """q3_sched_req."""
+    _fields_ = [("n_prompt", C.c_uint32), ("n_fed", C.c_uint32), ("n_gen", C.c_uint32),
+                ("max_new", C.c_uint32), ("state", C.c_int32), ("n_pages", C.c_uint32)]
 
-    def __post_init__(self) -> None:
-        self.rng = np.random.default_rng(self.params.seed)
+
+class SchedItem(C.Structure):
+    """q3_sched_item."""
+    _fields_ = [("slot", C.c_int32), ("row_start", C.c_uint32), ("rows", C.c_uint32),
+                ("pos", C.c_uint32), ("prefill", C.c_int32), ("needs_logits", C.c_int32)]
+
+
+class _Core:
+    """Owner of one q3_sched handle and the Request objects of its records
+    (index = slot = admission order in the core)."""
+
+    def __init__(self, num_pages: int, page_tokens: int) -> None:
+        h = C.c_void_p()
+        check(lib().q3_sched_create(int(num_pages), int(page_tokens), C.byref(h)), "q3_sched_create")
+        self.h = h
+        self.num_pages = int(num_pages)
+        self.page_tokens = int(page_tokens)
+        self.reqs: list = []
+
+    def __del__(self) -> None:
+        h = getattr(self, "h", None)
+        if h is not None and h.value:
+            lib().q3_sched_destroy(h)
+            self.h = C.c_void_p()
+
+    def bind(self, req: "Request") -> int:
+        """Registers req (once) and returns its slot."""
+        if req._core is self:
+            return req._slot
+        if req._core is not None:
+            raise ValueError(f"request {req.rid} belongs to another pool")
+        if req._local_pages:
+            raise ValueError(f"request {req.rid}: pages can only come from the pool")
+        slot = C.c_int32()
+        check(lib().q3_sched_add(self.h, req.n_prompt, int(req.params.max_new), C.byref(slot)),
+              "q3_sched_add")
+        req._core, req._slot = self, slot.value
+        self.reqs.append(req)
+        self.put(req, n_fed=req._local_n_fed, state=req._local_state)
+        return slot.value
+
+    def get(self, req: "Request") -> SchedReq:
+        r = SchedReq()
+        check(lib().q3_sched_get(self.h, req._slot, C.byref(r)), "q3_sched_get")
+        return r
+
+    def put(self, req: "Request", **kw) -> None:
+        r = self.get(req)
+        r.n_prompt = req.n_prompt
+        r.max_new = int(req.params.max_new)
+        r.n_gen = len(req.generated)
+        if "n_fed" in kw:
+            r.n_fed = int(kw["n_fed"])
+        if "state" in kw:
+            r.state = _STATES.index(State(kw["state"]))
+        check(lib().q3_sched_set(self.h, req._slot, C.byref(r)), "q3_sched_set")
+
+    def pages(self, req: "Request") -> list:
+        n = C.c_uint32()
+        check(lib().q3_sched_pages(self.h, req._slot, None, 0, C.byref(n)), "q3_sched_pages")
+        buf = (C.c_uint32 * max(n.value, 1))()
+        check(lib().q3_sched_pages(self.h, req._slot, buf, n.value, C.byref(n)), "q3_sched_pages")
+        return list(buf[:n.value])
+
+    def free_list(self) -> list:
+        n = C.c_uint32()
+        buf = (C.c_uint32 * max(self.num_pages, 1))()
+        check(lib().q3_sched_free_pages(self.h, buf, self.num_pages, C.byref(n)),
+              "q3_sched_free_pages")
+        return list(buf[:n.value])
+
+
+class Request:
+    """engine.py:33-59.  ``n_fed`` counts the tokens whose K/V are cached;
+    ``pages`` is the logical -> physical page table.  Until a pool or an
+    engine takes the request, n_fed / pages / state are held here; after
+    that they are the core record's."""
+
+    def __init__(self, rid: int, prompt, params: SamplingParams, generated=None, n_fed: int = 0,
+                 pages=None, state: State = State.WAITING, rng=None) -> None:
+        self.rid = rid
+        self.prompt = list(prompt)
+        self.params = params
+        self.generated = list(generated or [])
+        self.rng = rng if rng is not None else np.random.default_rng(params.seed)
+        self._core: _Core | None = None
+        self._slot = -1
+        self._local_n_fed = int(n_fed)
+        self._local_pages = list(pages or [])
+        self._local_state = State(state)
+
+    def __repr__(self) -> str:
+        return (f"Request(rid={self.rid}, n_prompt={self.n_prompt}, n_fed={self.n_fed}, "
+                f"generated={self.generated}, pages={self.pages}, state={self.state.value})")
+
+    @property
+    def n_fed(self) -> int:
+        return self._core.get(self).n_fed if self._core else self._local_n_fed
+
+    @n_fed.setter
+    def n_fed(self, v: int) -> None:
+        if self._core:
+            self._core.put(self, n_fed=v)
+        else:
+            self._local_n_fed = int(v)
+
+    @property
+    def state(self) -> State:
+        return _STATES[self._core.get(self).state] if self._core else self._local_state
+
+    @state.setter
+    def state(self, v: State) -> None:
+        if self._core:
+            self._core.put(self, state=v)
+        else:
+            self._local_state = State(v)
+
+    @property
+    def pages(self) -> list:
+        return self._core.pages(self) if self._core else list(self._local_pages)
 
     @property
     def n_prompt(self) -> int:
@@ -102,6 +226,8 @@ class BatchItem:
 class Batch:
     items: list
     total_rows: int
+    _core: object = field(default=None, repr=False, compare=False)
+    _raw: object = field(default=None, repr=False, compare=False)
 
     @property
     def requests(self) -> list:
@@ -109,44 +235,51 @@ class Batch:
 
 
 class PagePool:
-    """Physical KV pages shared by all requests (engine.py:81-115).  Pages
-    are handed out from the end of the free list and returned to its end,
-    so the assignment order equals the reference's."""
+    """Physical KV pages shared by all requests (engine.py:81-115), a view of
+    the core's free stack: pages are handed out from its top and returned to
+    it, so the assignment order equals the reference's."""
 
-    def __init__(self, num_pages: int, page_tokens: int = 32) -> None:
-        self.num_pages = int(num_pages)
-        self.page_tokens = int(page_tokens)
-        self.free = list(range(self.num_pages))
-        self.used: set = set()
+    def __init__(self, num_pages: int, page_tokens: int = 32, _core: _Core | None = None) -> None:
+        self._core = _core or _Core(num_pages, page_tokens)
 
-    def alloc_page(self) -> int | None:
-        if not self.free:
-            return None
-        page = self.free.pop()
-        self.used.add(page)
-        return page
+    @property
+    def num_pages(self) -> int:
+        return self._core.num_pages
 
-    def ensure(self, req: Request, n_tokens: int) -> bool:
-        """Grows req.pages to cover n_tokens; False when the pool runs dry
-        (the pages taken so far stay with the request)."""
-        need = -(-int(n_tokens) // self.page_tokens)
-        while len(req.pages) < need:
-            page = self.alloc_page()
-            if page is None:
-                return False
-            req.pages.append(page)
-        return True
+    @property
+    def page_tokens(self) -> int:
+        return self._core.page_tokens
 
-    def release(self, req: Request) -> None:
-        for page in req.pages:
-            if page in self.used:
-                self.used.discard(page)
-                self.free.append(page)
-        req.pages.clear()
+    @property
+    def free(self) -> list:
+        """Free pages, bottom to top (``alloc_page`` takes the last)."""
+        return self._core.free_list()
+
+    @property
+    def used(self) -> set:
+        return set(range(self.num_pages)) - set(self.free)
 
     @property
     def free_pages(self) -> int:
         return len(self.free)
+
+    def alloc_page(self) -> int | None:
+        page = C.c_int32()
+        check(lib().q3_sched_alloc_page(self._core.h, -1, C.byref(page)), "q3_sched_alloc_page")
+        return None if page.value < 0 else page.value
+
+    def ensure(self, req: Request, n_tokens: int) -> bool:
+        """Grows req.pages to cover n_tokens; False when the pool runs dry
+        (the pages taken so far stay with the request)."""
+        slot = self._core.bind(req)
+        ok = C.c_int32()
+        check(lib().q3_sched_ensure(self._core.h, slot, int(n_tokens), C.byref(ok)),
+              "q3_sched_ensure")
+        return bool(ok.value)
+
+    def release(self, req: Request) -> None:
+        if req._core is self._core:
+            check(lib().q3_sched_release(self._core.h, req._slot), "q3_sched_release")
 
 
 def _repetition_penalty(x: np.ndarray, generated: Sequence[int], penalty: float) -> None:
@@ -199,61 +332,50 @@ class Sampler:
 
 
 class Scheduler:
-    """engine.py:152-200: requests in admission order; a request still in
-    its prompt contributes one chunk of up to 32 rows, a decoding request one
-    row (its last generated id); a request that cannot get its pages waits
-    for a later batch."""
+    """engine.py:152-200 over the core: requests in admission order; a
+    request still in its prompt contributes one chunk of up to 32 rows, a
+    decoding request one row (its last generated id); a request that cannot
+    get its pages waits for a later batch."""
 
     def __init__(self, pool: PagePool, max_rows: int = 32) -> None:
         self.pool = pool
         self.max_rows = int(max_rows)
-        self.requests: list = []
+
+    @property
+    def requests(self) -> list:
+        return list(self.pool._core.reqs)
 
     def add(self, req: Request) -> None:
-        self.requests.append(req)
+        self.pool._core.bind(req)
 
     def finish(self, req: Request) -> None:
-        if req.state != State.FINISHED:
-            req.state = State.FINISHED
-            self.pool.release(req)
-
-    def _prefill_item(self, req: Request, rows: int) -> BatchItem | None:
-        chunk = min(PREFILL_CHUNK, req.n_prompt - req.n_fed, self.max_rows - rows)
-        if chunk <= 0 or not self.pool.ensure(req, req.n_fed + chunk):
-            return None
-        end = req.n_fed + chunk
-        return BatchItem(req, rows, chunk, req.n_fed, list(req.prompt[req.n_fed:end]),
-                         True, end == req.n_prompt)
-
-    def _decode_item(self, req: Request, rows: int) -> BatchItem | None:
-        if not req.generated or not self.pool.ensure(req, req.n_fed + 1):
-            return None
-        return BatchItem(req, rows, 1, req.n_fed, [req.generated[-1]], False, True)
+        core = self.pool._core
+        core.bind(req)
+        check(lib().q3_sched_finish(core.h, req._slot), "q3_sched_finish")
 
     def build_batch(self) -> Batch:
-        items: list = []
-        rows = 0
-        for req in self.requests:
-            if req.done:
-                continue
-            if req.n_fed < req.n_prompt:
-                item = self._prefill_item(req, rows) if rows < self.max_rows else None
-            elif len(req.generated) >= req.params.max_new:
-                self.finish(req)
-                continue
-            else:
-                item = self._decode_item(req, rows) if rows < self.max_rows else None
-            if item is not None:
-                items.append(item)
-                rows += item.rows
-        return Batch(items, rows)
+        core = self.pool._core
+        cap = max(len(core.reqs), 1)
+        raw = (SchedItem * cap)()
+        n, rows = C.c_uint32(), C.c_uint32()
+        check(lib().q3_sched_build(core.h, self.max_rows, raw, cap, C.byref(n), C.byref(rows)),
+              "q3_sched_build")
+        items = []
+        for it in raw[:n.value]:
+            req = core.reqs[it.slot]
+            ids = (req.prompt[it.pos:it.pos + it.rows] if it.prefill else [req.generated[-1]])
+            items.append(BatchItem(req, it.row_start, it.rows, it.pos, list(ids),
+                                   bool(it.prefill), bool(it.needs_logits)))
+        return Batch(items, rows.value, core, raw)
 
 
 GuestResult = Union[Sequence[float], np.ndarray, int]
 
 
 class Engine:
-    """engine.py:203-250."""
+    """engine.py:203-250: step = build a batch, run the guest step, take one
+    id per item with logits (the guest's device id, or the sampler's draw),
+    commit them to the core."""
 
     def __init__(self, guest_step: Callable[[Batch], Mapping[int, GuestResult]],
                  num_pages: int = 256, page_tokens: int = 32, max_rows: int = 32,
@@ -272,38 +394,29 @@ class Engine:
         self.sched.add(req)
         return req
 
-    def _finish_exhausted(self) -> None:
-        for req in self.sched.requests:
-            if (not req.done and req.n_fed >= req.n_prompt
-                    and len(req.generated) >= req.params.max_new):
-                self.sched.finish(req)
+    def _pick(self, req: Request, out: GuestResult) -> int:
+        if isinstance(out, (int, np.integer)):
+            if req.params.temperature > 0.0:
+                raise ValueError(f"request {req.rid}: the guest returned an id for a sampled "
+                                 "(temperature > 0) request")
+            return int(out)
+        return self.sampler.sample(out, req)
 
     def step(self) -> bool:
         """One batch; False when nothing could be scheduled."""
         batch = self.sched.build_batch()
+        core = self.pool._core
         if not batch.items:
-            self._finish_exhausted()
+            check(lib().q3_sched_finish_exhausted(core.h, None), "q3_sched_finish_exhausted")
             return False
         results = self.guest_step(batch)
-        for it in batch.items:
-            req = it.req
-            req.n_fed += it.rows
+        stop = (C.c_int32 * len(batch.items))()
+        for i, it in enumerate(batch.items):
             if it.needs_logits:
-                out = results[req.rid]
-                if isinstance(out, (int, np.integer)):
-                    if req.params.temperature > 0.0:
-                        raise ValueError(f"request {req.rid}: the guest returned an id for a "
-                                         "sampled (temperature > 0) request")
-                    tok = int(out)
-                else:
-                    tok = self.sampler.sample(out, req)
-                req.generated.append(tok)
-                if tok in req.params.stop_tokens or len(req.generated) >= req.params.max_new:
-                    self.sched.finish(req)
-                else:
-                    req.state = State.DECODE
-            elif req.n_fed < req.n_prompt:
-                req.state = State.PREFILL
+                tok = self._pick(it.req, results[it.req.rid])
+                it.req.generated.append(tok)
+                stop[i] = int(tok in it.req.params.stop_tokens)
+        check(lib().q3_sched_commit(core.h, batch._raw, len(batch.items), stop), "q3_sched_commit")
         self.steps += 1
         return True
 
@@ -316,86 +429,49 @@ class Engine:
 
 
 class GpuGuest:
-    """guest_step on the device model (a ``q3ops.Model``).
+    """guest_step on the device model (a ``q3ops.Model``) through
+    ``q3_sched_run``:
 
-    - A prefill chunk, or any row whose logits the host sampler needs, runs
+    - a prefill chunk, or any row whose logits the host sampler needs, runs
       ``q3_forward_chunk(pos, rows)`` after its ids are written to the blob's
       id array at ``pos`` and the request's pages are installed as the page
-      table; ``Q3_LM_LOGITS`` returns the last row's logits.
-    - Greedy decode rows (temperature <= 0) of one batch go to one
-      ``q3_decode_batch`` call: each row writes its K/V through its own page
-      table and its id comes back from the device argmax.
+      table; ``Q3_LM_LOGITS`` returns the last row's logits;
+    - greedy decode rows (temperature <= 0) of one batch share
+      ``q3_decode_batch`` calls: each row writes its K/V through its own
+      page table and its id comes back from the device argmax.
     Every request's result is bit-identical to running it alone: rows of
     different requests share GEMM launches but no arithmetic.
     """
 
     def __init__(self, model, greedy_on_device: bool = True) -> None:
-        import torch
         self.model = model
-        L = model.layout
-        self.page_slots = L.max_seq // 32
-        self.max_chunk = L.seq
-        self.max_seq = L.max_seq
+        self.vocab = model.layout.vocab
         self.greedy_on_device = greedy_on_device
-        dev = model.blob.device
-        self._ids = torch.zeros(L.seq, dtype=torch.int32, device=dev)
-        self._out = torch.zeros(L.seq, dtype=torch.int32, device=dev)
         self.launches = {"forward_chunk": 0, "decode_batch": 0}
 
-    def _table(self, req: Request) -> np.ndarray:
-        if len(req.pages) > self.page_slots or any(p >= self.page_slots for p in req.pages):
-            raise ValueError(f"request {req.rid}: pages {req.pages} exceed the model's pool "
-                             f"of {self.page_slots}")
-        t = np.zeros(self.page_slots, np.uint16)
-        t[:len(req.pages)] = req.pages
-        return t
-
-    def _check_rows(self, it: BatchItem) -> None:
-        if it.rows > self.max_chunk or it.pos + it.rows > self.max_seq:
-            raise ValueError(f"request {it.req.rid}: rows [{it.pos}, {it.pos + it.rows}) "
-                             f"exceed chunk {self.max_chunk} / max_seq {self.max_seq}")
-
-    def _run_chunk(self, it: BatchItem, out: dict) -> None:
-        import torch
-        from .model import LM_LOGITS, LM_NONE
-        self._check_rows(it)
-        m = self.model
-        m.set_page_table(self._table(it.req))
-        ids = np.ascontiguousarray(np.asarray(it.token_ids, np.int32))
-        o = m.layout["kIDS"] + 4 * it.pos
-        m.blob[o:o + 4 * ids.size].copy_(torch.from_numpy(ids.view(np.uint8)))
-        m.forward_chunk(it.pos, it.rows, LM_LOGITS if it.needs_logits else LM_NONE,
-                        optimize_tail=True)
-        self.launches["forward_chunk"] += 1
-        if it.needs_logits:
-            out[it.req.rid] = m.stage("logits", 1)[0].copy()
-
-    def _run_greedy_rows(self, items: list, out: dict) -> None:
-        import torch
-        for it in items:
-            self._check_rows(it)
-        n = len(items)
-        ids = np.array([it.token_ids[0] for it in items], np.int32)
-        self._ids[:n].copy_(torch.from_numpy(ids))
-        pos = np.array([it.pos for it in items], np.int32)
-        tables = np.stack([self._table(it.req) for it in items])
-        self.model.decode_batch(self._ids, pos, tables, self._out)
-        self.launches["decode_batch"] += 1
-        got = self._out[:n].cpu().numpy()
-        for it, tok in zip(items, got):
-            out[it.req.rid] = int(tok)
-
     def __call__(self, batch: Batch) -> dict:
+        n = len(batch.items)
+        if n == 0:
+            return {}
+        tokens = np.ascontiguousarray(np.concatenate(
+            [np.asarray(it.token_ids, np.int32) for it in batch.items]))
+        dev = np.array([int(self.greedy_on_device and not it.prefill
+                            and it.req.params.temperature <= 0.0) for it in batch.items], np.int32)
+        ids = np.full(n, -1, np.int32)
+        need = [i for i, it in enumerate(batch.items) if it.needs_logits and not dev[i]]
+        logits = np.zeros((n if need else 1, self.vocab), np.float32)
+        check(lib().q3_sched_run(batch._core.h, self.model.handle, batch._raw, n,
+                                 tokens.ctypes.data_as(C.c_void_p), dev.ctypes.data_as(C.c_void_p),
+                                 ids.ctypes.data_as(C.c_void_p),
+                                 logits.ctypes.data_as(C.c_void_p) if need else None,
+                                 self.vocab), "q3_sched_run")
+        self.launches["forward_chunk"] += int(n - dev.sum())
+        self.launches["decode_batch"] += -(-int(dev.sum()) // self.model.layout.seq)
         out: dict = {}
-        greedy_rows = []
-        for it in batch.items:
-            if (self.greedy_on_device and not it.prefill
-                    and it.req.params.temperature <= 0.0):
-                greedy_rows.append(it)
-            else:
-                self._run_chunk(it, out)
-        for i in range(0, len(greedy_rows), self.max_chunk):
-            self._run_greedy_rows(greedy_rows[i:i + self.max_chunk], out)
+        for i, it in enumerate(batch.items):
+            if not it.needs_logits:
+                continue
+            out[it.req.rid] = int(ids[i]) if dev[i] else logits[i].copy()
         return out
 
 

@@ -22,10 +22,17 @@ every kernel's counter is scaled by it.  FETCH_SIZE and WRITE_SIZE count
 L2 <-> fabric traffic, i.e. bytes that left the L2 (last-level-cache hits
 included).
 
-Derived figures (when their counters were collected in the same pass):
+Derived figures (when their counters were collected), rocprofv3's own
+MfmaUtil and VALUBusy expressions with one change: under --pmc every
+dispatch is serialised and GRBM_GUI_ACTIVE also counts the profiler's own
+window around it (several times the kernel), so the kernel's cycles are
+taken from a separate --kernel-trace run of the same command (--stats, its
+average duration x --clock-ghz):
   int8 ops per dispatch = SQ_INSTS_VALU_MFMA_MOPS_I8 * 512
-  MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE * CUs * 4 SIMDs)
-  VALU active = SQ_ACTIVE_INST_VALU / (GRBM_GUI_ACTIVE * CUs * 4 SIMDs)
+  MFMA util   = SQ_VALU_MFMA_BUSY_CYCLES / (kernel cycles * CUs * 4 SIMDs)
+  VALU busy   = SQ_ACTIVE_INST_VALU / (kernel cycles * CUs)
+  co-issue    = SQ_VALU_MFMA_COEXEC_CYCLES / (kernel cycles * CUs * 4 SIMDs)
+  achieved    = int8 ops per dispatch / kernel duration
   L2 hit rate = TCC_HIT_sum / (TCC_HIT_sum + TCC_MISS_sum)
 """
 from __future__ import annotations
@@ -142,15 +149,24 @@ def pmc_json(fetch: str, write: str, calib_bytes: int, cmd: str) -> dict:
             "kernels": kernels}
 
 
-def counters_json(paths: list[str], cmd: str, cus: int) -> dict:
+def _trace_durations(stats: str | None) -> dict[str, float]:
+    """kernel symbol -> average duration in ns from a kernel_stats.csv."""
+    if not stats:
+        return {}
+    return {r["Name"]: float(r["AverageNs"]) for r in csv.DictReader(open(stats))}
+
+
+def counters_json(paths: list[str], cmd: str, cus: int, stats: str | None = None,
+                  clock_ghz: float = 2.4, peak_tops: float = 5000.0) -> dict:
     """Per kernel class (and per kernel symbol within it): the mean of every
     counter over its dispatches, merged over several PMC passes, and the
-    derived MFMA / VALU / L2 figures of the module docstring."""
+    derived figures of the module docstring."""
     per: dict[str, dict[str, list[float]]] = {}
     for path in paths:
         for r in csv.DictReader(open(path)):
             name = r["Kernel_Name"]
             per.setdefault(name, {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    durs = _trace_durations(stats)
     kernels = {}
     for name, cnt in sorted(per.items()):
         cls = class_of(name)
@@ -159,20 +175,28 @@ def counters_json(paths: list[str], cmd: str, cus: int) -> dict:
         mean = {c: statistics.mean(v) for c, v in cnt.items()}
         d = {"kernel": short_name(name), "dispatches": max(len(v) for v in cnt.values()),
              "counters": mean}
-        act = mean.get("GRBM_GUI_ACTIVE")
-        if "SQ_INSTS_VALU_MFMA_MOPS_I8" in mean:
-            d["int8_ops_per_dispatch"] = mean["SQ_INSTS_VALU_MFMA_MOPS_I8"] * 512
-        if act:
+        ops = mean.get("SQ_INSTS_VALU_MFMA_MOPS_I8")
+        if ops is not None:
+            d["int8_ops_per_dispatch"] = ops * 512
+        ns = durs.get(name)
+        if ns:
+            cyc = ns * clock_ghz
+            d["trace_avg_us"] = ns / 1e3
+            if ops is not None:
+                d["achieved_tops"] = ops * 512 / ns / 1e3
+                d["frac_of_int8_peak"] = d["achieved_tops"] / peak_tops
             if "SQ_VALU_MFMA_BUSY_CYCLES" in mean:
-                d["mfma_busy"] = mean["SQ_VALU_MFMA_BUSY_CYCLES"] / (act * cus * 4)
+                d["mfma_util"] = mean["SQ_VALU_MFMA_BUSY_CYCLES"] / (cyc * cus * 4)
             if "SQ_ACTIVE_INST_VALU" in mean:
-                d["valu_active"] = mean["SQ_ACTIVE_INST_VALU"] / (act * cus * 4)
+                d["valu_busy"] = mean["SQ_ACTIVE_INST_VALU"] / (cyc * cus)
+            if "SQ_VALU_MFMA_COEXEC_CYCLES" in mean:
+                d["mfma_valu_coissue"] = mean["SQ_VALU_MFMA_COEXEC_CYCLES"] / (cyc * cus * 4)
         if "TCC_HIT_sum" in mean and "TCC_MISS_sum" in mean:
             tot = mean["TCC_HIT_sum"] + mean["TCC_MISS_sum"]
             d["l2_hit_rate"] = mean["TCC_HIT_sum"] / tot if tot else None
         key = cls if cls not in kernels else f"{cls}:{short_name(name)}"
         kernels[key] = d
-    return {"command": cmd, "cus": cus, "kernels": kernels}
+    return {"command": cmd, "cus": cus, "clock_ghz": clock_ghz, "kernels": kernels}
 
 
 def main(argv=None) -> int:
@@ -191,11 +215,13 @@ def main(argv=None) -> int:
     c.add_argument("csv", nargs="+")
     c.add_argument("--cmd", required=True)
     c.add_argument("--cus", type=int, default=256)
+    c.add_argument("--stats", help="kernel_stats.csv of a --kernel-trace run of the same command")
+    c.add_argument("--clock-ghz", type=float, default=2.4)
     a = ap.parse_args(argv)
     if a.cmd_name == "stats":
         sys.stdout.write(stats_md(a.csv, a.cmd, a.top))
     elif a.cmd_name == "counters":
-        json.dump(counters_json(a.csv, a.cmd, a.cus), sys.stdout, indent=1)
+        json.dump(counters_json(a.csv, a.cmd, a.cus, a.stats, a.clock_ghz), sys.stdout, indent=1)
         sys.stdout.write("\n")
     else:
         json.dump(pmc_json(a.fetch, a.write, a.calib_bytes, a.cmd), sys.stdout, indent=1)
