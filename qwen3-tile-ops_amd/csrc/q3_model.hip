@@ -67,6 +67,14 @@ struct q3_model {
   // decode: O projection folded into the attention kernel
   // (Q3_DECODE_FUSE_OPROJ, default 1; 0 runs it as its own GEMV)
   bool ofuse = true;
+  // q3_generate: the decode steps after the prefill chunks, captured as one
+  // HIP graph on the model's stream and replayed while the generation they
+  // were captured for (n_prompt, n_gen, mode, page table) is asked again
+  // (Q3_DECODE_GRAPH, default 1; 0 launches them one by one)
+  bool dgraph_on = true;
+  hipGraphExec_t dgraph = nullptr;
+  int32_t dg_key[3] = {-1, -1, -1};
+  uint64_t tab_version = 0, dg_tab_version = ~0ull;
 };
 
 namespace q3 {
@@ -890,6 +898,7 @@ extern "C" int q3_model_open(void *blob, const q3_layout *lay, void *stream, q3_
   m->pf_wgs = 128;
   if (const char *e = std::getenv("Q3_DECODE_PREFETCH_WGS")) m->pf_wgs = std::max(0, std::atoi(e));
   if (const char *e = std::getenv("Q3_DECODE_FUSE_OPROJ")) m->ofuse = std::atoi(e) != 0;
+  if (const char *e = std::getenv("Q3_DECODE_GRAPH")) m->dgraph_on = std::atoi(e) != 0;
   m->bkeys_ld = lay->vocab / 128 + 64;  // one key per 128-column block of the lm GEMM
   m->btab_off = (sizeof(int32_t) * lay->seq + 255) & ~size_t(255);
   const size_t bstate_bytes = m->btab_off + sizeof(uint16_t) * static_cast<size_t>(lay->seq) * m->n_pages;
@@ -1184,6 +1193,7 @@ extern "C" int q3_model_set_page_table(q3_model *m, const uint16_t *table, uint3
   Q3_HIP(hipMemcpyAsync(m->ptab, table, sizeof(uint16_t) * n, hipMemcpyHostToDevice, m->stream));
   Q3_HIP(hipStreamSynchronize(m->stream));
   m->htab.assign(table, table + n);
+  ++m->tab_version;
   return Q3_OK;
 }
 
@@ -1213,20 +1223,56 @@ extern "C" int q3_generate(q3_model *m) {
     return Q3_ERR_RANGE;
   const bool fused = (mode == 0);
   const uint32_t total = static_cast<uint32_t>(n_prompt + n_gen);
+  const uint32_t np = static_cast<uint32_t>(n_prompt);
   int32_t *ids = at<int32_t>(m, y.kIDS);
-  uint32_t pos = 0;
-  while (pos < total) {
-    const uint32_t np = static_cast<uint32_t>(n_prompt);
+  // one forward of the loop: a prompt chunk, or a one-row decode step
+  auto step = [&](uint32_t pos, uint32_t *next) {
     const uint32_t rows = (pos < np) ? ((np - pos < y.seq) ? np - pos : y.seq) : 1;
     const bool need_out = (pos + rows >= np);
     const int lm_out = need_out ? (fused ? Q3_LM_ARGMAX : Q3_LM_LOGITS) : Q3_LM_NONE;
-    const uint32_t next = pos + rows;
+    *next = pos + rows;
     // the id of the next token goes straight to ids[next] on the device
-    int32_t *id_dst = (need_out && next >= np && next < total) ? ids + next : nullptr;
-    const int rc = forward_chunk_impl(m, pos, rows, lm_out, fused ? 1 : 0, id_dst);
+    int32_t *id_dst = (need_out && *next >= np && *next < total) ? ids + *next : nullptr;
+    return forward_chunk_impl(m, pos, rows, lm_out, fused ? 1 : 0, id_dst);
+  };
+  // the decode steps run as one graph when the stream can capture (not the
+  // null stream) and no launch is being timed
+  const bool graph = m->dgraph_on && m->stream && m->kt_mask == 0 && total > np;
+  uint32_t pos = 0;
+  while (pos < total && !(graph && pos >= np)) {
+    uint32_t next = 0;
+    const int rc = step(pos, &next);
     if (rc != Q3_OK) return rc;
     pos = next;
   }
+  if (pos >= total) return Q3_OK;
+  const bool same = m->dgraph && m->dg_key[0] == n_prompt && m->dg_key[1] == n_gen &&
+                    m->dg_key[2] == mode && m->dg_tab_version == m->tab_version;
+  if (!same) {
+    if (m->dgraph) (void)hipGraphExecDestroy(m->dgraph);
+    m->dgraph = nullptr;
+    Q3_HIP(hipStreamBeginCapture(m->stream, hipStreamCaptureModeRelaxed));
+    int rc = Q3_OK;
+    for (uint32_t p = pos; p < total && rc == Q3_OK;) {
+      uint32_t next = 0;
+      rc = step(p, &next);
+      p = next;
+    }
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(m->stream, &g);
+    if (rc == Q3_OK && (e != hipSuccess || !g)) rc = Q3_ERR_HIP;
+    if (rc == Q3_OK && hipGraphInstantiate(&m->dgraph, g, nullptr, nullptr, 0) != hipSuccess) {
+      m->dgraph = nullptr;
+      rc = Q3_ERR_HIP;
+    }
+    if (g) (void)hipGraphDestroy(g);
+    if (rc != Q3_OK) return rc;
+    m->dg_key[0] = n_prompt;
+    m->dg_key[1] = n_gen;
+    m->dg_key[2] = mode;
+    m->dg_tab_version = m->tab_version;
+  }
+  Q3_HIP(hipGraphLaunch(m->dgraph, m->stream));
   return Q3_OK;
 }
 
@@ -1247,6 +1293,7 @@ extern "C" int q3_model_close(q3_model *m) {
   if (m->bkeys) (void)hipFree(m->bkeys);
   if (m->bbest) (void)hipFree(m->bbest);
   if (m->opart) (void)hipFree(m->opart);
+  if (m->dgraph) (void)hipGraphExecDestroy(m->dgraph);
   for (int c = 0; c < Q3_KT_COUNT; ++c)
     for (hipEvent_t e : m->kt_ev[c]) (void)hipEventDestroy(e);
   delete m;

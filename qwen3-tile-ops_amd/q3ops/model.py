@@ -104,12 +104,14 @@ class Model:
     def set_ctrl(self, n_prompt: int, n_gen: int, mode: int) -> None:
         o = self.layout.offsets
         ctrl = np.array([n_prompt, n_gen, self.layout.max_seq, mode], np.int32)
-        self.blob[o["kCTRL"]:o["kCTRL"] + 16].copy_(torch.from_numpy(ctrl.view(np.uint8)))
+        with torch.cuda.stream(self.stream):  # ordered with the model's launches
+            self.blob[o["kCTRL"]:o["kCTRL"] + 16].copy_(torch.from_numpy(ctrl.view(np.uint8)))
 
     def set_ids(self, ids) -> None:
         o = self.layout.offsets
         a = np.ascontiguousarray(np.asarray(ids, np.int32))
-        self.blob[o["kIDS"]:o["kIDS"] + 4 * a.size].copy_(torch.from_numpy(a.view(np.uint8)))
+        with torch.cuda.stream(self.stream):
+            self.blob[o["kIDS"]:o["kIDS"] + 4 * a.size].copy_(torch.from_numpy(a.view(np.uint8)))
 
     # -- readback -------------------------------------------------------------
     def read(self, off: int, nbytes: int) -> np.ndarray:

@@ -271,3 +271,57 @@ def test_cfg3_prefill_512_generate(cuda):
     m.close()
     assert np.array_equal(got, gen), (got, gen)
     assert idx == int(np.argmax(logits)) and bits_equal(np.float32(best), logits.max())
+
+
+def test_generate_decode_graph_replays(cuda, monkeypatch):
+    """On a stream of its own, q3_generate captures its decode steps as one
+    HIP graph and replays it while CTRL and the page table stay the same.
+    Every replay, with eager work and synchronisations in between, gives the
+    reference's ids and logits; a new CTRL mode or page table is captured
+    anew; the launch-by-launch path (Q3_DECODE_GRAPH=0) agrees."""
+    lay, blob = host_blob("cfg0")
+    g = load_cfg("cfg0")
+    gl = g["logits"]
+
+    def run(m, mode):
+        m.set_ctrl(40, 2, mode)
+        m.generate()
+        m.synchronize()
+        ids = m.ids()[40:42].copy()
+        if mode == 1:
+            return ids, m.stage("logits", 1)[0].copy()
+        return ids, m.argmax()
+
+    def check_out(ids, out, mode, what):
+        assert np.array_equal(ids, g["generated"]), (what, ids, g["generated"])
+        if mode == 1:
+            assert bits_equal(out, gl), (what, describe_diff(out, gl))
+        else:
+            best, idx = out
+            assert idx == int(np.argmax(gl)) and bits_equal(np.float32(best), gl.max()), what
+
+    results = {}
+    for flag in ("1", "0"):
+        monkeypatch.setenv("Q3_DECODE_GRAPH", flag)
+        st = torch.cuda.Stream()
+        with torch.cuda.stream(st):
+            m = Model(lay, blob, stream=st)
+        for rep in range(3):
+            note(f"decode graph={flag} replay {rep}")
+            ids, out = run(m, 1)
+            check_out(ids, out, 1, f"graph={flag} mode 1 call {rep}")
+            results.setdefault((flag, 1), []).append(out)
+            # eager work on the model's stream and on another stream between replays
+            m.forward_chunk(0, 32, LM_NONE)
+            torch.randn(4096, device=cuda).sum().item()
+            m.synchronize()
+        ids, out = run(m, 0)
+        check_out(ids, out, 0, f"graph={flag} mode 0")
+        tab = np.arange(lay.max_seq // 32, dtype=np.uint16)
+        np.random.default_rng(11).shuffle(tab)
+        m.set_page_table(tab)
+        for rep in range(2):
+            ids, out = run(m, 1)
+            check_out(ids, out, 1, f"graph={flag} shuffled pages call {rep}")
+        m.close()
+    assert all(bits_equal(a, b) for a, b in zip(results[("1", 1)], results[("0", 1)]))
