@@ -72,14 +72,16 @@ def time_graph(launch, count: int, stream, replays: int = 3) -> float:
     with torch.cuda.graph(g, stream=stream):
         for i in range(count):
             launch(i)
-    g.replay()
+    with torch.cuda.stream(stream):  # replay() launches on the current stream
+        g.replay()
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(replays):
-        g.replay()
-    end.record(stream)
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for _ in range(replays):
+            g.replay()
+        end.record(stream)
     end.synchronize()
     ms = start.elapsed_time(end) / (replays * count)
     del g

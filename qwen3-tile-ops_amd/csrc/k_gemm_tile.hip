@@ -33,10 +33,13 @@
 // group g + 1 are issued, so the two run side by side instead of
 // MFMA -> dequant -> MFMA on one set of registers.
 #include <algorithm>
+#include <cstdlib>
+#include <cstring>
 #include <type_traits>
 #include <utility>
 
 #include "q3_device.h"
+#include "q3_epi.h"
 #include "q3_kernels.h"
 
 namespace q3 {
@@ -46,48 +49,6 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ v4i zero4() {
   v4i z = {0, 0, 0, 0};
   return z;
-}
-
-// f(std::integral_constant<int, 0>{}), ..., f(std::integral_constant<int, N - 1>{})
-template <class F, int... I>
-__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
-  (f(std::integral_constant<int, I>{}), ...);
-}
-template <int N, class F>
-__device__ __forceinline__ void static_for(F &&f) {
-  static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-
-
-
-// ref_qwen3.py:194-200: e = exp(-g); e = e + 1; e = 1/e; out = (g * e) * u.
-__device__ __forceinline__ float swiglu1(float g, float u, const uint64_t *tab) {
-  float e = __fmul_rn(g, -1.0f);
-  e = exp_f32_tab(e, tab);
-  e = __fadd_rn(e, 1.0f);
-  e = __fdiv_rn(1.0f, e);
-  return __fmul_rn(__fmul_rn(g, e), u);
-}
-
-// Row destination of the int8 head output (dense view or paged KV slot).
-__device__ __forceinline__ void qdest_row(const QDest &d, int m, int head, int8_t **row8, float **scale) {
-  if (d.table || d.row_pos) {
-    uint32_t t = d.pos0 + static_cast<uint32_t>(m);
-    if (d.pos_dev) t += static_cast<uint32_t>(*d.pos_dev);
-    const uint16_t *table = d.table;
-    if (d.row_pos) {
-      t = static_cast<uint32_t>(d.row_pos[m]);
-      table = d.row_tables + m * d.ld_table;
-    }
-    const uint32_t page = table[t / d.page_tokens];
-    const uint32_t slot = t % d.page_tokens;
-    *row8 = d.q8 + page * d.page_bytes + slot * d.row_bytes + head * 128;
-    *scale = reinterpret_cast<float *>(reinterpret_cast<int8_t *>(d.qs) + page * d.scale_page_bytes +
-                                       slot * d.scale_row_bytes) + head;
-  } else {
-    *row8 = d.q8 + static_cast<int64_t>(m) * d.ldq8 + head * 128;
-    *scale = d.qs + static_cast<int64_t>(m) * d.ldqs + head * d.qs_col;
-  }
 }
 
 template <int BM, int BN, int WGM, int NMAT, int STAGES, int KS>
@@ -375,7 +336,7 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(TileArgs a) {
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           float v = acc[0][mt][nt][i];
-          if constexpr (EPI == EPI_SWIGLUQ) v = swiglu1(acc[0][mt][nt][i], acc[NMAT - 1][mt][nt][i], tab);
+          if constexpr (EPI == EPI_SWIGLUQ) v = swiglu_tab(acc[0][mt][nt][i], acc[NMAT - 1][mt][nt][i], tab);
           tile[(wm * S::WM + mt * 16 + lg * 4 + i) * S::LDT + wn * S::WN + nt * 16 + lr] = v;
         }
     __syncthreads();
@@ -520,6 +481,12 @@ bool gemm_tile_supported(const TileArgs &a, int epi) {
 
 hipError_t launch_gemm_tile(const TileArgs &a, int epi, hipStream_t s) {
   if (a.M <= 0) return hipSuccess;
+  static const bool stream_ok = [] {
+    const char *e = std::getenv("Q3_PREFILL_GEMM");
+    return !(e && std::strcmp(e, "tile") == 0);
+  }();
+  if ((stream_ok || a.b_packed) && gemm_stream_supported(a, epi)) return launch_gemm_stream(a, epi, s);
+  if (a.b_packed) return hipErrorInvalidValue;  // only the stream kernel reads packed weights
   if (!gemm_tile_supported(a, epi)) return hipErrorInvalidValue;
   if (a.bs_ld) {  // per-(row, K-group) B scales: plain and residual stores only
     if (epi != EPI_STORE && epi != EPI_ADD) return hipErrorInvalidValue;

@@ -26,6 +26,7 @@
 #include <algorithm>
 
 #include "q3_device.h"
+#include "q3_epi.h"
 #include "q3_kernels.h"
 
 namespace q3 {
@@ -36,15 +37,6 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ v4i zero4() {
   v4i z = {0, 0, 0, 0};
   return z;
-}
-
-// ref_qwen3.py:194-200 (exp table staged in LDS).
-__device__ __forceinline__ float swiglu1(float g, float u, const uint64_t *tab) {
-  float e = __fmul_rn(g, -1.0f);
-  e = exp_f32_tab(e, tab);
-  e = __fadd_rn(e, 1.0f);
-  e = __fdiv_rn(1.0f, e);
-  return __fmul_rn(__fmul_rn(g, e), u);
 }
 
 // The prologue builds the int8 A operand of M rows (K = 1024*QW columns,
@@ -510,7 +502,7 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
       }
       *dst = __fadd_rn(base, out);
     } else if (sg.epi == EPI_SWIGLU)
-      *dst = swiglu1(out, out2, exptab);
+      *dst = swiglu_tab(out, out2, exptab);
     else
       *dst = out;
   }

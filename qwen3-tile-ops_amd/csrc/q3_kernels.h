@@ -146,6 +146,9 @@ struct TileArgs {
   int64_t ldas;
   const int8_t *b0, *b1;
   int64_t ldb;
+  // b0 / b1 / seg[].b in the packed layout of launch_pack_b (stream kernel
+  // only; ldb unused)
+  int b_packed;
   const float *bs0, *bs1;
   int64_t bs_stride;
   int64_t bs_ld;  // GemmArgs::bs_ld (EPI_STORE / EPI_ADD)
@@ -181,6 +184,17 @@ struct TileArgs {
 };
 bool gemm_tile_supported(const TileArgs &a, int epi);
 hipError_t launch_gemm_tile(const TileArgs &a, int epi, hipStream_t s);
+// Prefill shapes (M > 64, K = 1024..3072 in steps of 1024): the A tile in
+// LDS, the weights streamed to registers (k_gemm_stream.hip).  Epilogues
+// STORE, ADD, HEADQ, NRQ, QKV, SWIGLUQ.  launch_gemm_tile takes this path
+// for the shapes it supports unless Q3_PREFILL_GEMM=tile.
+bool gemm_stream_supported(const TileArgs &a, int epi);
+hipError_t launch_gemm_stream(const TileArgs &a, int epi, hipStream_t s);
+// Weights [N][K] (row stride ldb) in the layout the stream kernel reads with
+// one contiguous 1 KiB load per MFMA operand fragment: fragment (16-row
+// block nb, 64-byte k-slice s) at byte 1024 (nb * K / 64 + s), lane
+// l = r + 16 q of it holding row 16 nb + r, bytes 64 s + 16 q .. + 15.
+hipError_t launch_pack_b(const int8_t *b, int64_t ldb, int N, int K, int8_t *out, hipStream_t s);
 
 // ---- fused gate/up GEMM + SwiGLU + per-256-column quant -----------------
 struct GateUpArgs {

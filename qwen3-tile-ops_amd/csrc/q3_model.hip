@@ -73,6 +73,12 @@ struct q3_model {
   // (Q3_DECODE_GRAPH, default 1; 0 launches them one by one)
   bool dgraph_on = true;
   hipGraphExec_t dgraph = nullptr;
+  // prefill chunks of more than 64 rows: every layer's weights repacked at
+  // open (q3::launch_pack_b) so that the stream GEMM reads each MFMA operand
+  // fragment as one contiguous 1 KiB (Q3_PACKED_WEIGHTS=0: no copy)
+  int8_t *packed = nullptr;
+  int64_t pk_layer = 0;   // bytes per layer
+  int64_t pk_off[7] = {}; // q, k, v, o, gate, up, down within a layer
   int32_t dg_key[3] = {-1, -1, -1};
   uint64_t tab_version = 0, dg_tab_version = ~0ull;
 };
@@ -108,6 +114,7 @@ T *at(const q3_model *m, int64_t off) {
 // Per-layer views (main_big.cpp:100-136).
 struct LayerPtrs {
   const int8_t *wq, *wk, *wv, *wo, *wg, *wu, *wd;
+  const int8_t *pq, *pk, *pv, *po, *pg, *pu, *pd;  // packed copies (null without)
   const float *wqs, *wks, *wvs, *wos, *wgs, *wus, *wds;
   const float *n1, *nq, *nk, *n2;
   int8_t *kc, *vc;
@@ -127,6 +134,9 @@ LayerPtrs layer_ptrs(const q3_model *m, uint32_t L) {
   p.wg = at<const int8_t>(m, y.kLG + w);
   p.wu = at<const int8_t>(m, y.kLU + w);
   p.wd = at<const int8_t>(m, y.kLD + w);
+  const int8_t *pl = m->packed ? m->packed + static_cast<int64_t>(L) * m->pk_layer : nullptr;
+  const int8_t **pp[7] = {&p.pq, &p.pk, &p.pv, &p.po, &p.pg, &p.pu, &p.pd};
+  for (int i = 0; i < 7; ++i) *pp[i] = pl ? pl + m->pk_off[i] : nullptr;
   p.wqs = at<const float>(m, y.kLQ_SCALE + w);
   p.wks = at<const float>(m, y.kLK_SCALE + w);
   p.wvs = at<const float>(m, y.kLV_SCALE + w);
@@ -275,6 +285,31 @@ q3::GemmArgs gemm_args(int M, int N, int K, int group, const int8_t *a, const fl
   g.bs = bs;
   g.bs_stride = 1;
   return g;
+}
+
+// A residual GEMM (O, down) of a prefill chunk on the packed weights pb,
+// when the stream kernel takes it: true and *rc = its status; false when
+// the caller's row-major launch must run instead.
+bool packed_add(const q3_model *m, const q3::GemmArgs &g, const int8_t *pb, hipStream_t s, int *rc) {
+  if (!pb) return false;
+  q3::TileArgs t{};
+  t.M = g.M;
+  t.N = g.N;
+  t.K = g.K;
+  t.group = g.group;
+  t.a = g.a;
+  t.lda = g.lda;
+  t.as = g.as;
+  t.ldas = g.ldas;
+  t.b0 = pb;
+  t.b_packed = 1;
+  t.bs0 = g.bs;
+  t.bs_stride = g.bs_stride;
+  t.out = g.out;
+  t.ldo = g.ldo;
+  if (!q3::gemm_stream_supported(t, g.epi)) return false;
+  *rc = q3::launch_gemm_stream(t, g.epi, s) == hipSuccess ? Q3_OK : Q3_ERR_HIP;
+  return true;
 }
 
 q3::GemvArgs gemv_args(int M, int K, int group) {
@@ -698,6 +733,14 @@ int qkv_projections(q3_model *m, const LayerPtrs &lp, uint32_t pos, uint32_t row
     t.seg[2].bs = lp.wvs;
     set_paged(t.seg[2].qd, m, lp.vc, lp.vcs, pos);
     t.seg[2].norm = 0;
+    if (lp.pq) {  // the packed weights, when the stream kernel takes the chunk
+      q3::TileArgs tp = t;
+      tp.b_packed = 1;
+      tp.seg[0].b = lp.pq;
+      tp.seg[1].b = lp.pk;
+      tp.seg[2].b = lp.pv;
+      if (q3::gemm_stream_supported(tp, q3::EPI_QKV)) return hip_status(q3::launch_gemm_stream(tp, q3::EPI_QKV, s));
+    }
     if (q3::gemm_tile_supported(t, q3::EPI_QKV)) return hip_status(q3::launch_gemm_tile(t, q3::EPI_QKV, s));
   }
   {
@@ -832,7 +875,12 @@ int forward_chunk_impl(q3_model *m, uint32_t pos, uint32_t rows, int lm_out,
       g.epi = q3::EPI_ADD;
       g.out = xt;
       g.ldo = H;
-      Q3_HIP(q3::launch_gemm(g, s));
+      int rc = Q3_OK;
+      if (packed_add(m, g, lp.po, s, &rc)) {
+        if (rc != Q3_OK) return rc;
+      } else {
+        Q3_HIP(q3::launch_gemm(g, s));
+      }
     }
     // post-attention RMSNorm + quant
     {
@@ -861,7 +909,30 @@ int forward_chunk_impl(q3_model *m, uint32_t pos, uint32_t rows, int lm_out,
       u.ss = ss + static_cast<int64_t>(tr0) * (I / 256);
       u.ldss = I / 256;
       u.ss_col = 1;
-      Q3_HIP(q3::launch_gate_up(u, s));
+      q3::TileArgs t{};  // the packed weights, when the stream kernel takes the chunk
+      t.M = M;
+      t.N = I;
+      t.K = H;
+      t.group = 256;
+      t.a = u.a;
+      t.lda = H;
+      t.as = u.as;
+      t.ldas = H / 256;
+      t.b0 = lp.pg;
+      t.b1 = lp.pu;
+      t.b_packed = 1;
+      t.bs0 = lp.wgs;
+      t.bs1 = lp.wus;
+      t.bs_stride = 1;
+      t.s8 = u.s8;
+      t.lds8 = I;
+      t.ss = u.ss;
+      t.ldss = I / 256;
+      t.ss_col = 1;
+      if (lp.pg && q3::gemm_stream_supported(t, q3::EPI_SWIGLUQ))
+        Q3_HIP(q3::launch_gemm_stream(t, q3::EPI_SWIGLUQ, s));
+      else
+        Q3_HIP(q3::launch_gate_up(u, s));
     }
     // down projection + residual into x
     {
@@ -870,7 +941,12 @@ int forward_chunk_impl(q3_model *m, uint32_t pos, uint32_t rows, int lm_out,
       g.epi = q3::EPI_ADD;
       g.out = xt;
       g.ldo = H;
-      Q3_HIP(q3::launch_gemm(g, s));
+      int rc = Q3_OK;
+      if (packed_add(m, g, lp.pd, s, &rc)) {
+        if (rc != Q3_OK) return rc;
+      } else {
+        Q3_HIP(q3::launch_gemm(g, s));
+      }
     }
   }
 
@@ -878,6 +954,35 @@ int forward_chunk_impl(q3_model *m, uint32_t pos, uint32_t rows, int lm_out,
 }
 
 }  // namespace
+
+// The packed copy of every layer's seven weight matrices (q3::launch_pack_b
+// layout), made once on the model's stream.
+static int pack_weights(q3_model *m) {
+  const q3_layout &y = m->lay;
+  const int64_t H = y.hidden, QW = static_cast<int64_t>(y.heads) * y.head_dim;
+  const int64_t KW = static_cast<int64_t>(y.kv_heads) * y.head_dim, I = y.inter;
+  const int64_t rows[7] = {QW, KW, KW, H, I, I, H}, cols[7] = {H, H, H, QW, H, H, I};
+  int64_t off = 0;
+  for (int i = 0; i < 7; ++i) {
+    if (rows[i] % 16 || cols[i] % 64) return Q3_OK;  // shapes the stream kernel never takes
+    m->pk_off[i] = off;
+    off += (rows[i] * cols[i] + 255) & ~int64_t(255);
+  }
+  m->pk_layer = off;
+  if (hipMalloc(&m->packed, static_cast<size_t>(off) * y.layers) != hipSuccess) {
+    m->packed = nullptr;
+    return Q3_ERR_HIP;
+  }
+  for (uint32_t L = 0; L < y.layers; ++L) {
+    const int64_t w = static_cast<int64_t>(L) * y.kLAYERW_STRIDE;
+    const int64_t src[7] = {y.kLQ, y.kLK, y.kLV, y.kLO, y.kLG, y.kLU, y.kLD};
+    for (int i = 0; i < 7; ++i)
+      Q3_HIP(q3::launch_pack_b(at<const int8_t>(m, src[i] + w), cols[i], static_cast<int>(rows[i]),
+                               static_cast<int>(cols[i]), m->packed + L * off + m->pk_off[i], m->stream));
+  }
+  Q3_HIP(hipStreamSynchronize(m->stream));
+  return Q3_OK;
+}
 
 extern "C" int q3_model_open(void *blob, const q3_layout *lay, void *stream, q3_model **out) {
   if (!blob || !lay || !out) return Q3_ERR_ARG;
@@ -927,6 +1032,14 @@ extern "C" int q3_model_open(void *blob, const q3_layout *lay, void *stream, q3_
       hipMemset(m->keys, 0, sizeof(unsigned long long) * 8) != hipSuccess) {
     q3_model_close(m);
     return Q3_ERR_HIP;
+  }
+  const char *pk_env = std::getenv("Q3_PACKED_WEIGHTS");
+  if (lay->seq > 64 && !(pk_env && std::atoi(pk_env) == 0)) {
+    const int rc = pack_weights(m);
+    if (rc != Q3_OK) {
+      q3_model_close(m);
+      return rc;
+    }
   }
   *out = m;
   return Q3_OK;
@@ -1250,6 +1363,7 @@ extern "C" int q3_generate(q3_model *m) {
                     m->dg_key[2] == mode && m->dg_tab_version == m->tab_version;
   if (!same) {
     if (m->dgraph) (void)hipGraphExecDestroy(m->dgraph);
+  if (m->packed) (void)hipFree(m->packed);
     m->dgraph = nullptr;
     Q3_HIP(hipStreamBeginCapture(m->stream, hipStreamCaptureModeRelaxed));
     int rc = Q3_OK;
@@ -1294,6 +1408,7 @@ extern "C" int q3_model_close(q3_model *m) {
   if (m->bbest) (void)hipFree(m->bbest);
   if (m->opart) (void)hipFree(m->opart);
   if (m->dgraph) (void)hipGraphExecDestroy(m->dgraph);
+  if (m->packed) (void)hipFree(m->packed);
   for (int c = 0; c < Q3_KT_COUNT; ++c)
     for (hipEvent_t e : m->kt_ev[c]) (void)hipEventDestroy(e);
   delete m;

@@ -47,6 +47,7 @@ import sys
 # kernel symbol -> kernel class.  Decode classes are those of
 # q3_model_set_kernel_timing; gemv_kernel<GPW, KSTEPS, NT, NMAT, prologue,
 # partials, ...> and gemm_tile_kernel<BM, BN, WGM, NMAT, STAGES, KS, epilogue,
+# group, ...> and gemm_stream_kernel<BM, NWN, KP, NT, NMAT, D, KB, epilogue,
 # group, ...> are matched on their template arguments (epilogue numbers:
 # 1 residual add, 2 V head quant, 3 Q/K norm+RoPE+quant, 6 SwiGLU+quant,
 # 7 the three-segment Q|K|V launch).
@@ -63,6 +64,11 @@ CLASS_OF = [
     (r"gemm_tile_kernel<\d+, \d+, \d+, 1, \d+, \d+, 7,", "prefill_qkv"),
     (r"gemm_tile_kernel<\d+, \d+, \d+, 1, \d+, \d+, 1, 128", "prefill_o"),
     (r"gemm_tile_kernel<\d+, \d+, \d+, 1, \d+, \d+, 1, 256", "prefill_down"),
+    (r"gemm_stream_kernel<(\d+, ){7}6,", "prefill_gate_up"),
+    (r"gemm_stream_kernel<(\d+, ){7}7,", "prefill_qkv"),
+    (r"gemm_stream_kernel<(\d+, ){7}1, 128", "prefill_o"),
+    (r"gemm_stream_kernel<(\d+, ){7}1, 256", "prefill_down"),
+    (r"pack_b_kernel", "pack_weights"),
     (r"attention_kernel", "prefill_attention"),
     (r"rows1024_kernel", "norm_quant_rows"),
     (r"argmax_finish_kernel", "argmax_finish"),
