@@ -345,7 +345,7 @@ __global__ void __launch_bounds__(256) attention_kernel(AttnArgs a) {
 
 }  // namespace
 
-hipError_t launch_attention(const AttnArgs &a, hipStream_t s) {
+hipError_t launch_attention_walk(const AttnArgs &a, hipStream_t s) {
   if (a.rows <= 0) return hipSuccess;
   // the stage copies address whole 32-key blocks inside one page
   if (a.page_tokens % KB || a.row_bytes % 16 || a.kv_heads <= 0 || a.heads % a.kv_heads ||

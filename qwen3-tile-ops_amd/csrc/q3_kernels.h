@@ -282,6 +282,11 @@ struct AttnArgs {
   int64_t ld_opart;
 };
 hipError_t launch_attention(const AttnArgs &a, hipStream_t s);
+// the two multi-row kernels behind launch_attention: the phase-parallel one
+// (default) and the block-order walk (Q3_PREFILL_ATTN=walk)
+hipError_t launch_attn_prefill(const AttnArgs &a, hipStream_t s);
+bool attn_prefill_supported(const AttnArgs &a);
+hipError_t launch_attention_walk(const AttnArgs &a, hipStream_t s);
 
 // ---- standalone per-head norm + RoPE + quant (f32 input) -----------------
 struct NrqArgs {

@@ -69,6 +69,7 @@ CLASS_OF = [
     (r"gemm_stream_kernel<(\d+, ){7}1, 128", "prefill_o"),
     (r"gemm_stream_kernel<(\d+, ){7}1, 256", "prefill_down"),
     (r"pack_b_kernel", "pack_weights"),
+    (r"attn_prefill_kernel", "prefill_attention"),
     (r"attention_kernel", "prefill_attention"),
     (r"rows1024_kernel", "norm_quant_rows"),
     (r"argmax_finish_kernel", "argmax_finish"),

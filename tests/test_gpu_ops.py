@@ -236,6 +236,36 @@ def test_attention_paged(cuda, rows, kv_len):
     assert bits_equal(host(os_), ros), describe_diff(host(os_), ros)
 
 
+@pytest.mark.parametrize("heads,kvh,rows,kv_len,causal", [
+    (16, 8, 512, 2048, True),   # a later chunk: 1536 keys of context before the rows
+    (16, 8, 100, 1000, True),   # row 0 at position 900 (not a multiple of 16 or 32)
+    (16, 8, 48, 300, True),     # 3 query blocks: the middle one walks alone
+    (16, 8, 17, 17, True),
+    (8, 8, 64, 200, True),      # GQA group 1
+    (16, 4, 96, 96, True),      # GQA group 4
+    (16, 8, 40, 300, False),    # no mask: every row walks every key
+])
+def test_attention_prefill_shapes(cuda, heads, kvh, rows, kv_len, causal):
+    """Multi-row attention (the phase-parallel prefill kernel) over contexts
+    that span several 8-block chunks, unaligned first positions, odd query
+    block counts, other GQA groups and the unmasked form."""
+    note(f"attention prefill heads={heads}/{kvh} rows={rows} kv_len={kv_len} causal={causal}")
+    rng = np.random.default_rng(rows * 7 + kv_len + heads + kvh)
+    n_pages = (kv_len + 31) // 32 + 2
+    (k8, v8, ks, vs), (kp, vp, ksp, vsp, table) = make_pages(rng, kv_len, kvh * 128, kvh, n_pages)
+    q8 = rng.integers(-127, 128, (rows, heads * 128)).astype(np.int8)
+    qs = rng.uniform(1e-3, 5e-2, (rows, heads)).astype(F)
+    kv = ops.paged_kv(dev(kp), dev(vp), dev(ksp), dev(vsp), dev(table.view(np.int16)))
+    o8 = torch.zeros((rows, heads * 128), dtype=torch.int8, device=cuda)
+    os_ = torch.zeros((rows, heads), dtype=torch.float32, device=cuda)
+    ops.attention_heads_gqa_tokscale_paged(dev(q8), dev(qs), kv, kv_len, o8, os_, heads, kvh, 128,
+                                           causal, QK)
+    attn = oracle.attention_heads_gqa_tokscale(q8, qs, k8, ks, v8, vs, heads, kvh, 128, causal, QK)
+    ro8, ros = oracle.quant_rows_heads(attn, 128)
+    assert bits_equal(host(o8), ro8), describe_diff(host(o8), ro8)
+    assert bits_equal(host(os_), ros), describe_diff(host(os_), ros)
+
+
 @pytest.mark.parametrize("heads,kvh,kv_len", [(16, 8, 1023), (16, 8, 1025), (16, 8, 2500),
                                               (8, 8, 77), (8, 8, 1100)])
 def test_attention_decode_chunks(cuda, heads, kvh, kv_len):
