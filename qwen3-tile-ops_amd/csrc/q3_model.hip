@@ -1363,7 +1363,6 @@ extern "C" int q3_generate(q3_model *m) {
                     m->dg_key[2] == mode && m->dg_tab_version == m->tab_version;
   if (!same) {
     if (m->dgraph) (void)hipGraphExecDestroy(m->dgraph);
-  if (m->packed) (void)hipFree(m->packed);
     m->dgraph = nullptr;
     Q3_HIP(hipStreamBeginCapture(m->stream, hipStreamCaptureModeRelaxed));
     int rc = Q3_OK;

@@ -257,20 +257,34 @@ def test_cfg3_prefill_512_chunk_stages(cuda):
 
 
 def test_cfg3_prefill_512_generate(cuda):
-    """q3_generate with CTRL [512, 4, mode 0]: one 512-row prefill chunk, then
-    four greedy decode steps; ids and the fused argmax equal the oracle's."""
-    note("512-row prefill + 4 greedy tokens, 2 layers")
+    """q3_generate with CTRL [512, 4, mode 0]: one 512-row prefill chunk (on
+    the weights packed at model open), then four greedy decode steps; ids and
+    the fused argmax equal the oracle's.  Three calls on the model's own
+    stream: the first captures the decode steps as a graph, the later ones
+    replay it, and between calls the device memory is churned (large tensors
+    filled and released), so a prefill reading weights that an earlier call
+    released would show."""
+    note("512-row prefill + 4 greedy tokens, 2 layers, 3 calls")
     lay, blob = host_blob("cfg3_perf", shape=SHAPE_512, init=INIT_512)
     om = oracle_512(blob, lay)
     logits, gen, _, _ = om.generate(lay.global_views(blob)["ids"], 512, 4, record=False)
-    m = Model(lay, blob)
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        m = Model(lay, blob, stream=st)
     m.set_ctrl(512, 4, 0)
-    m.generate()
-    got = m.ids()[512:516]
-    best, idx = m.argmax()
+    for rep in range(3):
+        note(f"generate call {rep}")
+        m.generate()
+        m.synchronize()
+        got = m.ids()[512:516].copy()
+        best, idx = m.argmax()
+        assert np.array_equal(got, gen), (rep, got, gen)
+        assert idx == int(np.argmax(logits)) and bits_equal(np.float32(best), logits.max()), rep
+        junk = [torch.full((64 << 20,), -1, dtype=torch.int8, device=cuda) for _ in range(8)]
+        torch.cuda.synchronize()
+        del junk
+        torch.cuda.empty_cache()
     m.close()
-    assert np.array_equal(got, gen), (got, gen)
-    assert idx == int(np.argmax(logits)) and bits_equal(np.float32(best), logits.max())
 
 
 def test_generate_decode_graph_replays(cuda, monkeypatch):
