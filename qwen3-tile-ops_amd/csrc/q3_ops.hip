@@ -188,6 +188,13 @@ int check_paged(const q3_paged_kv *kv) {
   return Q3_OK;
 }
 
+// The per-(device, stream) workspace of the ops that need device memory
+// between two launches (the argmax keys, the SwiGLU rows of a decode-shaped
+// gate/up): allocated by the first such call on a stream, kept until the
+// process ends.  Defined with the argmax entry points below.
+constexpr int64_t kWorkspaceBytes = int64_t(8) << 19;  // 4 MiB
+unsigned long long *stream_keys(hipStream_t s);
+
 }  // namespace
 
 extern "C" {
@@ -507,7 +514,49 @@ int q3_gemm_gate_up_swiglu_quant(const q3_view *a, const q3_view *a_scale,
   u.ss = static_cast<float *>(ss->data);
   u.ldss = ss->row_bytes / 4;
   u.ss_col = ss->col_bytes / 4;
-  return hip_status(q3::launch_gate_up(u, static_cast<hipStream_t>(stream)));
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  // decode shapes: the two-matrix GEMV (SwiGLU rows in f32, on every CU)
+  // into the stream's workspace, then the per-256-column quantisation of
+  // those rows (quant.h:89-138, the same arithmetic as swiglu_quant.h:197-231)
+  if (u.M <= 16 && u.ldw == u.K && u.ws_stride == 1 && u.ss_col == 1 && q3::gemv_supported(u.M, u.K, u.group) &&
+      static_cast<int64_t>(u.M) * u.N * 4 <= kWorkspaceBytes) {
+    float *tmp = reinterpret_cast<float *>(stream_keys(s));
+    if (!tmp) return Q3_ERR_HIP;
+    q3::GemvArgs v;
+    std::memset(&v, 0, sizeof(v));
+    v.M = u.M;
+    v.K = u.K;
+    v.group = u.group;
+    v.a = u.a;
+    v.lda = u.lda;
+    v.as = u.as;
+    v.ldas = u.ldas;
+    v.pro = q3::PRO_NONE;
+    v.nseg = 1;
+    v.seg[0].n0 = 0;
+    v.seg[0].n1 = u.N;
+    v.seg[0].epi = q3::EPI_SWIGLU;
+    v.seg[0].b = u.wg;
+    v.seg[0].b2 = u.wu;
+    v.seg[0].bs = u.wgs;
+    v.seg[0].bs2 = u.wus;
+    v.seg[0].out = tmp;
+    v.seg[0].ldo = u.N;
+    Q3_TRY(hip_status(q3::launch_gemv(v, s)));
+    q3::RowArgs r{};
+    r.mode = 0;
+    r.rows = u.M;
+    r.cols = u.N;
+    r.x = tmp;
+    r.ldx = u.N;
+    r.h8 = u.s8;
+    r.ldh8 = u.lds8;
+    r.hs = u.ss;
+    r.ldhs = u.ldss;
+    r.group = 256;
+    return hip_status(q3::launch_rows(r, s));
+  }
+  return hip_status(q3::launch_gate_up(u, s));
 }
 
 }  // extern "C"
@@ -520,7 +569,7 @@ int q3_gemm_gate_up_swiglu_quant(const q3_view *a, const q3_view *a_scale,
 namespace {
 constexpr int kMaxArgmaxRows = 256;
 // 4 MiB of keys, e.g. 256 rows x 1187 lm_head blocks of 128 columns.
-constexpr int64_t kArgmaxSlots = int64_t(1) << 19;
+constexpr int64_t kArgmaxSlots = kWorkspaceBytes / 8;
 constexpr int kMaxDevices = 64;
 
 // q3_gemm_nt_group_argmax: one workspace per (device, stream), allocated by

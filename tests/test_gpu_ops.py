@@ -346,7 +346,7 @@ def test_kv_paged_epilogues(cuda):
     assert not host(kp)[mask].any() and not host(vsp)[mask].any()
 
 
-@pytest.mark.parametrize("M", [1, 11, 64, 100, 512])
+@pytest.mark.parametrize("M", [1, 11, 16, 64, 100, 512])
 def test_gate_up_swiglu_quant(cuda, M):
     rng = np.random.default_rng(50 + M)
     a, as_, wg, wgs = rand_gemm(rng, M, 1024, 3072, 256)
@@ -360,6 +360,38 @@ def test_gate_up_swiglu_quant(cuda, M):
     rs8, rss = oracle.quant_rows_heads(oracle.swiglu(g, u), 256)
     assert bits_equal(host(s8), rs8), describe_diff(host(s8), rs8)
     assert bits_equal(host(ss), rss), describe_diff(host(ss), rss)
+
+
+def test_gate_up_swiglu_quant_strided_weights_two_streams(cuda):
+    """Decode-shaped gate/up (M <= 16): weight rows with padding (the
+    per-column-block kernel) and contiguous rows on two streams at once (the
+    GEMV through each stream's own workspace) give the oracle's bytes."""
+    rng = np.random.default_rng(77)
+    M = 5
+    a, as_, wg, wgs = rand_gemm(rng, M, 1024, 3072, 256)
+    _, _, wu, wus = rand_gemm(rng, M, 1024, 3072, 256)
+    g = oracle.gemm_nt_group(a, as_, wg, wgs, 256)
+    u = oracle.gemm_nt_group(a, as_, wu, wus, 256)
+    rs8, rss = oracle.quant_rows_heads(oracle.swiglu(g, u), 256)
+    pad = lambda w: dev(np.concatenate([w, np.full((w.shape[0], 64), 99, np.int8)], axis=1))[:, :1024]
+    s8 = torch.zeros((M, 3072), dtype=torch.int8, device=cuda)
+    ss = torch.zeros((M, 12), dtype=torch.float32, device=cuda)
+    ops.gemm_gate_up_swiglu_quant(dev(a), dev(as_), pad(wg), dev(wgs), pad(wu), dev(wus), s8, ss, 256)
+    assert bits_equal(host(s8), rs8) and bits_equal(host(ss), rss)
+    outs = []
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    args = (dev(a), dev(as_), dev(wg), dev(wgs), dev(wu), dev(wus))
+    torch.cuda.synchronize()
+    for st in streams:
+        o8 = torch.zeros((M, 3072), dtype=torch.int8, device=cuda)
+        os_ = torch.zeros((M, 12), dtype=torch.float32, device=cuda)
+        with torch.cuda.stream(st):
+            for _ in range(4):
+                ops.gemm_gate_up_swiglu_quant(*args, o8, os_, 256, stream=st)
+        outs.append((o8, os_))
+    torch.cuda.synchronize()
+    for o8, os_ in outs:
+        assert bits_equal(host(o8), rs8) and bits_equal(host(os_), rss)
 
 
 def test_gate_up_guest_fixture(cuda):
