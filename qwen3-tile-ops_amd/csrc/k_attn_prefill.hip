@@ -63,22 +63,32 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v2i __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) v2i *lds_v2i_ptr;
 
-constexpr int NW = 16;       // waves; wave w owns key block w of each chunk
-constexpr int CB = NW;       // key blocks per chunk
-constexpr int QB = 16;       // query rows per item
-constexpr int KB = 32;       // keys per block (= reference block)
+constexpr int QB = 16;   // query rows per item
+constexpr int KB = 32;   // keys per block (= reference block)
 constexpr int HD = 128;
-constexpr int LDB = CB + 4;  // row stride of the per-(row, block) arrays
 
+// NI query blocks per workgroup (2: the causal pair, 1: one block, two
+// workgroups per CU); 8 waves per query block; wave w owns key block w of
+// each chunk
+template <int NI>
+struct Cfg {
+  static constexpr int NW = 8 * NI;
+  static constexpr int CB = NW;       // key blocks per chunk
+  static constexpr int LDB = CB + 4;  // row stride of the per-(row, block) arrays
+};
+
+template <int NI>
 struct Lds {
-  int8_t v[2][CB][KB * HD];   // V stages of two chunks
-  uint64_t p8[2][CB][64];     // P8 of each (item, block), in MFMA operand lane order
-  float bm[2][QB][LDB];       // block maxima [item][row][block]
-  float corr[2][QB][LDB], psum[2][QB][LDB], pmax[2][QB][LDB];
-  float cmax[2][QB][8];       // |out| maxima of each 16-dim tile
-  float sc[NW][2 * KB];       // ks | vs of each wave's block
+  static constexpr int CB = Cfg<NI>::CB, LDB = Cfg<NI>::LDB;
+  int8_t v[2][CB][KB * HD];    // V stages of two chunks
+  uint64_t p8[NI][CB][64];     // P8 of each (item, block), in MFMA operand lane order
+  float bm[NI][QB][LDB];       // block maxima [item][row][block]
+  float corr[NI][QB][LDB], psum[NI][QB][LDB], pmax[NI][QB][LDB];
+  float cmax[NI][QB][8];       // |out| maxima of each 16-dim tile
+  float sc[Cfg<NI>::NW][2 * KB];  // ks | vs of each wave's block
   uint64_t etab[32];
 };
+static_assert(sizeof(Lds<1>) <= 80 * 1024, "two single-block workgroups per CU");
 
 __device__ __forceinline__ int vswz(int key) { return (key & 3) | ((key >> 2) & 4); }
 
@@ -139,9 +149,13 @@ __device__ __forceinline__ uint32_t pack4(int b0, int b1, int b2, int b3) {
          ((static_cast<uint32_t>(b2) & 0xffu) << 16) | (static_cast<uint32_t>(b3) << 24);
 }
 
-__global__ void __launch_bounds__(NW * 64) attn_prefill_kernel(AttnArgs a) {
+template <int NI>
+__global__ void __launch_bounds__(Cfg<NI>::NW * 64, NI == 1 ? 2 : 1) attn_prefill_kernel(AttnArgs a) {
+  constexpr int CB = Cfg<NI>::CB;
   extern __shared__ __align__(16) int8_t smem[];
-  Lds &L = *reinterpret_cast<Lds *>(smem);
+  Lds<NI> &L = *reinterpret_cast<Lds<NI> *>(smem);
+  // LDS slot of item it (A = 0, B = 1; one slot when there is no A)
+  auto sl = [](int it) { return NI == 2 ? it : 0; };
 
   // lane indices are re-read at every step (below): per-lane addresses
   // derived from them are recomputed, not hoisted out of the loop into
@@ -154,15 +168,28 @@ __global__ void __launch_bounds__(NW * 64) attn_prefill_kernel(AttnArgs a) {
   // L % kv_heads, so the workgroups of one XCD share the K/V rows its L2 holds
   const int group = a.heads / a.kv_heads;
   const int L_id = blockIdx.x + gridDim.x * blockIdx.y;
-  const int kvh = L_id % a.kv_heads;
-  const int r_id = L_id / a.kv_heads;
-  const int h = kvh * group + r_id % group;
-  const int pair = r_id / group;
+  const int nqb = (a.rows + QB - 1) / QB;
+  int kvh, h, qbA, qbB;
+  if constexpr (NI == 2) {  // grid: heads x the pairs
+    kvh = L_id % a.kv_heads;
+    const int r_id = L_id / a.kv_heads;
+    h = kvh * group + r_id % group;
+    qbA = r_id / group;
+    qbB = nqb - 1 - qbA;
+  } else {  // grid: heads x nqb; workgroups L and L + heads * ceil(nqb / 2)
+            // (dispatched one round apart, so usually on one CU) take
+            // complementary query blocks qb and nqb - 1 - qb of one head
+    const int half = (nqb + 1) / 2 * a.heads;
+    const int idx = L_id < half ? L_id : L_id - half;
+    const int hs = idx % a.heads;
+    kvh = hs % a.kv_heads;
+    h = kvh * group + hs / a.kv_heads;
+    qbB = L_id < half ? idx / a.heads : nqb - 1 - idx / a.heads;
+    qbA = qbB;
+  }
   int kv_len = static_cast<int>(a.kv_len);
   if (a.kv_len_dev) kv_len += *a.kv_len_dev;
-  const int nqb = (a.rows + QB - 1) / QB;
-  const int qbA = pair, qbB = nqb - 1 - pair;
-  const bool twoA = qbB > qbA;  // item A exists (else B is the only item)
+  const bool twoA = NI == 2 && qbB > qbA;  // item A exists (else B is the only item)
   const Item IA = make_item(a, qbA, kv_len);
   const Item IB = make_item(a, twoA ? qbB : qbA, kv_len);
   const int nA = twoA ? IA.nblk : 0;
@@ -238,7 +265,7 @@ __global__ void __launch_bounds__(NW * 64) attn_prefill_kernel(AttnArgs a) {
   };
   load_q(0);
   // phase-4 role: item it4, dims 16 dt..16 dt + 15
-  const int it4 = wave >> 3, dt = wave & 7;
+  const int it4 = NI == 2 ? wave >> 3 : 1, dt = wave & 7;
   // transposing-read address of this lane inside a V stage, for dims 16 dt..+15
   int v_tr_off;
   {
@@ -261,16 +288,16 @@ __global__ void __launch_bounds__(NW * 64) attn_prefill_kernel(AttnArgs a) {
       const int nbp = nb_of(it4, gp);
       const int8_t *vbase = &L.v[gp & 1][0][0];
       for (int b0 = 0; b0 < nbp; b0 += 4) {
-        const float4 c4 = *reinterpret_cast<const float4 *>(&L.corr[it4][lc][b0]);
-        const float4 p4 = *reinterpret_cast<const float4 *>(&L.pmax[it4][lc][b0]);
-        const float4 s4 = *reinterpret_cast<const float4 *>(&L.psum[it4][lc][b0]);
+        const float4 c4 = *reinterpret_cast<const float4 *>(&L.corr[sl(it4)][lc][b0]);
+        const float4 p4 = *reinterpret_cast<const float4 *>(&L.pmax[sl(it4)][lc][b0]);
+        const float4 s4 = *reinterpret_cast<const float4 *>(&L.psum[sl(it4)][lc][b0]);
         const float crv[4] = {c4.x, c4.y, c4.z, c4.w};
         const float pmv[4] = {p4.x, p4.y, p4.z, p4.w};
         const float psv[4] = {s4.x, s4.y, s4.z, s4.w};
         v4i c[4];
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-          const long pb = static_cast<long>(L.p8[it4][b0 + b][lane]);
+          const long pb = static_cast<long>(L.p8[sl(it4)][b0 + b][lane]);
           const v2i vt = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
               reinterpret_cast<lds_v2i_ptr>(to_lds(vbase + (b0 + b) * (KB * HD) + v_tr_off)));
           long va;
@@ -306,7 +333,7 @@ __global__ void __launch_bounds__(NW * 64) attn_prefill_kernel(AttnArgs a) {
         mx = fmaxf(__uint_as_float(pr.a), __uint_as_float(pr.b));
         pr = lane_pair32(__float_as_uint(mx));
         mx = fmaxf(__uint_as_float(pr.a), __uint_as_float(pr.b));
-        if (lg == 0) L.cmax[it4][lc][dt] = mx;
+        if (lg == 0) L.cmax[sl(it4)][lc][dt] = mx;
       }
     }
 
@@ -349,7 +376,7 @@ __global__ void __launch_bounds__(NW * 64) attn_prefill_kernel(AttnArgs a) {
           bmax = fmaxf(__uint_as_float(pr.a), __uint_as_float(pr.b));
           pr = lane_pair32(__float_as_uint(bmax));
           bmax = fmaxf(__uint_as_float(pr.a), __uint_as_float(pr.b));
-          if (lg == 0) L.bm[it][lc][wave] = bmax;
+          if (lg == 0) L.bm[sl(it)][lc][wave] = bmax;
         }
       }
     }
@@ -358,8 +385,8 @@ __global__ void __launch_bounds__(NW * 64) attn_prefill_kernel(AttnArgs a) {
     // ---- int8 store of item it4 if it ended with chunk g - 1 ----
     if (ended) {
       const Item &E = it4 ? IB : IA;
-      const float4 c0 = *reinterpret_cast<const float4 *>(&L.cmax[it4][lc][0]);
-      const float4 c1 = *reinterpret_cast<const float4 *>(&L.cmax[it4][lc][4]);
+      const float4 c0 = *reinterpret_cast<const float4 *>(&L.cmax[sl(it4)][lc][0]);
+      const float4 c1 = *reinterpret_cast<const float4 *>(&L.cmax[sl(it4)][lc][4]);
       const float mx = fmaxf(fmaxf(fmaxf(c0.x, c0.y), fmaxf(c0.z, c0.w)), fmaxf(fmaxf(c1.x, c1.y), fmaxf(c1.z, c1.w)));
       const float scale = __fmul_rn(mx, inv127());
       const double y = __ddiv_rn(1.0, static_cast<double>(scale));
@@ -391,7 +418,7 @@ __global__ void __launch_bounds__(NW * 64) attn_prefill_kernel(AttnArgs a) {
       const int nb = it ? nbB : nbA;
       float m = g == 0 ? -3.402823466e38f : m_run[it];
       const bool carry = (it ? nB : nA) > (g + 1) * CB;
-      const float *bmr = L.bm[it][lc];
+      const float *bmr = L.bm[sl(it)][lc];
 #pragma unroll
       for (int b = 0; b < CB; ++b)
         if (b < min(wave, nb)) m = (m > bmr[b]) ? m : bmr[b];
@@ -473,11 +500,11 @@ __global__ void __launch_bounds__(NW * 64) attn_prefill_kernel(AttnArgs a) {
               w8[kt] = pack4(quant_rcp_pos(p[kt][0], y), quant_rcp_pos(p[kt][1], y), quant_rcp_pos(p[kt][2], y),
                              quant_rcp_pos(p[kt][3], y));
           }
-          L.p8[it][wave][lane] = (static_cast<uint64_t>(w8[1]) << 32) | w8[0];
+          L.p8[sl(it)][wave][lane] = (static_cast<uint64_t>(w8[1]) << 32) | w8[0];
           if (lg == 0) {
-            L.corr[it][lc][wave] = corr;
-            L.psum[it][lc][wave] = psum;
-            L.pmax[it][lc][wave] = pmax;
+            L.corr[sl(it)][lc][wave] = corr;
+            L.psum[sl(it)][lc][wave] = psum;
+            L.pmax[sl(it)][lc][wave] = pmax;
           }
         }
         __builtin_amdgcn_sched_barrier(0);  // one unit at a time: bounds the live exp chains
@@ -506,16 +533,29 @@ bool attn_prefill_supported(const AttnArgs &a) {
 hipError_t launch_attn_prefill(const AttnArgs &a, hipStream_t s) {
   if (a.rows <= 0) return hipSuccess;
   if (!attn_prefill_supported(a)) return hipErrorInvalidValue;
-  static bool attr_set = false;  // more than 64 KiB of dynamic LDS must be allowed once
-  if (!attr_set) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&attn_prefill_kernel),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, sizeof(Lds));
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  static const bool pair = [] {
+    const char *e = std::getenv("Q3_PREFILL_ATTN");
+    return e && std::strcmp(e, "pair") == 0;
+  }();
+  static bool attr_set[2] = {false, false};  // more than 64 KiB of dynamic LDS must be allowed once
   const int nqb = (a.rows + QB - 1) / QB;
-  const dim3 grid(a.heads, (nqb + 1) / 2);
-  Q3_LAUNCH(attn_prefill_kernel, grid, dim3(NW * 64), sizeof(Lds), s, a);
+  if (pair) {
+    if (!attr_set[1]) {
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&attn_prefill_kernel<2>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, sizeof(Lds<2>));
+      if (e != hipSuccess) return e;
+      attr_set[1] = true;
+    }
+    Q3_LAUNCH(attn_prefill_kernel<2>, dim3(a.heads, (nqb + 1) / 2), dim3(Cfg<2>::NW * 64), sizeof(Lds<2>), s, a);
+  } else {
+    if (!attr_set[0]) {
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&attn_prefill_kernel<1>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, sizeof(Lds<1>));
+      if (e != hipSuccess) return e;
+      attr_set[0] = true;
+    }
+    Q3_LAUNCH(attn_prefill_kernel<1>, dim3(a.heads, nqb), dim3(Cfg<1>::NW * 64), sizeof(Lds<1>), s, a);
+  }
   return hipGetLastError();
 }
 
