@@ -14,7 +14,8 @@
 //   res  = res * corr + f32(P8 . V_j) * pmax
 // and ends with out = res * (1/den), quantised per head to int8.  Only the
 // den/res updates depend on the previous block; the running maximum is a
-// prefix max of the block maxima.  So per chunk of up to CB = 16 blocks:
+// prefix max of the block maxima.  So per chunk of up to CB blocks (8 per
+// query block of the workgroup):
 //   phase 1 (one wave per block)    S_j, s, block maximum bm_j
 //   phase 2 (every lane, tiny)      nmm_j = max(nmm_{j-1}, bm_j), in block order
 //   phase 3 (one wave per block)    corr_j, P, psum_j, pv, pmax_j, P8_j
@@ -23,17 +24,19 @@
 // with the reference's rounding points, so the result equals the one-block
 // walk bit for bit.  Chunks carry (maximum, den, res) the way blocks do.
 //
-// Work: a workgroup owns one query head and two 16-row query blocks, A = qb
-// and B = nqb - 1 - qb, so that under the causal mask every workgroup has
-// about the same number of (block, query block) units.  Both walk key
-// blocks from 0 and A's blocks are a prefix of B's, so each key block is
+// Work: 8 waves per 16-row query block of one head.  The default workgroup
+// holds one query block (74 KiB of LDS, two workgroups per CU) and the grid
+// is ordered so that the two workgroups a CU usually receives, L and
+// L + heads * ceil(nqb / 2), take the causally complementary blocks qb and
+// nqb - 1 - qb.  The paired form (NI = 2, 16 waves) walks both blocks of a
+// pair at once: A's key blocks are a prefix of B's, so each K/V block is
 // copied once and serves both (two 16-column MFMA tiles) while A needs it.
-// 16 waves: wave w owns block w of a chunk in phases 1 and 3 and, in phase 4,
-// item w / 8 and dims 16 (w % 8)..+15.  Step g runs phase 4 of chunk g - 1
-// and phase 1 of chunk g, barrier, phases 2-3 of chunk g (and the int8 store
-// of an item whose last chunk was g - 1), barrier.  Every wave copies its
-// own block of the next chunk: V with global_load_lds into the other half of
-// a two-chunk LDS ring, the K operand rows straight into registers, ks | vs
+// Wave w owns block w of a chunk in phases 1 and 3 and, in phase 4, 16 output
+// dimensions (16 (w % 8)..+15) of item w / 8.  Step g runs phase 4 of chunk
+// g - 1 and phase 1 of chunk g, barrier, phases 2-3 of chunk g (and the int8
+// store of an item whose last chunk was g - 1), barrier.  Every wave copies
+// its own block of the next chunk: V with global_load_lds into the other half
+// of a two-chunk LDS ring, the K operand rows straight into registers, ks | vs
 // with global_load_lds into a per-wave slot.
 //
 // Layouts (lane = lc + 16 lg):
