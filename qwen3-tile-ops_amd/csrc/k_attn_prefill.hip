@@ -125,22 +125,8 @@ __device__ __forceinline__ Item make_item(const AttnArgs &a, int qb, int kv_len)
   return it;
 }
 
-// quant(x, scale) = sat127(rne(RN(x / scale))) (ref_qwen3.py:69-76) with
-// y = RN64(1 / scale): RN32(x * y in f64) = RN32(x / scale), since a quotient
-// of two f32 is never an f32 rounding midpoint and stays at least 2^-50
-// (relative) away from every midpoint, while x * y is within 2^-52 of
-// x / scale.  Quotients where the f32 rounding is not the normal one
-// (subnormal: rne gives 0 either way; overflow: both saturate) and scale = 0
-// (y = inf: 0 * inf = NaN -> 0, x * inf = +-inf -> +-127) give the same int8
-// as the division.
-__device__ __forceinline__ int quant_rcp(float x, double y) {
-  const float q = __double2float_rn(__dmul_rn(static_cast<double>(x), y));
-  float r = (q != q) ? 0.0f : rintf(q);
-  r = fminf(127.0f, fmaxf(-127.0f, r));
-  return static_cast<int>(r);
-}
-
-// Same for x >= 0 (P * vs): the NaN of 0 * inf goes to +0 through the max.
+// quant_rcp (q3_device.h) for x >= 0 (P * vs): the NaN of 0 * inf goes to
+// +0 through the max.
 __device__ __forceinline__ int quant_rcp_pos(float x, double y) {
   float q = __double2float_rn(__dmul_rn(static_cast<double>(x), y));
   q = fmaxf(q, 0.0f);
@@ -392,7 +378,7 @@ __global__ void __launch_bounds__(Cfg<NI>::NW * 64, NI == 1 ? 2 : 1) attn_prefil
       const float4 c1 = *reinterpret_cast<const float4 *>(&L.cmax[sl(it4)][lc][4]);
       const float mx = fmaxf(fmaxf(fmaxf(c0.x, c0.y), fmaxf(c0.z, c0.w)), fmaxf(fmaxf(c1.x, c1.y), fmaxf(c1.z, c1.w)));
       const float scale = __fmul_rn(mx, inv127());
-      const double y = __ddiv_rn(1.0, static_cast<double>(scale));
+      const double y = rcp64(scale);
       if (lc < E.nr) {
         const int64_t row = E.qi + lc;
         const int col = h * HD + 16 * dt + 4 * lg;
@@ -484,7 +470,7 @@ __global__ void __launch_bounds__(Cfg<NI>::NW * 64, NI == 1 ? 2 : 1) attn_prefil
           pr = lane_pair32(__float_as_uint(pmx));
           pmx = fmaxf(__uint_as_float(pr.a), __uint_as_float(pr.b));
           const float pmax = __fmul_rn(pmx, inv127());
-          const double y = __ddiv_rn(1.0, static_cast<double>(pmax));
+          const double y = rcp64(pmax);
           uint32_t w8[2];
           if (__builtin_amdgcn_ballot_w64(!(pmax >= 1.17549435e-38f)) == 0) {
             // every row's pmax is normal: x / pmax <= 127 * (1 + 2^-23) for

@@ -114,15 +114,16 @@ __global__ void __launch_bounds__(NWN * KP * 64) gemm_stream_kernel(TileArgs a) 
   const float *nw = a.nw;
   bool do_norm = EPI == EPI_NRQ;
   if constexpr (EPI == EPI_QKV) {
-    int si = 0;
-    for (int i = 1; i < a.nseg; ++i)
-      if (n0 >= a.seg[i].n0) si = i;
-    B0 = a.seg[si].b;
-    BS0 = a.seg[si].bs;
-    nb = n0 - a.seg[si].n0;
-    qd = a.seg[si].qd;
-    nw = a.seg[si].nw;
-    do_norm = a.seg[si].norm != 0;
+    // every segment's fields are kernel arguments at fixed offsets: select
+    // among them rather than index, so no argument load waits on another
+    const int si = (a.nseg > 1 && n0 >= a.seg[1].n0) + (a.nseg > 2 && n0 >= a.seg[2].n0);
+    const auto &s0g = a.seg[0], &s1g = a.seg[1], &s2g = a.seg[2];
+    B0 = si == 2 ? s2g.b : si == 1 ? s1g.b : s0g.b;
+    BS0 = si == 2 ? s2g.bs : si == 1 ? s1g.bs : s0g.bs;
+    nb = n0 - (si == 2 ? s2g.n0 : si == 1 ? s1g.n0 : s0g.n0);
+    qd = si == 2 ? s2g.qd : si == 1 ? s1g.qd : s0g.qd;
+    nw = si == 2 ? s2g.nw : si == 1 ? s1g.nw : s0g.nw;
+    do_norm = (si == 2 ? s2g.norm : si == 1 ? s1g.norm : s0g.norm) != 0;
   }
   // LDS: exp table | A scales [BM][NG] | B scales [BN][NG] (BSG) | A tile [BM][K];
   // after the main loop the f32 epilogue tile overlays everything past the table
@@ -131,6 +132,56 @@ __global__ void __launch_bounds__(NWN * KP * 64) gemm_stream_kernel(TileArgs a) 
   float *bs_lds = as_lds + BM * NG;
   int8_t *a_lds = reinterpret_cast<int8_t *>(bs_lds + (BSG ? S::BN * NG : 0));
   float *tile = as_lds;
+
+  // 0. the epilogue's global operands first: issued before every copy and
+  //    weight load, they complete first, so the main loop's vmcnt counts are
+  //    unchanged and their latency hides behind the weight stream.  EPI_ADD:
+  //    the residual elements of the lane (last K partition; rows past M read
+  //    row M - 1 and store nothing).  Head epilogues: gains, cos/sin rows and
+  //    page ids of the wave's rows (rows past M: row M - 1's).
+  float xr[MT][4][NT];
+  if constexpr (EPI == EPI_ADD) {
+    if (kp == KP - 1) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = min(m0 + mt * 16 + lg * 4 + i, M - 1);
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt)
+            xr[mt][i][nt] = a.out[static_cast<int64_t>(m) * a.ldo + n0 + wn * S::WN + nt * 16 + lr];
+        }
+    }
+  }
+  constexpr bool HEADS = EPI == EPI_HEADQ || EPI == EPI_NRQ || EPI == EPI_QKV;
+  constexpr int RPW = (BM + NW - 1) / NW;  // head epilogue rows per wave
+  // loads that depend on another global load (device-side positions, per-row
+  // tables) wait for the epilogue; only independent ones are issued here
+  const bool pre_cs = do_norm && !a.cs_row_pos && !a.cs_row_dev;
+  const bool pre_pg = qd.table && !qd.pos_dev && !qd.row_pos;
+  float hw0 = 0.0f, hw1 = 0.0f, hcr[RPW], hsr[RPW];
+  // pre_pg: lane q < RPW holds the page id of the wave's row q (a per-lane
+  // value, so nothing waits for it before the epilogue reads it)
+  uint32_t hpg = 0;
+  if constexpr (HEADS) {
+    if (do_norm) {
+      hw0 = nw[static_cast<int64_t>(lane) * a.nw_stride];
+      hw1 = nw[static_cast<int64_t>(lane + 64) * a.nw_stride];
+    }
+#pragma unroll
+    for (int q = 0; q < RPW; ++q) {
+      const int mm = min(m0 + min(wave + NW * q, BM - 1), M - 1);
+      hcr[q] = hsr[q] = 0.0f;
+      if (pre_cs) {
+        hcr[q] = a.cos_t[static_cast<int64_t>(mm) * a.ld_cs + lane];
+        hsr[q] = a.sin_t[static_cast<int64_t>(mm) * a.ld_cs + lane];
+      }
+    }
+    if (pre_pg && lane < RPW) {
+      const int mm = min(m0 + min(wave + NW * lane, BM - 1), M - 1);
+      hpg = qd.table[(qd.pos0 + static_cast<uint32_t>(mm)) / qd.page_tokens];
+    }
+  }
 
   // 1. scales and the A tile -> LDS.  Instruction j of the A copy fills LDS
   //    bytes [1024 j, 1024 j + 1024) of the tile: row r = j / KB, chunks
@@ -343,20 +394,6 @@ __global__ void __launch_bounds__(NWN * KP * 64) gemm_stream_kernel(TileArgs a) 
   // 4. epilogues
   if constexpr (EPI == EPI_STORE || EPI == EPI_ADD) {
     if (kp != KP - 1) return;  // the last K partition holds the sums
-    // EPI_ADD: every residual element of the lane is loaded before the first
-    // store; rows past M read row M - 1 and store nothing
-    float xr[MT][4][NT];
-    if constexpr (EPI == EPI_ADD) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int m = min(m0 + mt * 16 + lg * 4 + i, M - 1);
-#pragma unroll
-          for (int nt = 0; nt < NT; ++nt)
-            xr[mt][i][nt] = a.out[static_cast<int64_t>(m) * a.ldo + n0 + wn * S::WN + nt * 16 + lr];
-        }
-    }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -387,47 +424,40 @@ __global__ void __launch_bounds__(NWN * KP * 64) gemm_stream_kernel(TileArgs a) 
         }
     __syncthreads();
     if constexpr (EPI == EPI_HEADQ || EPI == EPI_NRQ || EPI == EPI_QKV) {
-      // group_gemm.h:173-193 / norm_rope_quant.h:17-86 per (row, head): each
-      // wave's rows' operands (gains, cos/sin rows, destination slots) are
-      // loaded together first, then the rows are computed; rows past M load
-      // row M - 1's operands and store nothing
+      // group_gemm.h:173-193 / norm_rope_quant.h:17-86 per (row, head), on
+      // the operands loaded at the start (step 0) where they were independent
+      // of other loads; rows past M store nothing
       static_assert(S::BN == 128, "one head (128 columns) per tile");
-      constexpr int RPW = (BM + NW - 1) / NW;
-      float w0 = 0.0f, w1 = 0.0f, cr[RPW], sr[RPW];
-      int8_t *row8[RPW];
-      float *sp[RPW];
-      int64_t cs_off = 0;
-      if (do_norm) {
-        w0 = nw[static_cast<int64_t>(lane) * a.nw_stride];
-        w1 = nw[static_cast<int64_t>(lane + 64) * a.nw_stride];
-        if (a.cs_row_dev) cs_off = *a.cs_row_dev;
-      }
-#pragma unroll
-      for (int q = 0; q < RPW; ++q) {
-        const int mm = min(m0 + min(wave + NW * q, BM - 1), M - 1);
-        cr[q] = sr[q] = 0.0f;
-        if (do_norm) {
-          const int64_t crow = a.cs_row_pos ? static_cast<int64_t>(a.cs_row_pos[mm]) : mm + cs_off;
-          cr[q] = a.cos_t[crow * a.ld_cs + lane];
-          sr[q] = a.sin_t[crow * a.ld_cs + lane];
-        }
-        qdest_row(qd, mm, nb / 128, &row8[q], &sp[q]);
-      }
 #pragma unroll
       for (int q = 0; q < RPW; ++q) {
         const int rr = min(wave + NW * q, BM - 1);
         const bool store = wave + NW * q < BM && m0 + rr < M;
+        const int mm = min(m0 + rr, M - 1);
+        int8_t *row8;
+        float *sp;
+        if (pre_pg)
+          qdest_slot(qd, __builtin_amdgcn_readlane(hpg, q), qd.pos0 + static_cast<uint32_t>(mm), nb / 128, &row8,
+                     &sp);
+        else
+          qdest_row(qd, mm, nb / 128, &row8, &sp);
+        if (do_norm && !pre_cs) {
+          const int64_t crow = a.cs_row_pos ? static_cast<int64_t>(a.cs_row_pos[mm])
+                                            : mm + static_cast<int64_t>(a.cs_row_dev ? *a.cs_row_dev : 0);
+          hcr[q] = a.cos_t[crow * a.ld_cs + lane];
+          hsr[q] = a.sin_t[crow * a.ld_cs + lane];
+        }
         float t0 = tile[rr * S::LDT + lane];
         float t1 = tile[rr * S::LDT + lane + 64];
-        if (do_norm) head_norm_rope_regs(t0, t1, w0, w1, cr[q], sr[q], a.inv_hd, true);
+        if (do_norm) head_norm_rope_regs(t0, t1, hw0, hw1, hcr[q], hsr[q], a.inv_hd, true);
         const float mx = max64(fmaxf(fabsf(t0), fabsf(t1)));
         const float scale = __fmul_rn(mx, inv127());
-        const int8_t q0 = static_cast<int8_t>(quant1(t0, scale));
-        const int8_t q1 = static_cast<int8_t>(quant1(t1, scale));
+        const double y = rcp64(scale);
+        const int8_t q0 = static_cast<int8_t>(quant_rcp(t0, y));
+        const int8_t q1 = static_cast<int8_t>(quant_rcp(t1, y));
         if (store) {
-          row8[q][lane] = q0;
-          row8[q][lane + 64] = q1;
-          if (lane == 0) *sp[q] = scale;
+          row8[lane] = q0;
+          row8[lane + 64] = q1;
+          if (lane == 0) *sp = scale;
         }
       }
     } else if constexpr (EPI == EPI_SWIGLUQ) {
@@ -446,9 +476,10 @@ __global__ void __launch_bounds__(NWN * KP * 64) gemm_stream_kernel(TileArgs a) 
           for (int j = 0; j < 4; ++j) mx = fmaxf(mx, fabsf(v[j]));
           mx = max64(mx);
           const float scale = __fmul_rn(mx, inv127());
+          const double y = rcp64(scale);
           int8_t *dst = a.s8 + static_cast<int64_t>(m) * a.lds8 + n0 + q * 256;
 #pragma unroll
-          for (int j = 0; j < 4; ++j) dst[lane + 64 * j] = static_cast<int8_t>(quant1(v[j], scale));
+          for (int j = 0; j < 4; ++j) dst[lane + 64 * j] = static_cast<int8_t>(quant_rcp(v[j], y));
           if (lane == 0) a.ss[static_cast<int64_t>(m) * a.ldss + ((n0 + q * 256) / 256) * a.ss_col] = scale;
         }
       }

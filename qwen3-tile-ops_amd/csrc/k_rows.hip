@@ -124,6 +124,13 @@ __global__ void __launch_bounds__(256) rows1024_kernel(RowArgs a) {
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int c0 = 4 * t;
+  // the gains do not depend on the row: issued first, their latency overlaps
+  // the row's load and the sum of squares
+  float w[4];
+  if (a.mode != 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = a.w[static_cast<int64_t>(c0 + i) * a.w_stride];
+  }
   float v[4];
   if (a.mode == 2) {
     int64_t base = 0;
@@ -163,7 +170,7 @@ __global__ void __launch_bounds__(256) rows1024_kernel(RowArgs a) {
     const float rinv = rms_factor(ss, a.inv);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      v[i] = __fmul_rn(__fmul_rn(v[i], rinv), a.w[static_cast<int64_t>(c0 + i) * a.w_stride]);
+      v[i] = __fmul_rn(__fmul_rn(v[i], rinv), w[i]);
     if (a.h)
       *reinterpret_cast<float4 *>(a.h + static_cast<int64_t>(row) * a.ldh + c0) =
           make_float4(v[0], v[1], v[2], v[3]);
@@ -172,11 +179,12 @@ __global__ void __launch_bounds__(256) rows1024_kernel(RowArgs a) {
   float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
   m = max64(m);
   const float scale = __fmul_rn(m, inv127());
+  const double y = rcp64(scale);
   char4 q;
-  q.x = static_cast<signed char>(quant1(v[0], scale));
-  q.y = static_cast<signed char>(quant1(v[1], scale));
-  q.z = static_cast<signed char>(quant1(v[2], scale));
-  q.w = static_cast<signed char>(quant1(v[3], scale));
+  q.x = static_cast<signed char>(quant_rcp(v[0], y));
+  q.y = static_cast<signed char>(quant_rcp(v[1], y));
+  q.z = static_cast<signed char>(quant_rcp(v[2], y));
+  q.w = static_cast<signed char>(quant_rcp(v[3], y));
   *reinterpret_cast<char4 *>(a.h8 + static_cast<int64_t>(row) * a.ldh8 + c0) = q;
   if (lane == 0) a.hs[static_cast<int64_t>(row) * a.ldhs + (t >> 6)] = scale;
 }

@@ -198,6 +198,22 @@ __device__ __forceinline__ int quant1(float x, float scale) {
   return static_cast<int>(r);
 }
 
+// quant1(x, scale) with y = rcp64(scale) = RN64(1 / scale), one f64 multiply
+// per element instead of an f32 division: RN32(x * y) = RN32(x / scale),
+// since a quotient of two f32 is never an f32 rounding midpoint and stays at
+// least 2^-50 (relative) away from every midpoint, while x * y is within
+// 2^-52 of x / scale.  Quotients where the f32 rounding is not the normal
+// one (subnormal: rne gives 0 either way; overflow: both saturate) and
+// scale = 0 (y = inf: 0 * inf = NaN -> 0, x * inf = +-inf -> +-127) give the
+// same int8 as the division.
+__device__ __forceinline__ double rcp64(float scale) { return __ddiv_rn(1.0, static_cast<double>(scale)); }
+__device__ __forceinline__ int quant_rcp(float x, double y) {
+  const float q = __double2float_rn(__dmul_rn(static_cast<double>(x), y));
+  float r = (q != q) ? 0.0f : rintf(q);
+  r = fminf(127.0f, fmaxf(-127.0f, r));
+  return static_cast<int>(r);
+}
+
 // ---- lane exchanges in VALU (no LDS round trip) -----------------------
 // lane_xor<M>(x): lane i receives x of lane i ^ M.  M = 1, 2: DPP quad_perm;
 // M = 4: quad_perm [3,2,1,0] then row_half_mirror (i -> (i ^ 3) ^ 7);

@@ -21,6 +21,16 @@ __device__ __forceinline__ float swiglu_tab(float g, float u, const uint64_t *ta
   return __fmul_rn(__fmul_rn(g, e), u);
 }
 
+// Slot pointers of token position t in page `page` of a paged K/V pool,
+// head `head`.
+__device__ __forceinline__ void qdest_slot(const QDest &d, uint32_t page, uint32_t t, int head, int8_t **row8,
+                                           float **scale) {
+  const uint32_t slot = t % d.page_tokens;
+  *row8 = d.q8 + page * d.page_bytes + slot * d.row_bytes + head * 128;
+  *scale = reinterpret_cast<float *>(reinterpret_cast<int8_t *>(d.qs) + page * d.scale_page_bytes +
+                                     slot * d.scale_row_bytes) + head;
+}
+
 // Row destination of the int8 head output of row m, head `head`: a dense
 // [rows][heads * 128] view, or the page slot of token pos0 + m (or
 // row_pos[m] through that row's own table) of a paged K/V pool.
@@ -33,11 +43,7 @@ __device__ __forceinline__ void qdest_row(const QDest &d, int m, int head, int8_
       t = static_cast<uint32_t>(d.row_pos[m]);
       table = d.row_tables + m * d.ld_table;
     }
-    const uint32_t page = table[t / d.page_tokens];
-    const uint32_t slot = t % d.page_tokens;
-    *row8 = d.q8 + page * d.page_bytes + slot * d.row_bytes + head * 128;
-    *scale = reinterpret_cast<float *>(reinterpret_cast<int8_t *>(d.qs) + page * d.scale_page_bytes +
-                                       slot * d.scale_row_bytes) + head;
+    qdest_slot(d, table[t / d.page_tokens], t, head, row8, scale);
   } else {
     *row8 = d.q8 + static_cast<int64_t>(m) * d.ldq8 + head * 128;
     *scale = d.qs + static_cast<int64_t>(m) * d.ldqs + head * d.qs_col;
