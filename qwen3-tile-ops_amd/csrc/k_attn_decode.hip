@@ -337,8 +337,13 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
   const int pos0 = static_cast<int>(kv_len) - 1;
   const int kv_end = static_cast<int>(kv_len);
   const int nblocks = (kv_end + 31) / 32;
-  const int half = lane & 1;   // phase 1: lane pair (2c, 2c+1) on key c,
-  const int kc = lane >> 1;    //   lane parity picks dims [0,64) / [64,128)
+  // phase 1: load e of a block reads keys 8e .. 8e + 7 whole, lane l bytes
+  // kb16 .. kb16 + 15 of key 8e + kg (one load instruction covers 8 full
+  // 128-byte rows rather than 32 half rows); after the reduction lanes
+  // 2m, 2m + 1 hold the score of key kcl
+  const int kg = lane >> 3;
+  const int kb16 = 16 * (lane & 7);
+  const int kcl = 8 * ((lane >> 1) & 3) + kg;
   const int d0 = 4 * (lane & 31);   // phase 3: 4 dims per lane,
   const int kh = (lane >> 5) * 16;  //   16 keys per half-wave
 
@@ -347,7 +352,7 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
   float res = 0.0f, den = 0.0f;
   // the running max of each head across chunks, from -FLT_MAX (attention_gqa.h:418)
   float run0 = -3.402823466e38f, run1 = -3.402823466e38f;
-  int qv[QPW][16];
+  int qv[QPW][4];
   float qscale[QPW];
 
   // The exp table into LDS from immediates (no load to wait for; first
@@ -439,17 +444,15 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
                           slot0 * h.scale_row_bytes;
       const int8_t *vsb = reinterpret_cast<const int8_t *>(h.vs) + page * h.scale_page_bytes +
                           slot0 * h.scale_row_bytes;
-      const int kr = min(kc, last);
-      const int4 *kp = reinterpret_cast<const int4 *>(kb + kr * h.row_bytes + half * 64);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int4 v = kp[e];
+        const int4 v = *reinterpret_cast<const int4 *>(kb + min(8 * e + kg, last) * h.row_bytes + kb16);
         kw[i][4 * e] = v.x;
         kw[i][4 * e + 1] = v.y;
         kw[i][4 * e + 2] = v.z;
         kw[i][4 * e + 3] = v.w;
       }
-      kscale[i] = reinterpret_cast<const float *>(ksb + kr * h.scale_row_bytes)[kvh];
+      kscale[i] = reinterpret_cast<const float *>(ksb + min(kcl, last) * h.scale_row_bytes)[kvh];
 #pragma unroll
       for (int cc = 0; cc < 16; ++cc)
         vw[i][cc] = *reinterpret_cast<const int *>(vb + min(kh + cc, last) * h.row_bytes + d0);
@@ -478,9 +481,9 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
       __syncthreads();
 #pragma unroll
       for (int h = 0; h < QPW; ++h) {
-        const int *qp = reinterpret_cast<const int *>(sm.q8[h] + half * 64);
+        const int *qp = reinterpret_cast<const int *>(sm.q8[h] + kb16);
 #pragma unroll
-        for (int e = 0; e < 16; ++e) qv[h][e] = qp[e];
+        for (int e = 0; e < 4; ++e) qv[h][e] = qp[e];
         qscale[h] = sm.qs[h];
       }
     }
@@ -491,12 +494,14 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
       for (int i = 0; i < BPW; ++i) {
         const int j = (b0 + wave + NW * i) * 32;
         if (wave + NW * i >= nb) continue;
-        if (j + kc == pos0) {
-          const int *kn = reinterpret_cast<const int *>(sm.knew + half * 64);
+        const int *kn = reinterpret_cast<const int *>(sm.knew + kb16);
 #pragma unroll
-          for (int e = 0; e < 16; ++e) kw[i][e] = kn[e];
-          kscale[i] = sm.ksnew;
-        }
+        for (int e = 0; e < 4; ++e)
+          if (j + 8 * e + kg == pos0) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) kw[i][4 * e + t] = kn[t];
+          }
+        if (j + kcl == pos0) kscale[i] = sm.ksnew;
 #pragma unroll
         for (int cc = 0; cc < 16; ++cc)
           if (j + kh + cc == pos0) vw[i][cc] = *reinterpret_cast<const int *>(sm.vnew + d0);
@@ -509,22 +514,35 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
       const int jb = wave + NW * i;
       if (jb >= nb) continue;
       const int j = (b0 + jb) * 32;
-      const bool valid = j + kc < kv_end;
+      const bool valid = j + kcl < kv_end;
 #pragma unroll
       for (int h = 0; h < QPW; ++h) {
-        int acc = 0;
+        int p[4];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) acc = sdot4(qv[h][e], kw[i][e], acc);
-        acc += lane_xor<1>(acc);  // exact int32: both halves of the key
+        for (int e = 0; e < 4; ++e) {
+          p[e] = 0;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) p[e] = sdot4(qv[h][t], kw[i][4 * e + t], p[e]);
+        }
+        // exact int32 sums over the 8 lanes of a key, scattered over lane
+        // bits 2, 1, 0: lane l keeps keys 8 (2 b2 + {0, 1}) + kg after bit
+        // 2, key 8 (2 b2 + b1) + kg = kcl after bit 1
+        const bool b2 = lane & 4, b1 = lane & 2;
+        int k0 = b2 ? p[2] : p[0], k1 = b2 ? p[3] : p[1];
+        k0 += lane_xor<4>(b2 ? p[0] : p[2]);
+        k1 += lane_xor<4>(b2 ? p[1] : p[3]);
+        int acc = b1 ? k1 : k0;
+        acc += lane_xor<2>(b1 ? k0 : k1);
+        acc += lane_xor<1>(acc);
         float s = -INFINITY;
         if (valid) {
           s = __fmul_rn(static_cast<float>(acc), kscale[i]);
           s = __fmul_rn(s, qscale[h]);
           s = __fmul_rn(s, a.qk_scale);
-          if (kc > pos0 - j) s = -INFINITY;  // (col - row) > pos0 - j, row 0
+          if (kcl > pos0 - j) s = -INFINITY;  // (col - row) > pos0 - j, row 0
         }
         const float bm = max64(s);
-        if (half == 0) sm.s[h][jb * 32 + kc] = s;
+        if ((lane & 1) == 0) sm.s[h][jb * 32 + kcl] = s;
         if (lane == 0) sm.bmax[h][jb] = bm;
       }
     }
