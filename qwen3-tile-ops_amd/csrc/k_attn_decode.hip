@@ -258,9 +258,16 @@ __device__ void fused_compute(const AttnArgs &a, const HotArgs &h, SM &sm, Fused
 // Workgroup w of the pf_wgs prefetch workgroups reads 16 B per thread from
 // every (nthreads * 16)-byte chunk w, w + pf_wgs, ... of each range.  Four
 // loads are in flight per thread; the values only feed an empty asm
-// statement so that the loads are kept.
-__device__ void prefetch_ranges(const AttnArgs &a, int w) {
-  for (int r = 0; r < a.pf_n; ++r) {
+// statement so that the loads are kept.  With pf_kv_heads, the last four
+// ranges go to the L2s instead (AttnArgs::pf_kv_heads): the workgroup has
+// grid id first + w, on XCD (first + w) % 8, and the XCD's prefetch
+// workgroups split the rows; thread t reads 16 bytes of row t / 16 + 48 k of
+// the slice of the ((t / 8) % nh)-th of the XCD's nh query heads' kv heads
+// (every slice for nh <= 2), one load in flight per thread (measured faster
+// than two: the attention's own loads meet less of this traffic).
+__device__ void prefetch_ranges(const AttnArgs &a, int w, int first) {
+  const int nkv = a.pf_kv_heads > 0 ? 4 : 0;
+  for (int r = 0; r < a.pf_n - nkv; ++r) {
     const int8_t *base = a.pf[r];
     const int64_t n16 = a.pf_bytes[r] / 16;
     int64_t i = static_cast<int64_t>(w) * blockDim.x + threadIdx.x;
@@ -273,6 +280,35 @@ __device__ void prefetch_ranges(const AttnArgs &a, int w) {
       asm volatile("" ::"v"(v0.x), "v"(v1.x), "v"(v2.x), "v"(v3.x));
     }
     for (; i < n16; i += stride) {
+      const int4 v0 = reinterpret_cast<const int4 *>(base)[i];
+      asm volatile("" ::"v"(v0.x));
+    }
+  }
+  if (nkv == 0 || a.pf_n < nkv) return;
+  const int xcd = (first + w) % 8;
+  const int w0 = ((xcd - first) % 8 + 8) % 8;  // first prefetch workgroup on this XCD
+  const int nsub = (a.pf_wgs - w0 + 7) / 8;
+  const int sub = (w - w0) / 8;
+  const int nh = (a.pf_kv_heads - xcd + 7) / 8;
+  const int grp = a.pf_kv_heads / a.kv_heads;
+  if (nh <= 0 || grp <= 0) return;
+  const int t = threadIdx.x;
+  const int rpp = static_cast<int>(blockDim.x) / 16;  // rows per pass
+  const int kvh = (xcd + 8 * ((t >> 3) % nh)) / grp;
+  for (int r = a.pf_n - nkv; r < a.pf_n - 2; ++r) {
+    const int8_t *base = a.pf[r] + kvh * HD + 16 * (t & 7);
+    const int64_t rows = a.pf_bytes[r] / a.row_bytes;
+    for (int64_t row = static_cast<int64_t>(sub) * rpp + t / 16; row < rows;
+         row += static_cast<int64_t>(nsub) * rpp) {
+      const int4 v = *reinterpret_cast<const int4 *>(base + row * a.row_bytes);
+      asm volatile("" ::"v"(v.x));
+    }
+  }
+  for (int r = a.pf_n - 2; r < a.pf_n; ++r) {
+    const int8_t *base = a.pf[r];
+    const int64_t n16 = a.pf_bytes[r] / 16;
+    for (int64_t i = static_cast<int64_t>(sub) * blockDim.x + t; i < n16;
+         i += static_cast<int64_t>(nsub) * blockDim.x) {
       const int4 v0 = reinterpret_cast<const int4 *>(base)[i];
       asm volatile("" ::"v"(v0.x));
     }
@@ -294,11 +330,11 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
   if constexpr (FUSE) {
     if (blockIdx.y > 0) {
       const int w = static_cast<int>((blockIdx.y - 1) * gridDim.x + blockIdx.x);
-      if (w < a.pf_wgs) prefetch_ranges(a, w);
+      if (w < a.pf_wgs) prefetch_ranges(a, w, static_cast<int>(gridDim.x));
       return;
     }
   } else if (static_cast<int>(blockIdx.x) >= a.heads / QPW) {
-    prefetch_ranges(a, static_cast<int>(blockIdx.x) - a.heads / QPW);
+    prefetch_ranges(a, static_cast<int>(blockIdx.x) - a.heads / QPW, a.heads / QPW);
     return;
   }
   const HotArgs h = hot_args<FUSE, OFUSE>(a);
@@ -760,6 +796,9 @@ bool attn_decode_supported(const AttnArgs &a) {
   for (int r = 0; r < a.pf_n; ++r)
     if ((reinterpret_cast<uintptr_t>(a.pf[r]) & 15) != 0 || a.pf_bytes[r] < 0) return false;
   if (a.row_pos && (a.rows < 1 || a.rows > 65535 || a.fuse_heads || a.pf_n || !a.row_tables)) return false;
+  if (a.pf_kv_heads > 0 && (!a.fuse_heads || a.pf_n < 4 || a.kv_heads <= 0 || a.pf_kv_heads % a.kv_heads != 0 ||
+                            static_cast<int64_t>(a.kv_heads) * HD > a.row_bytes))
+    return false;
   // O projection fusion: b = 1 with the head epilogues; rows of wo cover
   // every head's 128 columns and are 16-byte aligned
   if (a.opart && (!a.fuse_heads || a.row_pos || !a.wo || !a.wos || !al16(a.wo) || (a.ldwo % 16) != 0 ||

@@ -280,6 +280,15 @@ struct AttnArgs {
   int o_rows;
   float *opart;
   int64_t ld_opart;
+  // (last, so that the fields above keep their kernel-argument offsets)
+  // fused b = 1 variant only: pf_kv_heads > 0 marks the last four ranges as
+  // the next attention's K pages, V pages, K scales and V scales (K/V rows
+  // row_bytes apart, as in this call), read into the L2 of the XCD that will
+  // read them: query head h's workgroup is workgroup h of the grid's first
+  // row, which the round-robin dispatch puts on XCD h % 8, so the prefetch
+  // workgroups on XCD x read the HD-byte slices of the kv heads of the query
+  // heads h = x (mod 8) (of pf_kv_heads) of every row, and all the scales.
+  int pf_kv_heads;
 };
 hipError_t launch_attention(const AttnArgs &a, hipStream_t s);
 // the two multi-row kernels behind launch_attention: the phase-parallel one

@@ -545,7 +545,8 @@ int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int opti
         if (ofuse) add_pf(nx.wo, HH * QW);
       }
       // the K/V pages (and scales) the next attention reads: the next
-      // layer's, or layer 0's for the next token after the last layer
+      // layer's, or layer 0's for the next token after the last layer; each
+      // kv head's slices go to the L2 of the XCDs whose heads read them
       {
         const LayerPtrs nx = layer_ptrs(m, is_last ? 0 : L + 1);
         const uint32_t span_len = std::min<uint32_t>(pos + rows + (is_last ? 1 : 0), y.max_seq);
@@ -558,10 +559,14 @@ int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int opti
           add_pf(nx.vc + lo * pgb, np * pgb);
           add_pf(reinterpret_cast<const int8_t *>(nx.kcs) + lo * spb, np * spb);
           add_pf(reinterpret_cast<const int8_t *>(nx.vcs) + lo * spb, np * spb);
+          t.pf_kv_heads = static_cast<int>(y.heads);
         }
       }
       t.pf_wgs = m->pf_wgs;
-      if (m->pf_wgs == 0) t.pf_n = 0;
+      if (m->pf_wgs == 0) {
+        t.pf_n = 0;
+        t.pf_kv_heads = 0;
+      }
     } else {
       // head epilogues: K (norm+RoPE+quant) and V (quant) of every row into
       // the page slots; Q (norm+RoPE+quant) of the tail rows
