@@ -295,12 +295,13 @@ __device__ void prefetch_ranges(const AttnArgs &a, int w, int first) {
   const int t = threadIdx.x;
   const int rpp = static_cast<int>(blockDim.x) / 16;  // rows per pass
   const int kvh = (xcd + 8 * ((t >> 3) % nh)) / grp;
+  // (32-bit row arithmetic: a span is far below 2^31 bytes, checked on the host)
+  const uint32_t rb = static_cast<uint32_t>(a.row_bytes);
   for (int r = a.pf_n - nkv; r < a.pf_n - 2; ++r) {
     const int8_t *base = a.pf[r] + kvh * HD + 16 * (t & 7);
-    const int64_t rows = a.pf_bytes[r] / a.row_bytes;
-    for (int64_t row = static_cast<int64_t>(sub) * rpp + t / 16; row < rows;
-         row += static_cast<int64_t>(nsub) * rpp) {
-      const int4 v = *reinterpret_cast<const int4 *>(base + row * a.row_bytes);
+    const uint32_t rows = static_cast<uint32_t>(a.pf_bytes[r]) / rb;
+    for (uint32_t row = static_cast<uint32_t>(sub * rpp + t / 16); row < rows; row += static_cast<uint32_t>(nsub * rpp)) {
+      const int4 v = *reinterpret_cast<const int4 *>(base + row * rb);
       asm volatile("" ::"v"(v.x));
     }
   }
@@ -797,7 +798,8 @@ bool attn_decode_supported(const AttnArgs &a) {
     if ((reinterpret_cast<uintptr_t>(a.pf[r]) & 15) != 0 || a.pf_bytes[r] < 0) return false;
   if (a.row_pos && (a.rows < 1 || a.rows > 65535 || a.fuse_heads || a.pf_n || !a.row_tables)) return false;
   if (a.pf_kv_heads > 0 && (!a.fuse_heads || a.pf_n < 4 || a.kv_heads <= 0 || a.pf_kv_heads % a.kv_heads != 0 ||
-                            static_cast<int64_t>(a.kv_heads) * HD > a.row_bytes))
+                            static_cast<int64_t>(a.kv_heads) * HD > a.row_bytes ||
+                            a.pf_bytes[a.pf_n - 4] >= (int64_t{1} << 31) || a.pf_bytes[a.pf_n - 3] >= (int64_t{1} << 31)))
     return false;
   // O projection fusion: b = 1 with the head epilogues; rows of wo cover
   // every head's 128 columns and are 16-byte aligned
