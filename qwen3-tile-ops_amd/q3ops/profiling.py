@@ -2,7 +2,7 @@
 (profiles/).  Every summary there is produced by this module from the CSV
 files of one of the rocprofv3 commands named in the summary.
 
-    python -m q3ops.profiling stats <kernel_stats.csv> --cmd "<command>" [--top N]
+    python -m q3ops.profiling stats <kernel_stats.csv> --cmd "<command>" [--top N] [--title T]
         -> markdown table of the per-kernel statistics (stdout)
 
     python -m q3ops.profiling pmc --fetch <counter_collection.csv>
@@ -100,10 +100,10 @@ def class_of(name: str) -> str | None:
     return None
 
 
-def stats_md(path: str, cmd: str, top: int) -> str:
+def stats_md(path: str, cmd: str, top: int, title: str | None = None) -> str:
     rows = list(csv.DictReader(open(path)))
     rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
-    out = [f"Command: `{cmd}`", "", f"Source: rocprofv3 `--kernel-trace --stats` ({path.split('/')[-1]})", "",
+    out = ([f"# {title}", ""] if title else []) + [f"Command: `{cmd}`", "", f"Source: rocprofv3 `--kernel-trace --stats` ({path.split('/')[-1]})", "",
            "| kernel | class | calls | avg us | min us | max us | % time |", "|---|---|---:|---:|---:|---:|---:|"]
     for r in rows[:top]:
         out.append(f"| `{short_name(r['Name'])}` | {class_of(r['Name']) or ''} | {r['Calls']} | "
@@ -213,6 +213,7 @@ def main(argv=None) -> int:
     s.add_argument("csv")
     s.add_argument("--cmd", required=True)
     s.add_argument("--top", type=int, default=20)
+    s.add_argument("--title", help="heading of the markdown summary")
     p = sub.add_parser("pmc")
     p.add_argument("--fetch", required=True)
     p.add_argument("--write", required=True)
@@ -226,7 +227,7 @@ def main(argv=None) -> int:
     c.add_argument("--clock-ghz", type=float, default=2.4)
     a = ap.parse_args(argv)
     if a.cmd_name == "stats":
-        sys.stdout.write(stats_md(a.csv, a.cmd, a.top))
+        sys.stdout.write(stats_md(a.csv, a.cmd, a.top, a.title))
     elif a.cmd_name == "counters":
         json.dump(counters_json(a.csv, a.cmd, a.cus, a.stats, a.clock_ghz), sys.stdout, indent=1)
         sys.stdout.write("\n")
