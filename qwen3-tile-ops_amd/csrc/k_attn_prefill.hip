@@ -36,8 +36,8 @@
 // g - 1 and phase 1 of chunk g, barrier, phases 2-3 of chunk g (and the int8
 // store of an item whose last chunk was g - 1), barrier.  Every wave copies
 // its own block of the next chunk: V with global_load_lds into the other half
-// of a two-chunk LDS ring, the K operand rows straight into registers, ks | vs
-// with global_load_lds into a per-wave slot.
+// of a two-chunk LDS ring, the K operand rows and ks | vs straight into
+// registers.
 //
 // Layouts (lane = lc + 16 lg):
 //   S^T_j = K_j . Q^T with v_mfma_i32_16x16x64_i8, keys as the M dimension:
@@ -88,7 +88,6 @@ struct Lds {
   float bm[NI][QB][LDB];       // block maxima [item][row][block]
   float corr[NI][QB][LDB], psum[NI][QB][LDB], pmax[NI][QB][LDB];
   float cmax[NI][QB][8];       // |out| maxima of each 16-dim tile
-  float sc[Cfg<NI>::NW][2 * KB];  // ks | vs of each wave's block
   uint64_t etab[32];
 };
 static_assert(sizeof(Lds<1>) <= 80 * 1024, "two single-block workgroups per CU");
@@ -138,8 +137,10 @@ __device__ __forceinline__ uint32_t pack4(int b0, int b1, int b2, int b3) {
          ((static_cast<uint32_t>(b2) & 0xffu) << 16) | (static_cast<uint32_t>(b3) << 24);
 }
 
+// (the second bound is waves per SIMD: 16 waves per CU, two single-block
+// workgroups or one pair, i.e. at most 128 VGPRs)
 template <int NI>
-__global__ void __launch_bounds__(Cfg<NI>::NW * 64, NI == 1 ? 2 : 1) attn_prefill_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(Cfg<NI>::NW * 64, 4) attn_prefill_kernel(AttnArgs a) {
   constexpr int CB = Cfg<NI>::CB;
   extern __shared__ __align__(16) int8_t smem[];
   Lds<NI> &L = *reinterpret_cast<Lds<NI> *>(smem);
@@ -192,16 +193,29 @@ __global__ void __launch_bounds__(Cfg<NI>::NW * 64, NI == 1 ? 2 : 1) attn_prefil
   // ---- this wave's copies of its block of chunk g ----
   v4i kop[2][2];  // K operand rows of the wave's block: [kt][64-byte k-step]
   const int phys = lane & 7;
+  // the page id of the wave's block of chunk g, held by lane 0: a kernel
+  // argument for the first blk_page_n blocks, else a table load (per lane: a
+  // wave-uniform load would be read into a scalar register at once, making
+  // the wave wait there for every load issued before it, i.e. for the K/V
+  // copies of the chunk before); users take it with pg()
   auto page_of = [&](int g) -> uint32_t {
-    if (g >= G || wave >= nb_of(1, g)) return 0;
-    return a.table[static_cast<uint32_t>((g * CB + wave) * KB) >> pt_shift];
+    uint32_t p = 0;
+    const int j = g * CB + wave;
+    if (g < G && wave < nb_of(1, g)) {
+      if (j < a.blk_page_n)
+        p = a.blk_page[j];
+      else if (lane == 0)
+        p = a.table[static_cast<uint32_t>(j * KB) >> pt_shift];
+    }
+    return p;
   };
+  auto pg = [](uint32_t p) { return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(p), 0)); };
   // in-page offsets fit in 32 bits (checked on the host)
   const int rb = static_cast<int>(a.row_bytes), srb = static_cast<int>(a.scale_row_bytes);
   auto copy_v = [&](int g, uint32_t page) {
     if (g >= G || wave >= nb_of(1, g)) return;
     const int slot0 = ((g * CB + wave) * KB) & (a.page_tokens - 1);
-    const int8_t *vb = a.v + static_cast<int64_t>(page) * a.page_bytes + kvh * HD;
+    const int8_t *vb = a.v + static_cast<int64_t>(pg(page)) * a.page_bytes + kvh * HD;
     int8_t *dst = L.v[g & 1][wave];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
@@ -213,27 +227,39 @@ __global__ void __launch_bounds__(Cfg<NI>::NW * 64, NI == 1 ? 2 : 1) attn_prefil
   auto load_k = [&](int g, uint32_t page) {
     if (g >= G || wave >= nb_of(1, g)) return;
     const int slot0 = ((g * CB + wave) * KB) & (a.page_tokens - 1);
-    const int8_t *kb = a.k + static_cast<int64_t>(page) * a.page_bytes + kvh * HD;
+    const int8_t *kb = a.k + static_cast<int64_t>(pg(page)) * a.page_bytes + kvh * HD;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
         kop[kt][ks] = *reinterpret_cast<const v4i *>(kb + ((slot0 + 16 * kt + lc) * rb + 64 * ks + 16 * lg));
   };
-  auto copy_sc = [&](int g, uint32_t page) {
+  // ks and vs of keys 16 kt + 4 lg + i of the wave's block, in registers
+  // (not staged through LDS by global_load_lds: a DS read of memory that an
+  // LDS DMA writes waits for every DMA in flight, i.e. for the next chunk's
+  // V copies)
+  float ksr[2][4], vsr[2][4];
+  auto load_sc = [&](int g, uint32_t page) {
     if (g >= G || wave >= nb_of(1, g)) return;
     const int slot0 = ((g * CB + wave) * KB) & (a.page_tokens - 1);
-    const int8_t *sb = reinterpret_cast<const int8_t *>(lane < 32 ? a.ks : a.vs) +
-                       static_cast<int64_t>(page) * a.scale_page_bytes + kvh * 4;
-    __builtin_amdgcn_global_load_lds(const_cast<int8_t *>(sb + (slot0 + (lane & 31)) * srb), to_lds(L.sc[wave]), 4,
-                                     0, 0);
+    const int64_t sp = static_cast<int64_t>(pg(page)) * a.scale_page_bytes + kvh * 4;
+    const int8_t *kb = reinterpret_cast<const int8_t *>(a.ks) + sp;
+    const int8_t *vb = reinterpret_cast<const int8_t *>(a.vs) + sp;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int off = (slot0 + 16 * kt + 4 * lg + i) * srb;
+        ksr[kt][i] = *reinterpret_cast<const float *>(kb + off);
+        vsr[kt][i] = *reinterpret_cast<const float *>(vb + off);
+      }
   };
 
   // ---- prologue: chunk 0 in flight, exp table, Q operands of both items ----
   uint32_t page = page_of(0);
   copy_v(0, page);
   load_k(0, page);
-  copy_sc(0, page);
+  load_sc(0, page);
   page = page_of(1);
   if (threadIdx.x == 0) stage_exp2_table(L.etab);
   // Q row lc of item A / B as the B operand, [item][64-byte k-step]; loaded
@@ -277,21 +303,62 @@ __global__ void __launch_bounds__(Cfg<NI>::NW * 64, NI == 1 ? 2 : 1) attn_prefil
       const int nbp = nb_of(it4, gp);
       const int8_t *vbase = &L.v[gp & 1][0][0];
       for (int b0 = 0; b0 < nbp; b0 += 4) {
-        const float4 c4 = *reinterpret_cast<const float4 *>(&L.corr[sl(it4)][lc][b0]);
-        const float4 p4 = *reinterpret_cast<const float4 *>(&L.pmax[sl(it4)][lc][b0]);
-        const float4 s4 = *reinterpret_cast<const float4 *>(&L.psum[sl(it4)][lc][b0]);
+        float4 c4, p4, s4;
+        v2i vt[4];
+        long pbv[4];
+        const int8_t *vq = vbase + b0 * (KB * HD) + v_tr_off;
+        if constexpr (NI == 1) {
+          // Every LDS read of this phase is inline asm: the compiler makes a DS
+          // read wait for every LDS DMA in flight (vmcnt 0) unless it can tell
+          // the memory apart, and here chunk g's V copies (into the other half
+          // of the ring) and K/Q/scale loads are in flight, which this phase
+          // does not read and should run under.  What it reads: chunk g - 1's
+          // V half, complete since that chunk's phase 1 (vmcnt 0) and its
+          // barriers, and corr/pmax/psum/P8 from its phase 3, before B2(g - 1).
+          // The reads complete at the lgkmcnt wait below, before B1(g), after
+          // which chunk g + 1's copies overwrite this V half.
+          // (one asm statement: the values exist only after its wait, and the
+          // early-clobbered outputs keep the addresses intact until issued)
+          auto la = [](const void *p) { return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p)); };
+          asm volatile(
+              "ds_read_b128 %0, %11\n\t"
+              "ds_read_b128 %1, %12\n\t"
+              "ds_read_b128 %2, %13\n\t"
+              "ds_read_b64_tr_b8 %3, %14\n\t"
+              "ds_read_b64_tr_b8 %4, %15\n\t"
+              "ds_read_b64_tr_b8 %5, %16\n\t"
+              "ds_read_b64_tr_b8 %6, %17\n\t"
+              "ds_read_b64 %7, %18\n\t"
+              "ds_read_b64 %8, %19\n\t"
+              "ds_read_b64 %9, %20\n\t"
+              "ds_read_b64 %10, %21\n\t"
+              "s_waitcnt lgkmcnt(0)"
+              : "=&v"(c4), "=&v"(p4), "=&v"(s4), "=&v"(vt[0]), "=&v"(vt[1]), "=&v"(vt[2]), "=&v"(vt[3]),
+                "=&v"(pbv[0]), "=&v"(pbv[1]), "=&v"(pbv[2]), "=&v"(pbv[3])
+              : "v"(la(&L.corr[sl(it4)][lc][b0])), "v"(la(&L.pmax[sl(it4)][lc][b0])),
+                "v"(la(&L.psum[sl(it4)][lc][b0])), "v"(la(vq)), "v"(la(vq + KB * HD)), "v"(la(vq + 2 * KB * HD)),
+                "v"(la(vq + 3 * KB * HD)), "v"(la(&L.p8[sl(it4)][b0][lane])), "v"(la(&L.p8[sl(it4)][b0 + 1][lane])),
+                "v"(la(&L.p8[sl(it4)][b0 + 2][lane])), "v"(la(&L.p8[sl(it4)][b0 + 3][lane]))
+              : "memory");
+        } else {  // (16 waves: the asm form's outputs do not fit the registers)
+          c4 = *reinterpret_cast<const float4 *>(&L.corr[sl(it4)][lc][b0]);
+          p4 = *reinterpret_cast<const float4 *>(&L.pmax[sl(it4)][lc][b0]);
+          s4 = *reinterpret_cast<const float4 *>(&L.psum[sl(it4)][lc][b0]);
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            vt[b] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(reinterpret_cast<lds_v2i_ptr>(to_lds(vq + b * (KB * HD))));
+            pbv[b] = static_cast<long>(L.p8[sl(it4)][b0 + b][lane]);
+          }
+        }
         const float crv[4] = {c4.x, c4.y, c4.z, c4.w};
         const float pmv[4] = {p4.x, p4.y, p4.z, p4.w};
         const float psv[4] = {s4.x, s4.y, s4.z, s4.w};
         v4i c[4];
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-          const long pb = static_cast<long>(L.p8[sl(it4)][b0 + b][lane]);
-          const v2i vt = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-              reinterpret_cast<lds_v2i_ptr>(to_lds(vbase + (b0 + b) * (KB * HD) + v_tr_off)));
           long va;
-          __builtin_memcpy(&va, &vt, sizeof(va));
-          c[b] = __builtin_amdgcn_mfma_i32_16x16x32_i8(va, pb, zero4(), 0, 0, 0);
+          __builtin_memcpy(&va, &vt[b], sizeof(va));
+          c[b] = __builtin_amdgcn_mfma_i32_16x16x32_i8(va, pbv[b], zero4(), 0, 0, 0);
         }
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
@@ -331,10 +398,6 @@ __global__ void __launch_bounds__(Cfg<NI>::NW * 64, NI == 1 ? 2 : 1) attn_prefil
     const int j = g * CB + wave;
     wait_vmcnt<0>();  // this wave's copies and K rows of chunk g
     if (wave < nbB) {
-      const float *ksc = L.sc[wave];
-      float4 k4[2];
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt) k4[kt] = *reinterpret_cast<const float4 *>(&ksc[16 * kt + 4 * lg]);
 #pragma unroll
       for (int it = 0; it < 2; ++it) {
         if (it == 1 || wave < nbA) {
@@ -346,7 +409,7 @@ __global__ void __launch_bounds__(Cfg<NI>::NW * 64, NI == 1 ? 2 : 1) attn_prefil
           for (int kt = 0; kt < 2; ++kt) {
             v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop[kt][0], qop[it][0], zero4(), 0, 0, 0);
             acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop[kt][1], qop[it][1], acc, 0, 0, 0);
-            const float kv[4] = {k4[kt].x, k4[kt].y, k4[kt].z, k4[kt].w};
+            const float kv[4] = {ksr[kt][0], ksr[kt][1], ksr[kt][2], ksr[kt][3]};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               float x = static_cast<float>(acc[i]);
@@ -426,10 +489,6 @@ __global__ void __launch_bounds__(Cfg<NI>::NW * 64, NI == 1 ? 2 : 1) attn_prefil
 
     // ---- phase 3: corr, P, psum, P8 of this wave's block, per item ----
     if (wave < nbB) {
-      const float *vsc = L.sc[wave] + KB;
-      float4 v4[2];
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt) v4[kt] = *reinterpret_cast<const float4 *>(&vsc[16 * kt + 4 * lg]);
 #pragma unroll
       for (int it = 0; it < 2; ++it) {
         if (it == 1 || wave < nbA) {
@@ -457,7 +516,7 @@ __global__ void __launch_bounds__(Cfg<NI>::NW * 64, NI == 1 ? 2 : 1) attn_prefil
           float pmx = 0.0f;
 #pragma unroll
           for (int kt = 0; kt < 2; ++kt) {
-            const float vv[4] = {v4[kt].x, v4[kt].y, v4[kt].z, v4[kt].w};
+            const float vv[4] = {vsr[kt][0], vsr[kt][1], vsr[kt][2], vsr[kt][3]};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               const int key = j * KB + 16 * kt + 4 * lg + i;
@@ -499,12 +558,11 @@ __global__ void __launch_bounds__(Cfg<NI>::NW * 64, NI == 1 ? 2 : 1) attn_prefil
         __builtin_amdgcn_sched_barrier(0);  // one unit at a time: bounds the live exp chains
       }
     }
-    // K rows of chunk g + 1, and ks | vs into this wave's slot after its
-    // last read above
+    // K rows, Q rows and ks | vs of chunk g + 1 (their registers were last
+    // read above)
     load_k(g + 1, page);
     load_q(g + 1);
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    copy_sc(g + 1, page);
+    load_sc(g + 1, page);
     page = page_of(g + 2);
     lds_barrier();  // B2(g)
   }
@@ -513,7 +571,7 @@ __global__ void __launch_bounds__(Cfg<NI>::NW * 64, NI == 1 ? 2 : 1) attn_prefil
 }  // namespace
 
 bool attn_prefill_supported(const AttnArgs &a) {
-  return a.page_tokens >= KB && (a.page_tokens & (a.page_tokens - 1)) == 0 && a.row_bytes % 16 == 0 &&
+  return a.blk_page_n >= 0 && a.blk_page_n <= 32 && a.page_tokens >= KB && (a.page_tokens & (a.page_tokens - 1)) == 0 && a.row_bytes % 16 == 0 &&
          a.row_bytes * a.page_tokens < (int64_t{1} << 31) && a.scale_row_bytes * a.page_tokens < (int64_t{1} << 31) &&
          a.kv_heads > 0 && a.heads % a.kv_heads == 0 && a.scale_row_bytes % 4 == 0 &&
          a.scale_page_bytes % 4 == 0;

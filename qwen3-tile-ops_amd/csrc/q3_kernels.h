@@ -244,8 +244,8 @@ struct AttnArgs {
   // K norm+RoPE+quant and V quant into their page slots, Q norm+RoPE+quant
   // into q8/qs (which must then be writable).
   int fuse_heads;
-  // with fuse_heads: the page ids of the first 32 key blocks
-  // (blk_page[j] = table[32 j / page_tokens], j < min(32, blocks)) and of
+  // with fuse_heads (or blk_page_n, below): the page ids of the first 32 key
+  // blocks (blk_page[j] = table[32 j / page_tokens], j < min(32, blocks)) and of
   // the new token (table[(kv_len - 1) / page_tokens]), copied from the
   // caller's host mirror of the table, so that the first K/V addresses come
   // from kernel arguments instead of a table load
@@ -280,6 +280,9 @@ struct AttnArgs {
   int o_rows;
   float *opart;
   int64_t ld_opart;
+  // prefill kernel (optional): blk_page[j] is valid for j < blk_page_n <= 32
+  // (else the table is read)
+  int blk_page_n;
   // (last, so that the fields above keep their kernel-argument offsets)
   // fused b = 1 variant only: pf_kv_heads > 0 marks the last four ranges as
   // the next attention's K pages, V pages, K scales and V scales (K/V rows

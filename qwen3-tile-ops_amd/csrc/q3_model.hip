@@ -478,6 +478,14 @@ int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int opti
     t.row_bytes = KW;
     t.scale_page_bytes = static_cast<int64_t>(kPageTokens) * y.kv_heads * 4;
     t.scale_row_bytes = y.kv_heads * 4;
+    // page ids of the first key blocks, from the host mirror of the table
+    // (the prefill kernel reads them from its arguments; the fused decode
+    // variant below sets the same entries)
+    {
+      const uint32_t nblk = std::min<uint32_t>(32, (pos + rows + 31) / 32);
+      for (uint32_t j = 0; j < nblk; ++j) t.blk_page[j] = m->htab[j * 32 / kPageTokens];
+      t.blk_page_n = static_cast<int>(nblk);
+    }
     t.o8 = o8 + static_cast<int64_t>(tr0) * QW;
     t.ldo = QW;
     t.os = os + static_cast<int64_t>(tr0) * y.heads;
