@@ -1,4 +1,4 @@
-// Decode-shaped group GEMM ("GEMV", M <= 16 rows) across the whole chip.
+// Decode-shaped group GEMM ("GEMV", M <= 64 rows) across the whole chip.
 //
 // Arithmetic of k_gemm.hip (kernels/group_gemm.h:27-222,
 // ref_qwen3.py:145-158): per K-group an exact int32 MFMA partial, dequant
@@ -9,7 +9,10 @@
 // its MFMAs and parks its dequantised per-group tiles in LDS; then one
 // (row, column) per thread adds the groups in order.  Workgroups never wait
 // for each other: there are no grid-wide dependencies, fences or contended
-// atomics in this kernel.
+// atomics in this kernel.  Batches of 17-64 rows (independent sequences
+// decoding together) run as MT = 2 or 4 tiles of 16 rows over the same
+// weight registers: a weight byte is loaded once per workgroup whatever M
+// is, and the A operand (M x K, read by every workgroup) comes from L2.
 //
 // Prologue (consumer-side quantisation): instead of reading a pre-quantised
 // int8 A operand, the workgroup may build it in LDS from f32 rows
@@ -270,15 +273,20 @@ constexpr int kMaxPart = 16;
 constexpr int kPartPro = 1, kPartEpi = 2;
 // BSG: per-(row, K-group) B scales seg[0].bs[n * bs_ld + g], loaded with
 // the other scales before the weight stream (PRO_NONE, one matrix).
-template <int GPW, int KSTEPS, int NT, int NMAT, int PRO, int PART, bool BSG = false>
+// MT row tiles of 16 (MT > 1: plain A operand, rows past M computed on row
+// M - 1's data and not stored), their A fragments loaded AB tiles at a time.
+template <int GPW, int KSTEPS, int NT, int NMAT, int PRO, int PART, bool BSG = false, int MT = 1, int AB = MT>
 __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
   static_assert(PART == 0 || NT == 1, "partials: one item column per thread");
   static_assert(!BSG || (NMAT == 1 && PRO == PRO_NONE && PART == 0), "per-group B scales: plain GEMV");
+  static_assert(MT == 1 || (PRO == PRO_NONE && PART == 0 && NT == 1), "row tiles: plain A operand");
+  static_assert(AB >= 1 && MT % AB == 0, "A fragment batches");
   constexpr int NPRO = PART == kPartPro ? kMaxPart : 0;
   constexpr int NEPI = PART == kPartEpi ? kMaxPart : 0;
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int NB = 16 * NT;       // columns per workgroup
   constexpr int PP = NB + 1;        // partial-tile pitch
+  constexpr int MR = 16 * MT;       // rows per workgroup
   const int lane = threadIdx.x & 63;
   const int wave = wave_id();
   const int lr = lane & 15;
@@ -330,10 +338,10 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
   const float *const sg_bs2 = pick(s_bs2);
   const GemvSeg &sg = a.seg[si];
 
-  // LDS: partials [NMAT][ngroups][16][PP] f32, then (prologue) A [M][K] i8
+  // LDS: partials [NMAT][ngroups][MR][PP] f32, then (prologue) A [M][K] i8
   // and its scales [M][K/256] f32 and 32 block sums
   float *part = reinterpret_cast<float *>(smem);
-  const int part_floats = NMAT * ngroups * 16 * PP;
+  const int part_floats = NMAT * ngroups * MR * PP;
   int8_t *a_lds = reinterpret_cast<int8_t *>(part + part_floats);
   float *as_lds = reinterpret_cast<float *>(a_lds + ((M * K + 15) & ~15));
   float *blk = as_lds + M * (K / 256);
@@ -359,27 +367,35 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
     for (int h = 0; h < NEPI; ++h) pe[h] = pc[min(h, ps.npart - 1) * ps.ld_part];
   }
   __builtin_amdgcn_sched_barrier(0);
-  // A operand rows and scales of the unfused path, also before the weights
+  // A operand rows and scales of the unfused path (the first AB row tiles),
+  // also before the weights
   const bool avalid = lr < M;
-  v4i av[GPW][KSTEPS];
-  float asv[GPW][4];
-  if constexpr (PRO == PRO_NONE) {
-    const int8_t *arow = ps.a + static_cast<int64_t>(avalid ? lr : 0) * ps.lda + lg * 16;
+  v4i av[AB][GPW][KSTEPS];
+  float asv[AB][GPW][4];
+  // row tiles t0 .. t0 + AB - 1; with one tile, rows past M are zeros
+  auto load_a = [&](int t0) {
 #pragma unroll
-    for (int gi = 0; gi < GPW; ++gi) {
-      const int g = min(wave + 4 * gi, ngroups - 1);
+    for (int tb = 0; tb < AB; ++tb) {
+      const int r = 16 * (t0 + tb) + lr;
+      const bool ok = r < M;
+      const int8_t *arow = ps.a + static_cast<int64_t>(MT == 1 ? (ok ? r : 0) : min(r, M - 1)) * ps.lda + lg * 16;
 #pragma unroll
-      for (int ks = 0; ks < KSTEPS; ++ks) {
-        const v4i v = *reinterpret_cast<const v4i *>(arow + g * G + ks * 64);
-        av[gi][ks] = avalid ? v : zero4();
-      }
+      for (int gi = 0; gi < GPW; ++gi) {
+        const int g = min(wave + 4 * gi, ngroups - 1);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = min(lg * 4 + i, M - 1);
-        asv[gi][i] = ps.as[static_cast<int64_t>(m) * ps.ldas + g];
+        for (int ks = 0; ks < KSTEPS; ++ks) {
+          const v4i v = *reinterpret_cast<const v4i *>(arow + g * G + ks * 64);
+          av[tb][gi][ks] = (MT > 1 || ok) ? v : zero4();
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = min(16 * (t0 + tb) + lg * 4 + i, M - 1);
+          asv[tb][gi][i] = ps.as[static_cast<int64_t>(m) * ps.ldas + g];
+        }
       }
     }
-  }
+  };
+  if constexpr (PRO == PRO_NONE) load_a(0);
   // the weight rows' scales, then the weights
   float bsv[NMAT][NT];
   float bsg[BSG ? GPW : 1][NT];
@@ -422,6 +438,21 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
   // before issuing the weights)
   __builtin_amdgcn_sched_barrier(0);
   if (NMAT == 2 && threadIdx.x == 0) stage_exp2_table(exptab);
+  // EPI_ADD over row tiles: the residual value of each of the thread's MT
+  // items (see the ordered sums below), loaded now so that the sums do not
+  // wait for one load per item (the store of an item would otherwise hold
+  // back the next item's load)
+  float basev[MT];
+  if constexpr (MT > 1) {
+    if (sg.epi == EPI_ADD) {
+#pragma unroll
+      for (int k = 0; k < MT; ++k) {
+        const int it = static_cast<int>(threadIdx.x) + 256 * k;
+        const int m = min(it / NB, M - 1);
+        basev[k] = sg.out[static_cast<int64_t>(m) * sg.ldo + (n_blk - sg_n0 + it % NB)];
+      }
+    }
+  }
 
   if constexpr (PRO != PRO_NONE) {
     pro_compute_row<PRO, QW, NPRO>(a, 0, r0, a_lds, as_lds, blk);
@@ -436,43 +467,59 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
       const int g = min(wave + 4 * gi, ngroups - 1);
 #pragma unroll
       for (int ks = 0; ks < KSTEPS; ++ks)
-        av[gi][ks] = avalid ? *reinterpret_cast<const v4i *>(arow + g * G + ks * 64) : zero4();
+        av[0][gi][ks] = avalid ? *reinterpret_cast<const v4i *>(arow + g * G + ks * 64) : zero4();
 #pragma unroll
-      for (int i = 0; i < 4; ++i) asv[gi][i] = as_lds[min(lg * 4 + i, M - 1) * (K / 256) + g];
+      for (int i = 0; i < 4; ++i) asv[0][gi][i] = as_lds[min(lg * 4 + i, M - 1) * (K / 256) + g];
     }
   }
+  // MFMAs of row tiles t0 .. t0 + AB - 1, dequantised group tiles into LDS
+  auto compute = [&](int t0) {
 #pragma unroll
-  for (int gi = 0; gi < GPW; ++gi) {
-    const int g = wave + 4 * gi;
-    if (g >= ngroups) break;
-    float asv_[4];
+    for (int gi = 0; gi < GPW; ++gi) {
+      const int g = wave + 4 * gi;
+      if (g >= ngroups) break;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) asv_[i] = (lg * 4 + i < M) ? asv[gi][i] : 0.0f;
+      for (int tb = 0; tb < AB; ++tb) {
+        float asv_[4];
 #pragma unroll
-    for (int mi = 0; mi < NMAT; ++mi)
+        for (int i = 0; i < 4; ++i) asv_[i] = (MT > 1 || lg * 4 + i < M) ? asv[tb][gi][i] : 0.0f;
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        v4i acc = zero4();
+        for (int mi = 0; mi < NMAT; ++mi)
 #pragma unroll
-        for (int ks = 0; ks < KSTEPS; ++ks)
-          acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[gi][ks], bv[mi][nt][gi][ks], acc, 0, 0, 0);
-        float *pt = part + ((mi * ngroups + g) * 16) * PP + nt * 16 + lr;
-        const float bsc = BSG ? bsg[BSG ? gi : 0][nt] : bsv[mi][nt];
+          for (int nt = 0; nt < NT; ++nt) {
+            v4i acc = zero4();
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          pt[(lg * 4 + i) * PP] = __fmul_rn(__fmul_rn(static_cast<float>(acc[i]), bsc), asv_[i]);
+            for (int ks = 0; ks < KSTEPS; ++ks)
+              acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[tb][gi][ks], bv[mi][nt][gi][ks], acc, 0, 0, 0);
+            float *pt = part + ((mi * ngroups + g) * MR + 16 * (t0 + tb)) * PP + nt * 16 + lr;
+            const float bsc = BSG ? bsg[BSG ? gi : 0][nt] : bsv[mi][nt];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              pt[(lg * 4 + i) * PP] = __fmul_rn(__fmul_rn(static_cast<float>(acc[i]), bsc), asv_[i]);
+          }
       }
+    }
+  };
+  compute(0);
+  // later batches of row tiles: their A fragments into the same registers
+#pragma unroll
+  for (int t0 = AB; t0 < MT; t0 += AB) {
+    load_a(t0);
+    compute(t0);
   }
   __syncthreads();
 
-  // ordered group sums: item = (row m, column j); 16*NB items over 256 threads
-  for (int it = threadIdx.x; it < 16 * NB; it += 256) {
+  // ordered group sums: item = (row m, column j); MR*NB items over 256 threads
+  static_assert((MR * NB) % 256 == 0 && (MT == 1 || MR * NB == 256 * MT), "items per thread");
+#pragma unroll
+  for (int k = 0; k < MR * NB / 256; ++k) {
+    const int it = static_cast<int>(threadIdx.x) + 256 * k;
     const int m = it / NB;
     const int j = it % NB;
     float out = 0.0f, out2 = 0.0f;
     for (int g = 0; g < ngroups; ++g) {
-      out = __fadd_rn(out, part[(g * 16 + m) * PP + j]);
-      if (NMAT == 2) out2 = __fadd_rn(out2, part[((ngroups + g) * 16 + m) * PP + j]);
+      out = __fadd_rn(out, part[(g * MR + m) * PP + j]);
+      if (NMAT == 2) out2 = __fadd_rn(out2, part[((ngroups + g) * MR + m) * PP + j]);
     }
     const int ncol = n_blk - sg_n0 + j;
     if (sg.epi == EPI_ARGMAX) {
@@ -492,7 +539,7 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
     if (m >= M) continue;
     float *dst = sg.out + static_cast<int64_t>(m) * sg.ldo + ncol;
     if (sg.epi == EPI_ADD) {
-      float base = *dst;
+      float base = MT > 1 ? basev[k] : *dst;
       if constexpr (NEPI > 0) {
         float o = 0.0f;  // the O projection, partials in head order
 #pragma unroll
@@ -851,18 +898,50 @@ __global__ void __launch_bounds__(256) qkv_heads_kernel(QkvHeadArgs a) {
   if (lane == 0) *sp = scale;
 }
 
-template <int GPW, int KSTEPS, int NT, int NMAT, int PRO, int PART, bool BSG = false>
+template <int GPW, int KSTEPS, int NT, int NMAT, int PRO, int PART, bool BSG = false, int MT = 1, int AB = MT>
 hipError_t launch_t(const GemvArgs &a, int ncols, hipStream_t s) {
   constexpr int NB = 16 * NT;
   // the prologue gives each wave GPW * KSTEPS / 4 groups of 256 columns
   if (PRO != PRO_NONE && a.K != 256 * GPW * KSTEPS) return hipErrorInvalidValue;
+  if (a.M > 16 * MT) return hipErrorInvalidValue;
   const int ngroups = a.K / a.group;
-  size_t lds = sizeof(float) * NMAT * ngroups * 16 * (NB + 1);
+  size_t lds = sizeof(float) * NMAT * ngroups * 16 * MT * (NB + 1);
   if (PRO != PRO_NONE)
     lds += ((a.M * a.K + 15) & ~15) + sizeof(float) * (a.M * (a.K / 256) + a.K / 32);
-  if (lds > 65536) return hipErrorInvalidValue;
-  Q3_LAUNCH((gemv_kernel<GPW, KSTEPS, NT, NMAT, PRO, PART, BSG>), dim3(ncols / NB), dim3(256), lds, s, a);
+  // dynamic LDS beyond 64 KiB (row tiles) must be allowed once; the kernel's
+  // static LDS (the exp table) counts against the same 160 KiB
+  constexpr size_t kMaxDyn = 159 * 1024;
+  if (lds > (MT > 1 ? kMaxDyn : 65536)) return hipErrorInvalidValue;
+  if constexpr (MT > 1) {
+    static bool attr_set = false;
+    if (!attr_set) {
+      const hipError_t e = hipFuncSetAttribute(
+          reinterpret_cast<const void *>(&gemv_kernel<GPW, KSTEPS, NT, NMAT, PRO, PART, BSG, MT, AB>),
+          hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDyn);
+      if (e != hipSuccess) return e;
+      attr_set = true;
+    }
+  }
+  Q3_LAUNCH((gemv_kernel<GPW, KSTEPS, NT, NMAT, PRO, PART, BSG, MT, AB>), dim3(ncols / NB), dim3(256), lds, s, a);
   return hipGetLastError();
+}
+
+// 17-64 rows (plain A operand, 16-column tiles): 2 or 4 row tiles; with
+// three groups per wave (K = 3072) the A fragments of 4 tiles come in two
+// batches so that they and the weights fit the register file.
+template <int NMAT, bool BSG>
+hipError_t dispatch_rows(const GemvArgs &a, int ncols, hipStream_t s) {
+  const bool four = a.M > 32;
+#define Q3_ROWS(GPW, KS)                                                                     \
+  return four ? launch_t<GPW, KS, 1, NMAT, PRO_NONE, 0, BSG, 4, (GPW * KS > 8 ? 2 : 4)>(a, ncols, s) \
+              : launch_t<GPW, KS, 1, NMAT, PRO_NONE, 0, BSG, 2, 2>(a, ncols, s)
+  if (a.K == 1024 && a.group == 256) Q3_ROWS(1, 4);
+  if (a.K == 1024 && a.group == 128) Q3_ROWS(2, 2);
+  if (a.K == 2048 && a.group == 128) Q3_ROWS(4, 2);
+  if (a.K == 2048 && a.group == 256) Q3_ROWS(2, 4);
+  if (a.K == 3072 && a.group == 256) Q3_ROWS(3, 4);
+#undef Q3_ROWS
+  return hipErrorInvalidValue;
 }
 
 // The prologue kinds (a template parameter, so that no branch on a kernel
@@ -931,6 +1010,10 @@ bool gemv_supported(int M, int K, int group) {
          (K == 3072 && group == 256);
 }
 
+bool gemv_rows_supported(int M, int K, int group, int ncols) {
+  return M >= 1 && M <= 64 && ncols < 65536 && gemv_supported(1, K, group);
+}
+
 namespace {
 
 int ncols_of(const GemvArgs &a) {
@@ -965,7 +1048,8 @@ int stream_grid(int ntiles) {
 bool gemv_group_bscale_supported(const GemvArgs &a) {
   const int epi = a.seg[0].epi;
   return a.pro == PRO_NONE && a.nseg == 1 && !a.part && (epi == EPI_STORE || epi == EPI_ADD) &&
-         !use_stream(a) && gemv_supported(a.M, a.K, a.group);
+         !use_stream(a) && (a.M <= 16 ? gemv_supported(a.M, a.K, a.group)
+                                      : gemv_rows_supported(a.M, a.K, a.group, ncols_of(a)));
 }
 
 int gemv_argmax_slots(const GemvArgs &a) {
@@ -992,6 +1076,7 @@ hipError_t launch_gemv(const GemvArgs &a, hipStream_t s) {
     return hipGetLastError();
   }
   if (use_stream(a)) {
+    if (a.M > 16) return hipErrorInvalidValue;
     const int ntiles = ncols / 64;
     const size_t lds = sizeof(float) * 4 * 16 * 65 +
                        (a.pro != PRO_NONE ? ((a.M * a.K + 15) & ~15) + sizeof(float) * (a.M * 4 + 32) : 0);
@@ -1006,6 +1091,11 @@ hipError_t launch_gemv(const GemvArgs &a, hipStream_t s) {
     return hipGetLastError();
   }
   const bool two = a.seg[0].epi == EPI_SWIGLU;
+  if (a.M > 16) {  // a batch of rows: plain A operand, no partials, 16-column tiles
+    if (a.pro != PRO_NONE || a.part || !gemv_rows_supported(a.M, a.K, a.group, ncols)) return hipErrorInvalidValue;
+    if (two) return dispatch_rows<2, false>(a, ncols, s);
+    return a.bs_ld ? dispatch_rows<1, true>(a, ncols, s) : dispatch_rows<1, false>(a, ncols, s);
+  }
   if (a.part) return two ? dispatch_part<2>(a, ncols, s) : dispatch_part<1>(a, ncols, s);
   if (two) return dispatch_k<1, 2>(a, ncols, s);
   if (ncols >= 65536) return dispatch_k<4, 1>(a, ncols, s);

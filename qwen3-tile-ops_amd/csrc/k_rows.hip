@@ -189,6 +189,35 @@ __global__ void __launch_bounds__(256) rows1024_kernel(RowArgs a) {
   if (lane == 0) a.hs[static_cast<int64_t>(row) * a.ldhs + (t >> 6)] = scale;
 }
 
+// Quantisation alone (mode 0) of rows whose width is a multiple of 256 with
+// 256-column groups: one wave per (row, group), lane l owns columns 4l..4l+3
+// of the group (the arithmetic of rows1024_kernel's quantisation).
+__global__ void __launch_bounds__(256) quant_groups_kernel(RowArgs a, int ngroups) {
+  const int lane = threadIdx.x & 63;
+  const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (item >= a.rows * ngroups) return;
+  const int row = item / ngroups, g = item % ngroups;
+  const int c0 = 256 * g + 4 * lane;
+  const float4 x = *reinterpret_cast<const float4 *>(a.x + static_cast<int64_t>(row) * a.ldx + c0);
+  float m = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
+  m = max64(m);
+  const float scale = __fmul_rn(m, inv127());
+  const double y = rcp64(scale);
+  char4 q;
+  q.x = static_cast<signed char>(quant_rcp(x.x, y));
+  q.y = static_cast<signed char>(quant_rcp(x.y, y));
+  q.z = static_cast<signed char>(quant_rcp(x.z, y));
+  q.w = static_cast<signed char>(quant_rcp(x.w, y));
+  *reinterpret_cast<char4 *>(a.h8 + static_cast<int64_t>(row) * a.ldh8 + c0) = q;
+  if (lane == 0) a.hs[static_cast<int64_t>(row) * a.ldhs + g] = scale;
+}
+
+bool quant_groups_ok(const RowArgs &a) {
+  auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  return a.mode == 0 && a.h8 && a.group == 256 && a.cols % 256 == 0 && (a.ldx & 3) == 0 && al16(a.x) &&
+         (a.ldh8 & 3) == 0 && (reinterpret_cast<uintptr_t>(a.h8) & 3) == 0;
+}
+
 bool rows1024_ok(const RowArgs &a) {
   auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
   if (a.cols != 1024) return false;
@@ -214,6 +243,13 @@ hipError_t launch_nrq_rows(const NrqArgs &a, hipStream_t s) {
 
 hipError_t launch_rows(const RowArgs &a, hipStream_t s) {
   if (a.rows <= 0) return hipSuccess;
+  if (quant_groups_ok(a)) {
+    const int ngroups = a.cols / 256;
+    const int64_t items = static_cast<int64_t>(a.rows) * ngroups;
+    hipLaunchKernelGGL(quant_groups_kernel, dim3(static_cast<unsigned>((items + 3) / 4)), dim3(256), 0, s, a,
+                       ngroups);
+    return hipGetLastError();
+  }
   if (rows1024_ok(a)) {
     hipLaunchKernelGGL(rows1024_kernel, dim3(a.rows), dim3(256), 0, s, a);
     return hipGetLastError();

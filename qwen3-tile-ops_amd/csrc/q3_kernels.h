@@ -318,9 +318,10 @@ struct NrqArgs {
 };
 hipError_t launch_nrq_rows(const NrqArgs &a, hipStream_t s);
 
-// ---- decode-shaped group GEMM (M <= 16) ---------------------------------
+// ---- decode-shaped group GEMM (M <= 64) ---------------------------------
 // One launch can cover up to three column ranges with their own weights and
-// epilogue (fused Q/K/V).  No grid-wide synchronisation.
+// epilogue (fused Q/K/V).  No grid-wide synchronisation.  Prologues, O
+// partials and the lm_head's column streaming take at most 16 rows.
 enum Pro : int {
   PRO_NONE = 0,   // A operand int8 + scales from global memory
   PRO_NORM = 1,   // A = quant256(rmsnorm(x, w_pre))
@@ -370,6 +371,8 @@ struct GemvArgs {
   int64_t bs_ld;
 };
 bool gemv_supported(int M, int K, int group);
+// 17-64 rows (also 1-16): plain A operand, no partials, fewer than 65536 columns
+bool gemv_rows_supported(int M, int K, int group, int ncols);
 // whether launch_gemv takes per-(row, K-group) B scales for this launch
 bool gemv_group_bscale_supported(const GemvArgs &a);
 // key slots per row that an EPI_ARGMAX launch writes (keys_ld must cover it)

@@ -1142,13 +1142,59 @@ extern "C" int q3_decode_batch(q3_model *m, uint32_t n, const int32_t *ids, cons
     return hip_status(q3::launch_rows(r, s));
   };
   Q3_TRY(rows(2, layer_ptrs(m, 0).n1));
+  // up to 64 rows: the GEMMs run on the 16-column GEMV tiles (every CU
+  // streams a slice of the weights; the rows come from L2), with the head
+  // epilogues and the SwiGLU quantisation as launches of their own
+  const bool gv = q3::gemv_rows_supported(M, H, 256, QW + 2 * KW) && q3::gemv_rows_supported(M, QW, HD, H) &&
+                  q3::gemv_rows_supported(M, I, 256, H) && q3::gemv_rows_supported(M, H, 256, I);
+  float *qf = at<float>(m, y.kQ), *kf = at<float>(m, y.kK), *vf = at<float>(m, y.kV);
+  float *swf = at<float>(m, y.kSW);
   for (uint32_t L = 0; L < y.layers; ++L) {
     const LayerPtrs lp = layer_ptrs(m, L);
     if (L != 0) Q3_TRY(rows(1, lp.n1));
-    // Q | K | V in one tile launch with the head epilogues: Q (norm, RoPE,
-    // quant) into the dense q8/qs rows, K (norm, RoPE, quant) and V (quant)
-    // into each row's page slot at its own position
-    {
+    if (gv) {
+      // Q | K | V rows in f32, then the head epilogues of every (row, head):
+      // Q (norm, RoPE, quant) into the dense q8/qs rows, K (norm, RoPE,
+      // quant) and V (quant) into each row's page slot at its own position
+      q3::GemvArgs g = gemv_args(M, H, 256);
+      g.a = h8;
+      g.lda = H;
+      g.as = hs;
+      g.ldas = H / 256;
+      g.nseg = 3;
+      g.seg[0] = gemv_seg(0, QW, q3::EPI_STORE, lp.wq, lp.wqs, qf, QW);
+      g.seg[1] = gemv_seg(QW, QW + KW, q3::EPI_STORE, lp.wk, lp.wks, kf, KW);
+      g.seg[2] = gemv_seg(QW + KW, QW + 2 * KW, q3::EPI_STORE, lp.wv, lp.wvs, vf, KW);
+      Q3_HIP(q3::launch_gemv(g, s));
+      q3::QkvHeadArgs e;
+      std::memset(&e, 0, sizeof(e));
+      e.M = M;
+      e.q_heads = static_cast<int>(y.heads);
+      e.kv_heads = static_cast<int>(y.kv_heads);
+      e.q = qf;
+      e.k = kf;
+      e.v = vf;
+      e.ldq = QW;
+      e.ldk = KW;
+      e.qd.q8 = q8;
+      e.qd.ldq8 = QW;
+      e.qd.qs = qs;
+      e.qd.ldqs = y.heads;
+      e.qd.qs_col = 1;
+      set_paged(e.kd, m, lp.kc, lp.kcs, 0);
+      set_paged(e.vd, m, lp.vc, lp.vcs, 0);
+      e.nq = lp.nq;
+      e.nk = lp.nk;
+      e.cos_q = e.cos_k = cos_t;
+      e.sin_q = e.sin_k = sin_t;
+      e.ld_cs = HALF;
+      e.inv_hd = 1.0f / static_cast<float>(HD);
+      e.row_pos = m->bpos;
+      e.row_tables = m->btab;
+      e.ld_table = ld_table;
+      Q3_HIP(q3::launch_qkv_heads(e, s));
+    } else {
+      // Q | K | V in one tile launch with the head epilogues, as above
       q3::TileArgs t{};
       t.M = M;
       t.N = QW + 2 * KW;
@@ -1234,7 +1280,16 @@ extern "C" int q3_decode_batch(q3_model *m, uint32_t n, const int32_t *ids, cons
       KTimer kt(m, Q3_KT_ATTN_DECODE);
       Q3_HIP(q3::launch_attn_decode(t, s));
     }
-    {  // O projection + residual
+    if (gv) {  // O projection + residual
+      q3::GemvArgs g = gemv_args(M, QW, HD);
+      g.a = o8;
+      g.lda = QW;
+      g.as = os;
+      g.ldas = y.heads;
+      g.nseg = 1;
+      g.seg[0] = gemv_seg(0, H, q3::EPI_ADD, lp.wo, lp.wos, x, H);
+      Q3_HIP(q3::launch_gemv(g, s));
+    } else {
       q3::GemmArgs g = gemm_args(M, H, QW, HD, o8, os, lp.wo, lp.wos);
       g.ldas = y.heads;
       g.epi = q3::EPI_ADD;
@@ -1243,7 +1298,30 @@ extern "C" int q3_decode_batch(q3_model *m, uint32_t n, const int32_t *ids, cons
       Q3_HIP(q3::launch_gemm(g, s));
     }
     Q3_TRY(rows(1, lp.n2));
-    {  // gate/up + SwiGLU + quant
+    if (gv) {  // gate/up + SwiGLU (f32 rows), then the per-256-column quant
+      q3::GemvArgs g = gemv_args(M, H, 256);
+      g.a = h8;
+      g.lda = H;
+      g.as = hs;
+      g.ldas = H / 256;
+      g.nseg = 1;
+      g.seg[0] = gemv_seg(0, I, q3::EPI_SWIGLU, lp.wg, lp.wgs, swf, I);
+      g.seg[0].b2 = lp.wu;
+      g.seg[0].bs2 = lp.wus;
+      Q3_HIP(q3::launch_gemv(g, s));
+      q3::RowArgs r{};
+      r.mode = 0;
+      r.rows = M;
+      r.cols = I;
+      r.x = swf;
+      r.ldx = I;
+      r.h8 = s8;
+      r.ldh8 = I;
+      r.hs = ss;
+      r.ldhs = I / 256;
+      r.group = 256;
+      Q3_HIP(q3::launch_rows(r, s));
+    } else {  // gate/up + SwiGLU + quant
       q3::GateUpArgs u;
       std::memset(&u, 0, sizeof(u));
       u.M = M;
@@ -1267,7 +1345,16 @@ extern "C" int q3_decode_batch(q3_model *m, uint32_t n, const int32_t *ids, cons
       u.ss_col = 1;
       Q3_HIP(q3::launch_gate_up(u, s));
     }
-    {  // down projection + residual
+    if (gv) {  // down projection + residual
+      q3::GemvArgs g = gemv_args(M, I, 256);
+      g.a = s8;
+      g.lda = I;
+      g.as = ss;
+      g.ldas = I / 256;
+      g.nseg = 1;
+      g.seg[0] = gemv_seg(0, H, q3::EPI_ADD, lp.wd, lp.wds, x, H);
+      Q3_HIP(q3::launch_gemv(g, s));
+    } else {
       q3::GemmArgs g = gemm_args(M, H, I, 256, s8, ss, lp.wd, lp.wds);
       g.epi = q3::EPI_ADD;
       g.out = x;

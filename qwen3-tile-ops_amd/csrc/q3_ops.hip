@@ -117,11 +117,14 @@ int gemm_common(const q3_view *a, const q3_view *a_scale, const q3_view *b,
   return Q3_OK;
 }
 
-// Decode-shaped STORE/ADD/ARGMAX GEMMs go to the whole-chip GEMV kernel.
+// Decode-shaped STORE/ADD/ARGMAX GEMMs (up to 64 rows; more than 16 only
+// below 65536 columns) go to the whole-chip GEMV kernel.
 q3::GemvArgs to_gemv(const q3::GemmArgs &g);
 
 bool use_gemv(const q3::GemmArgs &g) {
-  return q3::gemv_supported(g.M, g.K, g.group) && g.ldb == g.K && g.bs_stride == 1 &&
+  const bool shape = g.M <= 16 ? q3::gemv_supported(g.M, g.K, g.group)
+                               : q3::gemv_rows_supported(g.M, g.K, g.group, g.N);
+  return shape && g.ldb == g.K && g.bs_stride == 1 &&
          (g.epi == q3::EPI_STORE || g.epi == q3::EPI_ADD || g.epi == q3::EPI_ARGMAX) &&
          (!g.bs_ld || q3::gemv_group_bscale_supported(to_gemv(g)));
 }
@@ -518,7 +521,7 @@ int q3_gemm_gate_up_swiglu_quant(const q3_view *a, const q3_view *a_scale,
   // decode shapes: the two-matrix GEMV (SwiGLU rows in f32, on every CU)
   // into the stream's workspace, then the per-256-column quantisation of
   // those rows (quant.h:89-138, the same arithmetic as swiglu_quant.h:197-231)
-  if (u.M <= 16 && u.ldw == u.K && u.ws_stride == 1 && u.ss_col == 1 && q3::gemv_supported(u.M, u.K, u.group) &&
+  if (u.ldw == u.K && u.ws_stride == 1 && u.ss_col == 1 && q3::gemv_rows_supported(u.M, u.K, u.group, u.N) &&
       static_cast<int64_t>(u.M) * u.N * 4 <= kWorkspaceBytes) {
     float *tmp = reinterpret_cast<float *>(stream_keys(s));
     if (!tmp) return Q3_ERR_HIP;
