@@ -291,7 +291,9 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
   const int wave = wave_id();
   const int lr = lane & 15;
   const int lg = lane >> 4;
-  const int M = a.M;
+  // grid row y: rows [row0, row0 + M) of the launch (plain A operand)
+  const int row0 = static_cast<int>(blockIdx.y) * MR;
+  const int M = min(MR, a.M - row0);
   const int K = a.K;
   const int G = a.group;
   const int ngroups = K / G;
@@ -318,6 +320,10 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
     s_bs2[i] = NMAT == 2 ? a.seg[i].bs2 : s_bs[i];
   }
   pin_src<PRO, PART != 0>(ps);
+  if constexpr (PRO == PRO_NONE) {
+    ps.a += static_cast<int64_t>(row0) * ps.lda;
+    ps.as += static_cast<int64_t>(row0) * ps.ldas;
+  }
   nseg = pin_sgpr(nseg);
 #pragma unroll
   for (int i = 0; i < 3; ++i) {
@@ -368,10 +374,24 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
   }
   __builtin_amdgcn_sched_barrier(0);
   // A operand rows and scales of the unfused path (the first AB row tiles),
-  // also before the weights
+  // also before the weights.  With row tiles the A scales of all MR rows go
+  // through LDS instead (asg[r][g], rows past M hold row M - 1's): a few
+  // loads per thread rather than 4 per (tile, group) and lane, which would
+  // overrun the 63 loads that vmcnt can count in flight.
   const bool avalid = lr < M;
   v4i av[AB][GPW][KSTEPS];
   float asv[AB][GPW][4];
+  float *asg = part + part_floats;
+  constexpr int NSG = MT > 1 ? (MR * 4 * GPW + 255) / 256 : 1;  // staged scales per thread
+  float sgv[NSG];
+  if constexpr (MT > 1) {
+#pragma unroll
+    for (int k = 0; k < NSG; ++k) {
+      const int e = min(static_cast<int>(threadIdx.x) + 256 * k, MR * ngroups - 1);
+      const int m = min(e / ngroups, M - 1);
+      sgv[k] = ps.as[static_cast<int64_t>(m) * ps.ldas + e % ngroups];
+    }
+  }
   // row tiles t0 .. t0 + AB - 1; with one tile, rows past M are zeros
   auto load_a = [&](int t0) {
 #pragma unroll
@@ -387,10 +407,12 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
           const v4i v = *reinterpret_cast<const v4i *>(arow + g * G + ks * 64);
           av[tb][gi][ks] = (MT > 1 || ok) ? v : zero4();
         }
+        if constexpr (MT == 1) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int m = min(16 * (t0 + tb) + lg * 4 + i, M - 1);
-          asv[tb][gi][i] = ps.as[static_cast<int64_t>(m) * ps.ldas + g];
+          for (int i = 0; i < 4; ++i) {
+            const int m = min(16 * (t0 + tb) + lg * 4 + i, M - 1);
+            asv[tb][gi][i] = ps.as[static_cast<int64_t>(m) * ps.ldas + g];
+          }
         }
       }
     }
@@ -449,7 +471,7 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
       for (int k = 0; k < MT; ++k) {
         const int it = static_cast<int>(threadIdx.x) + 256 * k;
         const int m = min(it / NB, M - 1);
-        basev[k] = sg.out[static_cast<int64_t>(m) * sg.ldo + (n_blk - sg_n0 + it % NB)];
+        basev[k] = sg.out[static_cast<int64_t>(row0 + m) * sg.ldo + (n_blk - sg_n0 + it % NB)];
       }
     }
   }
@@ -472,6 +494,12 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
       for (int i = 0; i < 4; ++i) asv[0][gi][i] = as_lds[min(lg * 4 + i, M - 1) * (K / 256) + g];
     }
   }
+  if constexpr (MT > 1) {
+#pragma unroll
+    for (int k = 0; k < NSG; ++k)
+      asg[min(static_cast<int>(threadIdx.x) + 256 * k, MR * ngroups - 1)] = sgv[k];
+    lds_barrier();
+  }
   // MFMAs of row tiles t0 .. t0 + AB - 1, dequantised group tiles into LDS
   auto compute = [&](int t0) {
 #pragma unroll
@@ -482,7 +510,12 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
       for (int tb = 0; tb < AB; ++tb) {
         float asv_[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) asv_[i] = (MT > 1 || lg * 4 + i < M) ? asv[tb][gi][i] : 0.0f;
+        for (int i = 0; i < 4; ++i) {
+          if constexpr (MT > 1)
+            asv_[i] = asg[(16 * (t0 + tb) + lg * 4 + i) * ngroups + g];
+          else
+            asv_[i] = lg * 4 + i < M ? asv[tb][gi][i] : 0.0f;
+        }
 #pragma unroll
         for (int mi = 0; mi < NMAT; ++mi)
 #pragma unroll
@@ -533,11 +566,11 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
         const unsigned long long o = lane_xor_u64(key, s);
         key = o > key ? o : key;
       }
-      if (m < M && j == 0) a.keys[static_cast<int64_t>(m) * a.keys_ld + blockIdx.x] = key;
+      if (m < M && j == 0) a.keys[static_cast<int64_t>(row0 + m) * a.keys_ld + blockIdx.x] = key;
       continue;
     }
     if (m >= M) continue;
-    float *dst = sg.out + static_cast<int64_t>(m) * sg.ldo + ncol;
+    float *dst = sg.out + static_cast<int64_t>(row0 + m) * sg.ldo + ncol;
     if (sg.epi == EPI_ADD) {
       float base = MT > 1 ? basev[k] : *dst;
       if constexpr (NEPI > 0) {
@@ -899,13 +932,15 @@ __global__ void __launch_bounds__(256) qkv_heads_kernel(QkvHeadArgs a) {
 }
 
 template <int GPW, int KSTEPS, int NT, int NMAT, int PRO, int PART, bool BSG = false, int MT = 1, int AB = MT>
-hipError_t launch_t(const GemvArgs &a, int ncols, hipStream_t s) {
+hipError_t launch_t(const GemvArgs &a, int ncols, hipStream_t s, int ry = 1) {
   constexpr int NB = 16 * NT;
   // the prologue gives each wave GPW * KSTEPS / 4 groups of 256 columns
   if (PRO != PRO_NONE && a.K != 256 * GPW * KSTEPS) return hipErrorInvalidValue;
-  if (a.M > 16 * MT) return hipErrorInvalidValue;
+  if (a.M > 16 * MT * ry || (ry > 1 && PRO != PRO_NONE)) return hipErrorInvalidValue;
   const int ngroups = a.K / a.group;
+  if (MT > 1 && ngroups != 4 * GPW) return hipErrorInvalidValue;  // the scale staging covers 4 * GPW groups
   size_t lds = sizeof(float) * NMAT * ngroups * 16 * MT * (NB + 1);
+  if (MT > 1) lds += sizeof(float) * 16 * MT * ngroups;  // the staged A scales
   if (PRO != PRO_NONE)
     lds += ((a.M * a.K + 15) & ~15) + sizeof(float) * (a.M * (a.K / 256) + a.K / 32);
   // dynamic LDS beyond 64 KiB (row tiles) must be allowed once; the kernel's
@@ -922,19 +957,27 @@ hipError_t launch_t(const GemvArgs &a, int ncols, hipStream_t s) {
       attr_set = true;
     }
   }
-  Q3_LAUNCH((gemv_kernel<GPW, KSTEPS, NT, NMAT, PRO, PART, BSG, MT, AB>), dim3(ncols / NB), dim3(256), lds, s, a);
+  Q3_LAUNCH((gemv_kernel<GPW, KSTEPS, NT, NMAT, PRO, PART, BSG, MT, AB>), dim3(ncols / NB, ry), dim3(256), lds, s, a);
   return hipGetLastError();
 }
 
-// 17-64 rows (plain A operand, 16-column tiles): 2 or 4 row tiles; with
-// three groups per wave (K = 3072) the A fragments of 4 tiles come in two
-// batches so that they and the weights fit the register file.
+// 17-64 rows (plain A operand, 16-column tiles).  A workgroup streams its
+// weights and every row of A it covers, and a CU has only so many cache
+// lines in flight, so the rows are split between workgroups until the grid
+// fills the chip: narrow launches (O, down: 64 column tiles) run one 16-row
+// tile per workgroup in grid rows; wide ones (Q|K|V, gate/up) run 2 or 4
+// row tiles per workgroup over the same weight registers.  With three
+// groups per wave (K = 3072) the A fragments of 4 tiles come in two batches
+// so that they and the weights fit the register file.
 template <int NMAT, bool BSG>
 hipError_t dispatch_rows(const GemvArgs &a, int ncols, hipStream_t s) {
   const bool four = a.M > 32;
-#define Q3_ROWS(GPW, KS)                                                                     \
-  return four ? launch_t<GPW, KS, 1, NMAT, PRO_NONE, 0, BSG, 4, (GPW * KS > 8 ? 2 : 4)>(a, ncols, s) \
-              : launch_t<GPW, KS, 1, NMAT, PRO_NONE, 0, BSG, 2, 2>(a, ncols, s)
+  const int ry = (a.M + 15) / 16;
+  const bool split = (ncols / 16) * ry <= 512;
+#define Q3_ROWS(GPW, KS)                                                                               \
+  return split ? launch_t<GPW, KS, 1, NMAT, PRO_NONE, 0, BSG>(a, ncols, s, ry)                         \
+         : four ? launch_t<GPW, KS, 1, NMAT, PRO_NONE, 0, BSG, 4, (GPW * KS > 8 ? 2 : 4)>(a, ncols, s) \
+                : launch_t<GPW, KS, 1, NMAT, PRO_NONE, 0, BSG, 2, 2>(a, ncols, s)
   if (a.K == 1024 && a.group == 256) Q3_ROWS(1, 4);
   if (a.K == 1024 && a.group == 128) Q3_ROWS(2, 2);
   if (a.K == 2048 && a.group == 128) Q3_ROWS(4, 2);
