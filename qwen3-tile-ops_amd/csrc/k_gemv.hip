@@ -963,21 +963,23 @@ hipError_t launch_t(const GemvArgs &a, int ncols, hipStream_t s, int ry = 1) {
 
 // 17-64 rows (plain A operand, 16-column tiles).  A workgroup streams its
 // weights and every row of A it covers, and a CU has only so many cache
-// lines in flight, so the rows are split between workgroups until the grid
-// fills the chip: narrow launches (O, down: 64 column tiles) run one 16-row
-// tile per workgroup in grid rows; wide ones (Q|K|V, gate/up) run 2 or 4
-// row tiles per workgroup over the same weight registers.  With three
-// groups per wave (K = 3072) the A fragments of 4 tiles come in two batches
-// so that they and the weights fit the register file.
+// lines in flight, so the rows are split between workgroups (grid rows)
+// until the grid holds about two workgroups per CU: narrow launches (O,
+// down: 64 column tiles) run one 16-row tile per workgroup, wide ones
+// (Q|K|V, gate/up at 64 rows) 2 row tiles over the same weight registers
+// (4 when even 2 would exceed that grid).  With three groups per wave
+// (K = 3072) the A fragments of 4 tiles come in two batches so that they
+// and the weights fit the register file.
 template <int NMAT, bool BSG>
 hipError_t dispatch_rows(const GemvArgs &a, int ncols, hipStream_t s) {
-  const bool four = a.M > 32;
-  const int ry = (a.M + 15) / 16;
-  const bool split = (ncols / 16) * ry <= 512;
+  constexpr int kMaxWgs = 512;  // fewest row tiles per workgroup that keep the grid within this
+  const int cb = ncols / 16;
+  const int r1 = (a.M + 15) / 16, r2 = (a.M + 31) / 32;
+  const int mt = cb * r1 <= kMaxWgs ? 1 : cb * r2 <= kMaxWgs ? 2 : 4;
 #define Q3_ROWS(GPW, KS)                                                                               \
-  return split ? launch_t<GPW, KS, 1, NMAT, PRO_NONE, 0, BSG>(a, ncols, s, ry)                         \
-         : four ? launch_t<GPW, KS, 1, NMAT, PRO_NONE, 0, BSG, 4, (GPW * KS > 8 ? 2 : 4)>(a, ncols, s) \
-                : launch_t<GPW, KS, 1, NMAT, PRO_NONE, 0, BSG, 2, 2>(a, ncols, s)
+  return mt == 1 ? launch_t<GPW, KS, 1, NMAT, PRO_NONE, 0, BSG>(a, ncols, s, r1)                       \
+         : mt == 2 ? launch_t<GPW, KS, 1, NMAT, PRO_NONE, 0, BSG, 2, 2>(a, ncols, s, r2)               \
+                : launch_t<GPW, KS, 1, NMAT, PRO_NONE, 0, BSG, 4, (GPW * KS > 8 ? 2 : 4)>(a, ncols, s, 1)
   if (a.K == 1024 && a.group == 256) Q3_ROWS(1, 4);
   if (a.K == 1024 && a.group == 128) Q3_ROWS(2, 2);
   if (a.K == 2048 && a.group == 128) Q3_ROWS(4, 2);
