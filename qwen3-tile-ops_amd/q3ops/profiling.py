@@ -58,6 +58,9 @@ CLASS_OF = [
     (r"gemv_kernel<4, 2, 1, 1,", "gemv_o"),
     (r"gemv_kernel<1, 4, 1, 2, 1, 1", "gemv_gate_up"),
     (r"gemv_kernel<3, 4, 1, 1, 2, 2", "gemv_down"),
+    (r"gemv_kernel<1, 4, 1, 1, 0, 0, \w+, [24],", "batch_qkv"),
+    (r"gemv_kernel<1, 4, 1, 2, 0, 0, \w+, [24],", "batch_gate_up"),
+    (r"gemv_kernel<3, 4, 1, 1, 0, 0,", "batch_down"),
     (r"gemv_row_kernel<1, 4", "lm_head"),
     (r"gemv_stream_kernel<", "lm_head_rows"),
     (r"gemm_tile_kernel<\d+, \d+, \d+, 2, \d+, \d+, 6,", "prefill_gate_up"),
@@ -72,6 +75,9 @@ CLASS_OF = [
     (r"attn_prefill_kernel", "prefill_attention"),
     (r"attention_kernel", "prefill_attention"),
     (r"rows1024_kernel", "norm_quant_rows"),
+    (r"quant_groups_kernel", "quant_rows"),
+    (r"qkv_heads_kernel", "qkv_heads"),
+    (r"gemm_tile_kernel<(\d+, ){6}4,", "lm_head_batch"),
     (r"argmax_finish_kernel", "argmax_finish"),
 ]
 
