@@ -130,8 +130,8 @@ def test_gemm_group_bscale_residual_config1(cuda, M, K, N, group):
 @pytest.mark.parametrize("M", [1, 5, 16, 17, 64, 300])
 def test_gemm_group_bscale_store(cuda, M):
     """Per-(row, group) B scales with the plain store, on every GEMM path
-    (M <= 16: the GEMV kernel; 17..64: 32-column tiles; above: 128-column
-    tiles), at both group sizes."""
+    (M <= 64: the GEMV kernel, with row tiles above 16; above: the
+    prefill-shaped kernels), at both group sizes."""
     for K, N, group in ((1024, 2048, 256), (2048, 1024, 128)):
         rng = np.random.default_rng(M + K)
         a, as_, b, _ = rand_gemm(rng, M, K, N, group)
@@ -442,6 +442,49 @@ def test_lm_argmax_two_streams(cuda):
         logits = oracle.gemm_nt_group(a, as_, b, bs, 256)
         assert bidx.cpu().numpy().tolist() == [int(i) for i in np.argmax(logits, axis=1)]
         assert bits_equal(best.cpu().numpy(), logits.max(axis=1))
+
+
+# 17-64 rows on the GEMV kernel: each way of splitting the rows (one 16-row
+# tile per workgroup in grid rows; 2 tiles per workgroup; 4 tiles with the A
+# fragments in one batch or, at three groups per wave, in two), at both
+# group sizes, with rows past M inside a workgroup's last tile
+ROW_TILE_CASES = [
+    ("split", 20, 3072, 1024, 256),
+    ("mt2", 48, 1024, 4096, 256),
+    ("mt2_g128", 33, 1024, 4096, 128),
+    ("mt4_two_batches", 64, 3072, 4224, 256),
+    ("mt4_g128", 40, 2048, 4224, 128),
+]
+
+
+@pytest.mark.parametrize("case,M,K,N,group", ROW_TILE_CASES)
+def test_gemm_row_tiles(cuda, case, M, K, N, group):
+    """Store, residual add, per-(row, group) B scales and the argmax key
+    epilogue of the row-tiled GEMV against the oracle, bit for bit."""
+    note(f"gemm row tiles {case} M={M} K={K} N={N} g={group}")
+    rng = np.random.default_rng(131 * M + K + N + group)
+    a, as_, b, bs = rand_gemm(rng, M, K, N, group)
+    ref = oracle.gemm_nt_group(a, as_, b, bs, group)
+    out = torch.zeros((M, N), dtype=torch.float32, device=cuda)
+    ops.gemm_nt_group_store(dev(a), dev(as_), dev(b), dev(bs), out, group)
+    got = host(out)
+    assert bits_equal(got, ref), ("store", describe_diff(got, ref))
+    x = rng.normal(size=(M, N)).astype(F)
+    xt = dev(x)
+    ops.gemm_nt_group_store(dev(a), dev(as_), dev(b), dev(bs), None, group, add=xt)
+    got = host(xt)
+    exp = (ref + x).astype(F)
+    assert bits_equal(got, exp), ("residual", describe_diff(got, exp))
+    bsg = rng.uniform(1e-3, 1e-1, (N, K // group)).astype(F)
+    ops.gemm_nt_group_store(dev(a), dev(as_), dev(b), dev(bsg), out, group)
+    got = host(out)
+    exp = oracle.gemm_nt_group_bg(a, as_, b, bsg, group)
+    assert bits_equal(got, exp), ("group B scales", describe_diff(got, exp))
+    best = torch.full((M,), -3.0e38, dtype=torch.float32, device=cuda)
+    bidx = torch.zeros(M, dtype=torch.int32, device=cuda)
+    ops.gemm_nt_group_argmax(dev(a), dev(as_), dev(b), dev(bs), best, bidx, group)
+    assert host(bidx).tolist() == [int(i) for i in np.argmax(ref, axis=1)]
+    assert bits_equal(host(best), ref.max(axis=1))
 
 
 @pytest.mark.parametrize("M", [2, 5, 16, 33, 64, 100])
