@@ -487,7 +487,7 @@ def test_gemm_row_tiles(cuda, case, M, K, N, group):
     assert bits_equal(host(best), ref.max(axis=1))
 
 
-@pytest.mark.parametrize("M", [2, 5, 16, 33, 64, 100])
+@pytest.mark.parametrize("M", [2, 5, 16, 20, 33, 64, 100])
 def test_lm_argmax_wide_multirow(cuda, M):
     """lm_head width with several rows: one running key per row and
     workgroup across the column tiles each workgroup walks (M <= 16), one key
