@@ -180,8 +180,13 @@ def run_batch_case(cuda, n, lay, blob, ctx, tables, dense, ids0):
     assert not probs, probs
 
 
-@pytest.mark.parametrize("n", [1, 5, 20, 64])
+@pytest.mark.parametrize("n", [1, 5, 16, 17, 20, 40, 64])
 def test_decode_batch_matches_oracle(cuda, n):
+    """One batched greedy step of n sequences against the oracle, stage by
+    stage.  16/17 straddle the GEMV's one-tile/row-tile boundary; 20 and 40
+    leave a workgroup's last row tile partly past n (one 16-row tile per
+    workgroup in grid rows for the narrow launches, two per workgroup for
+    Q|K|V and gate/up at 40)."""
     note(f"decode_batch n={n}")
     run_batch_case(cuda, n, *make_case(n, seed=100 + n))
 
