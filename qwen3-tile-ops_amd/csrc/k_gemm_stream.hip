@@ -306,11 +306,15 @@ __global__ void __launch_bounds__(NWN * KP * 64) gemm_stream_kernel(TileArgs a) 
   };
 
   // the slice s of this wave: MFMAs on it from ring slot `slot` into
-  // buffer `par`, then slice s + D into that slot
-  auto slice = [&](auto SLOT, auto PAR, int s) {
+  // buffer `par`, then (ISSUE) slice s + D into that slot.  AFTER: slices
+  // issued after this one (D - 1, fewer near the end, where no slice past
+  // the wave's last is issued: a wave cannot finish, nor pass a barrier,
+  // before every load it issued has returned)
+  auto slice = [&](auto SLOT, auto PAR, auto AFTER, auto ISSUE, int s) {
     constexpr int slot = decltype(SLOT)::value;
     constexpr int par = decltype(PAR)::value;
-    wait_vmcnt<(D - 1) * S::LPS>();
+    constexpr int after = decltype(AFTER)::value;
+    wait_vmcnt<after * S::LPS>();
     v4i af[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -323,17 +327,20 @@ __global__ void __launch_bounds__(NWN * KP * 64) gemm_stream_kernel(TileArgs a) 
         for (int nt = 0; nt < NT; ++nt)
           c[par][mi][mt][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[mt], ring[slot][mi][nt],
                                                                        c[par][mi][mt][nt], 0, 0, 0);
-    issue(std::integral_constant<int, slot>{}, s + D);
+    if constexpr (decltype(ISSUE)::value) issue(std::integral_constant<int, slot>{}, s + D);
   };
 
   if constexpr (KP == 1) {
     // 3. main loop, GPB groups per iteration; group g accumulates in buffer
-    //    g & 1, and slice s of the kernel lives in ring slot s % D
-#pragma unroll 1
-    for (int g0 = 0; g0 < NG; g0 += GPB) {
+    //    g & 1, and slice s of the kernel lives in ring slot s % D; the last
+    //    iteration (LAST) issues no slice past the end
+    auto body = [&](auto LAST, int g0) {
       static_for<BODY>([&](auto J) {
         constexpr int j = decltype(J)::value;
+        constexpr bool last = decltype(LAST)::value;
+        constexpr int after = last ? (D - 1 < BODY - 1 - j ? D - 1 : BODY - 1 - j) : D - 1;
         slice(std::integral_constant<int, j % D>{}, std::integral_constant<int, (j / SPG) & 1>{},
+              std::integral_constant<int, after>{}, std::integral_constant<bool, !last || j + D < BODY>{},
               g0 * SPG + j);
         // at a group's first slice: the previous group, whose MFMAs are all
         // issued, is dequantised while these run
@@ -342,7 +349,10 @@ __global__ void __launch_bounds__(NWN * KP * 64) gemm_stream_kernel(TileArgs a) 
           if (g > 0) dequant(std::integral_constant<int, ((j / SPG) & 1) ^ 1>{}, g - 1);
         }
       });
-    }
+    };
+#pragma unroll 1
+    for (int g0 = 0; g0 < NG - GPB; g0 += GPB) body(std::false_type{}, g0);
+    body(std::true_type{}, NG - GPB);
     dequant(std::integral_constant<int, (NG - 1) & 1>{}, NG - 1);
   } else {
     // 3'. K partitions: the wave's GPP groups, each dequantised into a
@@ -354,7 +364,9 @@ __global__ void __launch_bounds__(NWN * KP * 64) gemm_stream_kernel(TileArgs a) 
       constexpr int gi = decltype(GI)::value;
       static_for<SPG>([&](auto J) {
         constexpr int j = gi * SPG + decltype(J)::value;
-        slice(std::integral_constant<int, j % D>{}, std::integral_constant<int, 0>{}, j);
+        constexpr int after = D - 1 < S::SW - 1 - j ? D - 1 : S::SW - 1 - j;
+        slice(std::integral_constant<int, j % D>{}, std::integral_constant<int, 0>{},
+              std::integral_constant<int, after>{}, std::integral_constant<bool, (j + D < S::SW)>{}, j);
       });
       dequant(std::integral_constant<int, 0>{}, kp * GPP + gi);
 #pragma unroll
