@@ -10,9 +10,11 @@
 // (row, column) per thread adds the groups in order.  Workgroups never wait
 // for each other: there are no grid-wide dependencies, fences or contended
 // atomics in this kernel.  Batches of 17-64 rows (independent sequences
-// decoding together) run as MT = 2 or 4 tiles of 16 rows over the same
-// weight registers: a weight byte is loaded once per workgroup whatever M
-// is, and the A operand (M x K, read by every workgroup) comes from L2.
+// decoding together) run either as MT = 2 or 4 tiles of 16 rows over the
+// same weight registers (each weight byte loaded once per workgroup) or as
+// one 16-row tile per workgroup in grid rows (each weight byte loaded once
+// per grid row, a quarter of A per workgroup); dispatch_rows picks per
+// launch width.  The A operand comes from L2.
 //
 // Prologue (consumer-side quantisation): instead of reading a pre-quantised
 // int8 A operand, the workgroup may build it in LDS from f32 rows
