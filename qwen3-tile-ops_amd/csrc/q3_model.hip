@@ -702,6 +702,47 @@ int qkv_projections(q3_model *m, const LayerPtrs &lp, uint32_t pos, uint32_t row
   const float *cos_t = at<const float>(m, y.kCOS);
   const float *sin_t = at<const float>(m, y.kSIN);
   const float inv_hd = 1.0f / static_cast<float>(HD);
+  if (do_tail && tr0 == 0 && tr == rows && rows <= 64 &&
+      q3::gemv_rows_supported(static_cast<int>(rows), H, 256, QW + 2 * KW)) {
+    // up to 64 rows: Q | K | V rows in f32 on the GEMV tiles, then the head
+    // epilogues of every (row, head) (Q into q8/qs, K and V into the page
+    // slots of positions pos + row)
+    float *qf = at<float>(m, y.kQ), *kf = at<float>(m, y.kK), *vf = at<float>(m, y.kV);
+    q3::GemvArgs g = gemv_args(static_cast<int>(rows), H, 256);
+    g.a = h8;
+    g.lda = H;
+    g.as = hs;
+    g.ldas = H / 256;
+    g.nseg = 3;
+    g.seg[0] = gemv_seg(0, QW, q3::EPI_STORE, lp.wq, lp.wqs, qf, QW);
+    g.seg[1] = gemv_seg(QW, QW + KW, q3::EPI_STORE, lp.wk, lp.wks, kf, KW);
+    g.seg[2] = gemv_seg(QW + KW, QW + 2 * KW, q3::EPI_STORE, lp.wv, lp.wvs, vf, KW);
+    Q3_HIP(q3::launch_gemv(g, s));
+    q3::QkvHeadArgs e;
+    std::memset(&e, 0, sizeof(e));
+    e.M = static_cast<int>(rows);
+    e.q_heads = static_cast<int>(y.heads);
+    e.kv_heads = static_cast<int>(y.kv_heads);
+    e.q = qf;
+    e.k = kf;
+    e.v = vf;
+    e.ldq = QW;
+    e.ldk = KW;
+    e.qd.q8 = q8;
+    e.qd.ldq8 = QW;
+    e.qd.qs = qs;
+    e.qd.ldqs = y.heads;
+    e.qd.qs_col = 1;
+    set_paged(e.kd, m, lp.kc, lp.kcs, pos);
+    set_paged(e.vd, m, lp.vc, lp.vcs, pos);
+    e.nq = lp.nq;
+    e.nk = lp.nk;
+    e.cos_q = e.cos_k = cos_t + static_cast<int64_t>(pos) * HALF;
+    e.sin_q = e.sin_k = sin_t + static_cast<int64_t>(pos) * HALF;
+    e.ld_cs = HALF;
+    e.inv_hd = inv_hd;
+    return hip_status(q3::launch_qkv_heads(e, s));
+  }
   if (do_tail && tr0 == 0 && tr == rows) {
     // Q | K | V as one launch (3x the workgroups of each alone), each column
     // segment with its own weights, epilogue and destination
@@ -881,8 +922,21 @@ int forward_chunk_impl(q3_model *m, uint32_t pos, uint32_t rows, int lm_out,
         Q3_HIP(q3::launch_attention(t, s));
     }
     float *xt = x + static_cast<int64_t>(tr0) * H;
+    // up to 64 rows: the GEMMs below on the GEMV tiles (the gate/up as
+    // SwiGLU rows in f32, then their per-256-column quant)
+    const bool gv = M <= 64 && q3::gemv_rows_supported(M, QW, HD, H) && q3::gemv_rows_supported(M, H, 256, I) &&
+                    q3::gemv_rows_supported(M, I, 256, H);
     // O projection (group = head_dim) + residual into x
-    {
+    if (gv) {
+      q3::GemvArgs g = gemv_args(M, QW, HD);
+      g.a = o8 + static_cast<int64_t>(tr0) * QW;
+      g.lda = QW;
+      g.as = os + static_cast<int64_t>(tr0) * y.heads;
+      g.ldas = y.heads;
+      g.nseg = 1;
+      g.seg[0] = gemv_seg(0, H, q3::EPI_ADD, lp.wo, lp.wos, xt, H);
+      Q3_HIP(q3::launch_gemv(g, s));
+    } else {
       q3::GemmArgs g = gemm_args(M, H, QW, HD, o8 + static_cast<int64_t>(tr0) * QW,
                                  os + static_cast<int64_t>(tr0) * y.heads, lp.wo, lp.wos);
       g.epi = q3::EPI_ADD;
@@ -942,13 +996,47 @@ int forward_chunk_impl(q3_model *m, uint32_t pos, uint32_t rows, int lm_out,
       t.ss = u.ss;
       t.ldss = I / 256;
       t.ss_col = 1;
-      if (lp.pg && q3::gemm_stream_supported(t, q3::EPI_SWIGLUQ))
+      if (gv) {
+        float *swf = at<float>(m, y.kSW) + static_cast<int64_t>(tr0) * I;
+        q3::GemvArgs g = gemv_args(M, H, 256);
+        g.a = u.a;
+        g.lda = H;
+        g.as = u.as;
+        g.ldas = H / 256;
+        g.nseg = 1;
+        g.seg[0] = gemv_seg(0, I, q3::EPI_SWIGLU, lp.wg, lp.wgs, swf, I);
+        g.seg[0].b2 = lp.wu;
+        g.seg[0].bs2 = lp.wus;
+        Q3_HIP(q3::launch_gemv(g, s));
+        q3::RowArgs r{};
+        r.mode = 0;
+        r.rows = M;
+        r.cols = I;
+        r.x = swf;
+        r.ldx = I;
+        r.h8 = u.s8;
+        r.ldh8 = I;
+        r.hs = u.ss;
+        r.ldhs = I / 256;
+        r.group = 256;
+        Q3_HIP(q3::launch_rows(r, s));
+      } else if (lp.pg && q3::gemm_stream_supported(t, q3::EPI_SWIGLUQ)) {
         Q3_HIP(q3::launch_gemm_stream(t, q3::EPI_SWIGLUQ, s));
-      else
+      } else {
         Q3_HIP(q3::launch_gate_up(u, s));
+      }
     }
     // down projection + residual into x
-    {
+    if (gv) {
+      q3::GemvArgs g = gemv_args(M, I, 256);
+      g.a = s8 + static_cast<int64_t>(tr0) * I;
+      g.lda = I;
+      g.as = ss + static_cast<int64_t>(tr0) * (I / 256);
+      g.ldas = I / 256;
+      g.nseg = 1;
+      g.seg[0] = gemv_seg(0, H, q3::EPI_ADD, lp.wd, lp.wds, xt, H);
+      Q3_HIP(q3::launch_gemv(g, s));
+    } else {
       q3::GemmArgs g = gemm_args(M, H, I, 256, s8 + static_cast<int64_t>(tr0) * I,
                                  ss + static_cast<int64_t>(tr0) * (I / 256), lp.wd, lp.wds);
       g.epi = q3::EPI_ADD;
