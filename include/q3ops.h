@@ -17,7 +17,7 @@
  *    ops are asynchronous and stream-ordered and none synchronises.  None
  *    allocates, except that the first call on a stream of
  *    q3_gemm_nt_group_argmax, or of q3_gemm_gate_up_swiglu_quant with at most
- *    16 rows, allocates that stream's 4 MiB workspace (kept until the
+ *    64 rows, allocates that stream's 4 MiB workspace (kept until the
  *    process ends; calls on one stream share it in stream order).
  *  - Every function returns an int status: Q3_OK (0) or a negative Q3_ERR_*.
  *    The reference silently returns on unsupported shapes
@@ -183,9 +183,10 @@ int q3_attention_heads_gqa_tokscale_paged(const q3_view *q8,
 /* kernels/swiglu_quant.h:164-255 gemm_gate_up_swiglu_quant(a, a_scale, wg,
  * wgs, wu, wus, s8, ss, group_k): g/u as gemm_nt_group_store,
  * sw = RN(RN(g * RN(1/RN(exp(-g)+1))) * u), then per-256-column int8 quant
- * into s8 [M][I] / ss [M][I/256].  With M <= 16 (contiguous weight rows,
- * per-row weight scales, I <= 65536) the SwiGLU rows pass through the
- * stream's workspace between a GEMV over every CU and the quantisation. */
+ * into s8 [M][I] / ss [M][I/256].  With M <= 64 (contiguous weight rows,
+ * per-row weight scales, I < 65536, M * I * 4 bytes within the 4 MiB
+ * workspace) the SwiGLU rows pass through the stream's workspace between a
+ * GEMV over every CU and the quantisation. */
 int q3_gemm_gate_up_swiglu_quant(const q3_view *a, const q3_view *a_scale,
                                  const q3_view *wg, const q3_view *wgs,
                                  const q3_view *wu, const q3_view *wus,
