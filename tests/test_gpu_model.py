@@ -169,6 +169,23 @@ def test_cfg0_chunk_and_page_invariance(cuda):
     m.close()
 
 
+@pytest.mark.parametrize("seq", [17, 20, 33, 48])
+def test_cfg0_prompt_chunk_sizes(cuda, seq):
+    """The 40-token prompt in chunks of at most `seq` rows (17+17+6, 20+20,
+    33+7, 40): the GEMV row splits of 17-64-row chunks and the single-row
+    and block-sized remainders give the reference's ids and logits."""
+    g = load_cfg("cfg0")
+    shape = ModelShape(layers=1, vocab=1024, seq=seq, max_seq=256)
+    lay, blob = host_blob("cfg0", shape=shape)
+    m = Model(lay, blob)
+    m.set_ctrl(40, 2, 1)
+    m.generate()
+    assert np.array_equal(m.ids()[40:42], g["generated"])
+    got = m.stage("logits", 1)[0]
+    assert bits_equal(got, g["logits"]), describe_diff(got, g["logits"])
+    m.close()
+
+
 def test_cfg2_full_depth(cuda, gold_meta):
     note("cfg2 28 layers, 32-token prefill, mode 1")
     lay, blob = host_blob("cfg2")
