@@ -37,7 +37,7 @@ LD_TABLE = 8  # pages per sequence table (contexts up to 254 tokens + 2 steps)
 # the steps); the longest needs 65 table entries.
 LONG_CTX = [383, 384, 385, 767, 768, 769, 1535, 2046, 2047, 2048]
 LD_TABLE_LONG = 66
-SHAPE = ModelShape(layers=2, vocab=1024, seq=64, max_seq=32768)
+SHAPE = ModelShape(layers=2, vocab=1024, seq=96, max_seq=32768)
 INIT = InitConfig(n_prompt=1, n_gen=0, mode=0)
 _cache = {}
 
@@ -180,13 +180,13 @@ def run_batch_case(cuda, n, lay, blob, ctx, tables, dense, ids0):
     assert not probs, probs
 
 
-@pytest.mark.parametrize("n", [1, 5, 16, 17, 20, 40, 64])
+@pytest.mark.parametrize("n", [1, 5, 16, 17, 20, 40, 64, 80])
 def test_decode_batch_matches_oracle(cuda, n):
     """One batched greedy step of n sequences against the oracle, stage by
     stage.  16/17 straddle the GEMV's one-tile/row-tile boundary; 20 and 40
     leave a workgroup's last row tile partly past n (one 16-row tile per
     workgroup in grid rows for the narrow launches, two per workgroup for
-    Q|K|V and gate/up at 40)."""
+    Q|K|V and gate/up at 40); 80 takes the prefill-shaped GEMMs."""
     note(f"decode_batch n={n}")
     run_batch_case(cuda, n, *make_case(n, seed=100 + n))
 
