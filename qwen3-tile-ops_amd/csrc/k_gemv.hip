@@ -867,6 +867,71 @@ __global__ void __launch_bounds__(256) gemv_row_kernel(GemvArgs a, int N) {
   }
 }
 
+// M = 1, per-256 quant prologue and residual add (the decode down
+// projection, K = 1024 KB): one whole weight row per wave, lane l holding
+// bytes k = 1024 j + 16 l .. + 15 (contiguous 1 KB per load instruction),
+// on N / 4 workgroups (every CU for the 1024 rows of the model).  Per row:
+// v_dot4 partials (exact int32), the 16 lanes of each 256-column group
+// g = 4 j + l / 16 summed with DPP (exact), then the group GEMM's arithmetic
+// p_g = RN(RN(f32(I_g) * bs[n]) * as_g), out = (((0 + p_0) + p_1) + ...) in
+// ascending g, and the residual add of gemv_kernel's EPI_ADD:
+// dst = (dst + o) + out, o the O partials summed in head order (NEPI).
+template <int KB, int NEPI>
+__global__ void __launch_bounds__(256) gemv_wr_kernel(GemvArgs a, int N) {
+  __shared__ float blk[32];
+  __shared__ __align__(16) int8_t a_lds[1024 * KB];
+  __shared__ float as_lds[4 * KB];
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_id();
+  const GemvSeg &sg = a.seg[0];
+  ProSrc ps = read_src<PRO_QUANT, NEPI != 0>(a);
+  pin_src<PRO_QUANT, NEPI != 0>(ps);
+  ProRow<KB, 0> r0;
+  pro_load_row<PRO_QUANT, KB, 0>(a, ps, 0, r0);
+  __builtin_amdgcn_sched_barrier(0);  // (issue order: prologue operands first)
+  const int row = static_cast<int>(blockIdx.x) * 4 + wave;
+  const int n = min(row, N - 1);
+  // the row's residual, its O partials (lane h < 16: partial h) and scale,
+  // then its weights
+  const float xv = sg.out[n];
+  float pv = 0.0f;
+  if constexpr (NEPI > 0) pv = ps.part[min(lane & 15, ps.npart - 1) * ps.ld_part + n];
+  const float bsn = sg.bs[n];
+  int4 w[KB];
+#pragma unroll
+  for (int j = 0; j < KB; ++j)
+    w[j] = *reinterpret_cast<const int4 *>(sg.b + static_cast<int64_t>(n) * (1024 * KB) + 1024 * j + 16 * lane);
+  __builtin_amdgcn_sched_barrier(0);
+  pro_compute_row<PRO_QUANT, KB, 0>(a, 0, r0, a_lds, as_lds, blk);  // ends with a barrier
+  float out = 0.0f;
+#pragma unroll
+  for (int j = 0; j < KB; ++j) {
+    const int4 av = *reinterpret_cast<const int4 *>(a_lds + 1024 * j + 16 * lane);
+    int acc = sdot4(w[j].x, av.x, 0);
+    acc = sdot4(w[j].y, av.y, acc);
+    acc = sdot4(w[j].z, av.z, acc);
+    acc = sdot4(w[j].w, av.w, acc);
+    acc += lane_xor<1>(acc);
+    acc += lane_xor<2>(acc);
+    acc += lane_xor<4>(acc);
+    acc += lane_xor<8>(acc);
+    const float p = __fmul_rn(__fmul_rn(static_cast<float>(acc), bsn), as_lds[4 * j + (lane >> 4)]);
+    out = __fadd_rn(out, lane_bcast<0>(p));
+    out = __fadd_rn(out, lane_bcast<16>(p));
+    out = __fadd_rn(out, lane_bcast<32>(p));
+    out = __fadd_rn(out, lane_bcast<48>(p));
+  }
+  float base = xv;
+  if constexpr (NEPI > 0) {
+    float o = 0.0f;  // the O projection, partials in head order
+#pragma unroll
+    for (int h = 0; h < NEPI; ++h)
+      if (h < ps.npart) o = __fadd_rn(o, __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(pv), h)));
+    base = __fadd_rn(base, o);
+  }
+  if (lane == 0 && row < N) sg.out[n] = __fadd_rn(base, out);
+}
+
 // Per (row, head) wave: the head epilogues of the Q/K/V projections
 // (kernels/norm_rope_quant.h:17-86, group_gemm.h:173-193), from f32 rows.
 __global__ void __launch_bounds__(256) qkv_heads_kernel(QkvHeadArgs a) {
@@ -1044,7 +1109,13 @@ hipError_t dispatch_part(const GemvArgs &a, int ncols, hipStream_t s) {
   if constexpr (NMAT == 2) {
     if (pro && a.K == 1024) return launch_t<1, 4, 1, NMAT, PRO_NORM, kPartPro>(a, ncols, s);
   } else {
-    if (epi && a.K == 3072 && a.pro == PRO_QUANT) return launch_t<3, 4, 1, NMAT, PRO_QUANT, kPartEpi>(a, ncols, s);
+    if (epi && a.K == 3072 && a.pro == PRO_QUANT) {
+      if (ncols % 4 == 0) {  // whole weight rows, a row per wave
+        Q3_LAUNCH((gemv_wr_kernel<3, kMaxPart>), dim3(ncols / 4), dim3(256), 0, s, a, ncols);
+        return hipGetLastError();
+      }
+      return launch_t<3, 4, 1, NMAT, PRO_QUANT, kPartEpi>(a, ncols, s);
+    }
   }
   return hipErrorInvalidValue;
 }
