@@ -867,69 +867,127 @@ __global__ void __launch_bounds__(256) gemv_row_kernel(GemvArgs a, int N) {
   }
 }
 
-// M = 1, per-256 quant prologue and residual add (the decode down
-// projection, K = 1024 KB): one whole weight row per wave, lane l holding
-// bytes k = 1024 j + 16 l .. + 15 (contiguous 1 KB per load instruction),
-// on N / 4 workgroups (every CU for the 1024 rows of the model).  Per row:
-// v_dot4 partials (exact int32), the 16 lanes of each 256-column group
-// g = 4 j + l / 16 summed with DPP (exact), then the group GEMM's arithmetic
-// p_g = RN(RN(f32(I_g) * bs[n]) * as_g), out = (((0 + p_0) + p_1) + ...) in
-// ascending g, and the residual add of gemv_kernel's EPI_ADD:
-// dst = (dst + o) + out, o the O partials summed in head order (NEPI).
-template <int KB, int NEPI>
+// M = 1 on whole weight rows (the decode Q|K|V, gate/up and down launches,
+// K = 1024 KB): R rows per wave, lane l holding bytes k = 1024 j + 16 l ..
+// + 15 of a row (contiguous 1 KB per load instruction) instead of the MFMA
+// operand layout's 16 rows x 64 B per instruction, on N / (4 R) workgroups.
+// The prologue builds the int8 A row in LDS as gemv_kernel's does (PRO,
+// with the O partials when NP > 0).  Per row: v_dot4 partials (exact
+// int32), the 16 lanes of each 256-column group g = 4 j + l / 16 summed
+// with DPP (exact), then the group GEMM's arithmetic p_g = RN(RN(f32(I_g) *
+// bs[n]) * as_g), out = (((0 + p_0) + p_1) + ...) in ascending g, in
+// registers.  Epilogues as gemv_kernel's: STORE, SWIGLU (NMAT = 2: gate and
+// up rows of the same column) and ADD (dst = (dst + o) + out, o the O
+// partials summed in head order when NEPI > 0).  A wave's rows lie in one
+// segment (segment boundaries are multiples of 4 R).
+template <int PRO, int KB, int NMAT, int R, int NP, int NEPI>
 __global__ void __launch_bounds__(256) gemv_wr_kernel(GemvArgs a, int N) {
   __shared__ float blk[32];
   __shared__ __align__(16) int8_t a_lds[1024 * KB];
   __shared__ float as_lds[4 * KB];
+  __shared__ uint64_t exptab[32];
+  static_assert(NP == 0 || NEPI == 0, "partials: prologue or epilogue");
   const int lane = threadIdx.x & 63;
   const int wave = wave_id();
-  const GemvSeg &sg = a.seg[0];
-  ProSrc ps = read_src<PRO_QUANT, NEPI != 0>(a);
-  pin_src<PRO_QUANT, NEPI != 0>(ps);
-  ProRow<KB, 0> r0;
-  pro_load_row<PRO_QUANT, KB, 0>(a, ps, 0, r0);
-  __builtin_amdgcn_sched_barrier(0);  // (issue order: prologue operands first)
-  const int row = static_cast<int>(blockIdx.x) * 4 + wave;
-  const int n = min(row, N - 1);
-  // the row's residual, its O partials (lane h < 16: partial h) and scale,
-  // then its weights
-  const float xv = sg.out[n];
-  float pv = 0.0f;
-  if constexpr (NEPI > 0) pv = ps.part[min(lane & 15, ps.npart - 1) * ps.ld_part + n];
-  const float bsn = sg.bs[n];
-  int4 w[KB];
+  ProSrc ps = read_src<PRO, (NP + NEPI) != 0>(a);
+  // the segment fields the weight loads need, selected from all three
+  int nseg = a.nseg;
+  int s_n0[3];
+  const int8_t *s_b[3], *s_b2[3];
+  const float *s_bs[3], *s_bs2[3];
 #pragma unroll
-  for (int j = 0; j < KB; ++j)
-    w[j] = *reinterpret_cast<const int4 *>(sg.b + static_cast<int64_t>(n) * (1024 * KB) + 1024 * j + 16 * lane);
+  for (int i = 0; i < 3; ++i) {
+    s_n0[i] = a.seg[i].n0;
+    s_b[i] = a.seg[i].b;
+    s_bs[i] = a.seg[i].bs;
+    s_b2[i] = NMAT == 2 ? a.seg[i].b2 : s_b[i];
+    s_bs2[i] = NMAT == 2 ? a.seg[i].bs2 : s_bs[i];
+  }
+  pin_src<PRO, (NP + NEPI) != 0>(ps);
+  ProRow<KB, NP> r0;
+  pro_load_row<PRO, KB, NP>(a, ps, 0, r0);
+  __builtin_amdgcn_sched_barrier(0);  // (issue order: prologue operands first)
+  const int row0 = (static_cast<int>(blockIdx.x) * 4 + wave) * R;
+  const int si = (nseg > 1 && row0 >= s_n0[1] ? 1 : 0) + (nseg > 2 && row0 >= s_n0[2] ? 1 : 0);
+  auto pick = [&](const auto (&v)[3]) { return si == 0 ? v[0] : si == 1 ? v[1] : v[2]; };
+  const int sg_n0 = pick(s_n0);
+  const int8_t *const sg_b = pick(s_b);
+  const int8_t *const sg_b2 = pick(s_b2);
+  const float *const sg_bs = pick(s_bs);
+  const float *const sg_bs2 = pick(s_bs2);
+  // the rows' scales and weights (rows past N reload row N - 1, unused),
+  // and for the residual epilogue its operands
+  int nr[R];
+  float bsn[NMAT][R];
+  int4 w[NMAT][R][KB];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    nr[r] = min(row0 + r, N - 1) - sg_n0;  // row within the segment
+#pragma unroll
+    for (int mi = 0; mi < NMAT; ++mi) {
+      bsn[mi][r] = (mi == 0 ? sg_bs : sg_bs2)[nr[r]];
+#pragma unroll
+      for (int j = 0; j < KB; ++j)
+        w[mi][r][j] = *reinterpret_cast<const int4 *>((mi == 0 ? sg_b : sg_b2) +
+                                                      static_cast<int64_t>(nr[r]) * (1024 * KB) + 1024 * j + 16 * lane);
+    }
+  }
+  float pv[R];
+  if constexpr (NEPI > 0) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) pv[r] = ps.part[min(lane & 15, ps.npart - 1) * ps.ld_part + sg_n0 + nr[r]];
+  }
   __builtin_amdgcn_sched_barrier(0);
-  pro_compute_row<PRO_QUANT, KB, 0>(a, 0, r0, a_lds, as_lds, blk);  // ends with a barrier
-  float out = 0.0f;
+  if (NMAT == 2 && threadIdx.x == 0) stage_exp2_table(exptab);
+  pro_compute_row<PRO, KB, NP>(a, 0, r0, a_lds, as_lds, blk);  // ends with a barrier
+  const GemvSeg &sg = a.seg[si];
+  int4 av[KB];
+  float asg[KB];
 #pragma unroll
   for (int j = 0; j < KB; ++j) {
-    const int4 av = *reinterpret_cast<const int4 *>(a_lds + 1024 * j + 16 * lane);
-    int acc = sdot4(w[j].x, av.x, 0);
-    acc = sdot4(w[j].y, av.y, acc);
-    acc = sdot4(w[j].z, av.z, acc);
-    acc = sdot4(w[j].w, av.w, acc);
-    acc += lane_xor<1>(acc);
-    acc += lane_xor<2>(acc);
-    acc += lane_xor<4>(acc);
-    acc += lane_xor<8>(acc);
-    const float p = __fmul_rn(__fmul_rn(static_cast<float>(acc), bsn), as_lds[4 * j + (lane >> 4)]);
-    out = __fadd_rn(out, lane_bcast<0>(p));
-    out = __fadd_rn(out, lane_bcast<16>(p));
-    out = __fadd_rn(out, lane_bcast<32>(p));
-    out = __fadd_rn(out, lane_bcast<48>(p));
+    av[j] = *reinterpret_cast<const int4 *>(a_lds + 1024 * j + 16 * lane);
+    asg[j] = as_lds[4 * j + (lane >> 4)];
   }
-  float base = xv;
-  if constexpr (NEPI > 0) {
-    float o = 0.0f;  // the O projection, partials in head order
 #pragma unroll
-    for (int h = 0; h < NEPI; ++h)
-      if (h < ps.npart) o = __fadd_rn(o, __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(pv), h)));
-    base = __fadd_rn(base, o);
+  for (int r = 0; r < R; ++r) {
+    float out[NMAT];
+#pragma unroll
+    for (int mi = 0; mi < NMAT; ++mi) {
+      out[mi] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < KB; ++j) {
+        int acc = sdot4(w[mi][r][j].x, av[j].x, 0);
+        acc = sdot4(w[mi][r][j].y, av[j].y, acc);
+        acc = sdot4(w[mi][r][j].z, av[j].z, acc);
+        acc = sdot4(w[mi][r][j].w, av[j].w, acc);
+        acc += lane_xor<1>(acc);
+        acc += lane_xor<2>(acc);
+        acc += lane_xor<4>(acc);
+        acc += lane_xor<8>(acc);
+        const float p = __fmul_rn(__fmul_rn(static_cast<float>(acc), bsn[mi][r]), asg[j]);
+        out[mi] = __fadd_rn(out[mi], lane_bcast<0>(p));
+        out[mi] = __fadd_rn(out[mi], lane_bcast<16>(p));
+        out[mi] = __fadd_rn(out[mi], lane_bcast<32>(p));
+        out[mi] = __fadd_rn(out[mi], lane_bcast<48>(p));
+      }
+    }
+    float *dst = sg.out + nr[r];
+    float v = out[0];
+    if (sg.epi == EPI_ADD) {
+      float base = *dst;
+      if constexpr (NEPI > 0) {
+        float o = 0.0f;  // the O projection, partials in head order
+#pragma unroll
+        for (int h = 0; h < NEPI; ++h)
+          if (h < ps.npart) o = __fadd_rn(o, __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(pv[r]), h)));
+        base = __fadd_rn(base, o);
+      }
+      v = __fadd_rn(base, out[0]);
+    } else if (NMAT == 2 && sg.epi == EPI_SWIGLU) {
+      v = swiglu_tab(out[0], out[NMAT - 1], exptab);
+    }
+    if (lane == 0 && row0 + r < N) *dst = v;
   }
-  if (lane == 0 && row < N) sg.out[n] = __fadd_rn(base, out);
 }
 
 // Per (row, head) wave: the head epilogues of the Q/K/V projections
@@ -1110,14 +1168,60 @@ hipError_t dispatch_part(const GemvArgs &a, int ncols, hipStream_t s) {
     if (pro && a.K == 1024) return launch_t<1, 4, 1, NMAT, PRO_NORM, kPartPro>(a, ncols, s);
   } else {
     if (epi && a.K == 3072 && a.pro == PRO_QUANT) {
-      if (ncols % 4 == 0) {  // whole weight rows, a row per wave
-        Q3_LAUNCH((gemv_wr_kernel<3, kMaxPart>), dim3(ncols / 4), dim3(256), 0, s, a, ncols);
-        return hipGetLastError();
-      }
       return launch_t<3, 4, 1, NMAT, PRO_QUANT, kPartEpi>(a, ncols, s);
     }
   }
   return hipErrorInvalidValue;
+}
+
+// One row with a prologue (the decode launches): the whole-row kernel, R
+// rows per wave so that each launch has N / (4 R) = 256 workgroups for the
+// model's shapes: Q|K|V (K = 1024, 4 rows), gate/up (two matrices, 3 rows),
+// down (K = 3072, 1 row).  Returns false where it does not apply.
+template <int PRO, int KB, int NMAT, int R, int NP, int NEPI>
+hipError_t launch_wr(const GemvArgs &a, int ncols, hipStream_t s) {
+  Q3_LAUNCH((gemv_wr_kernel<PRO, KB, NMAT, R, NP, NEPI>), dim3(ncols / (4 * R)), dim3(256), 0, s, a, ncols);
+  return hipGetLastError();
+}
+
+bool wr_launch(const GemvArgs &a, int ncols, hipStream_t s, hipError_t *err) {
+  if (a.M != 1 || a.group != 256 || a.bs_ld || a.pro == PRO_NONE) return false;
+  const int epi = a.seg[0].epi;
+  const bool two = epi == EPI_SWIGLU;
+  int R;
+  if (two) {
+    if (a.K != 1024 || a.pro != PRO_NORM || a.nseg != 1) return false;
+    R = 3;
+  } else if (a.K == 3072) {
+    if (a.pro != PRO_QUANT || a.nseg != 1 || epi != EPI_ADD) return false;
+    R = 1;
+  } else if (a.K == 1024) {
+    if (a.pro != PRO_NORM && a.pro != PRO_EMBED) return false;
+    R = 4;
+  } else {
+    return false;
+  }
+  if (ncols % (4 * R)) return false;
+  for (int i = 0; i < a.nseg; ++i) {
+    const int e = a.seg[i].epi;
+    if (a.seg[i].n0 % (4 * R) || (two != (e == EPI_SWIGLU)) || (e != EPI_STORE && e != EPI_ADD && e != EPI_SWIGLU))
+      return false;
+  }
+  if (a.part) {  // O partials: gate/up's prologue or down's epilogue, as dispatch_part takes them
+    const bool pro = a.pro == PRO_NORM;
+    if (a.npart < 1 || a.npart > kMaxPart || a.nseg != 1 || pro != two || (!pro && epi != EPI_ADD) ||
+        a.ld_part < (pro ? a.K : ncols) || (reinterpret_cast<uintptr_t>(a.part) & 15) != 0 || (a.ld_part % 4) != 0)
+      return false;
+  }
+  const bool part = a.part != nullptr;
+  if (two)
+    *err = part ? launch_wr<PRO_NORM, 1, 2, 3, kMaxPart, 0>(a, ncols, s) : launch_wr<PRO_NORM, 1, 2, 3, 0, 0>(a, ncols, s);
+  else if (a.K == 3072)
+    *err = part ? launch_wr<PRO_QUANT, 3, 1, 1, 0, kMaxPart>(a, ncols, s) : launch_wr<PRO_QUANT, 3, 1, 1, 0, 0>(a, ncols, s);
+  else
+    *err = a.pro == PRO_NORM ? launch_wr<PRO_NORM, 1, 1, 4, 0, 0>(a, ncols, s)
+                             : launch_wr<PRO_EMBED, 1, 1, 4, 0, 0>(a, ncols, s);
+  return true;
 }
 
 }  // namespace
@@ -1207,6 +1311,10 @@ hipError_t launch_gemv(const GemvArgs &a, hipStream_t s) {
       default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+  }
+  {
+    hipError_t err = hipSuccess;
+    if (wr_launch(a, ncols, s, &err)) return err;
   }
   const bool two = a.seg[0].epi == EPI_SWIGLU;
   if (a.M > 16) {  // a batch of rows: plain A operand, no partials, 16-column tiles
