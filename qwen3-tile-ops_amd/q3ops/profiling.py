@@ -45,7 +45,8 @@ import statistics
 import sys
 
 # kernel symbol -> kernel class.  Decode classes are those of
-# q3_model_set_kernel_timing; gemv_kernel<GPW, KSTEPS, NT, NMAT, prologue,
+# q3_model_set_kernel_timing; gemv_wr_kernel<prologue, KB, NMAT, R, ...>,
+# gemv_kernel<GPW, KSTEPS, NT, NMAT, prologue,
 # partials, ...> and gemm_tile_kernel<BM, BN, WGM, NMAT, STAGES, KS, epilogue,
 # group, ...> and gemm_stream_kernel<BM, NWN, KP, NT, NMAT, D, KB, epilogue,
 # group, ...> are matched on their template arguments (epilogue numbers:
@@ -54,6 +55,9 @@ import sys
 CLASS_OF = [
     (r"attn_decode_kernel<1, ", "attn_decode"),
     (r"attn_decode_kernel<2, ", "attn_decode_batch"),
+    (r"gemv_wr_kernel<[13], 1, 1, 4,", "gemv_qkv"),
+    (r"gemv_wr_kernel<1, 1, 2, 3,", "gemv_gate_up"),
+    (r"gemv_wr_kernel<2, 3, 1, 1,", "gemv_down"),
     (r"gemv_kernel<1, 4, 1, 1, [13], 0", "gemv_qkv"),
     (r"gemv_kernel<4, 2, 1, 1,", "gemv_o"),
     (r"gemv_kernel<1, 4, 1, 2, 1, 1", "gemv_gate_up"),
