@@ -9,9 +9,9 @@
 // CB = NW * BPW blocks:
 //   phase 1 (parallel over blocks)  S_j = q8.k8^T (v_dot4_i32_i8, exact),
 //                                   s = ((f32 S * ks) * qs) * qk, block max
-//   phase 2 (sequential, tiny)      nmm_j = max(nmm_{j-1}, max_j)
-//   phase 3 (parallel over blocks)  corr_j = exp(nmm_{j-1} - nmm_j),
-//                                   P = exp(s - nmm_j), psum_j = tree_sum(P),
+//   phase 2 (a scan, one lane/block) nmm_j = max(nmm_{j-1}, max_j),
+//                                   corr_j = exp(nmm_{j-1} - nmm_j)
+//   phase 3 (parallel over blocks)  P = exp(s - nmm_j), psum_j = tree_sum(P),
 //                                   P *= vs, pmax_j, P8, PV_j = f32(P8.V) * pmax_j
 //   phase 4 (sequential per dim)    den = den*corr_j + psum_j,
 //                                   res = res*corr_j + PV_j
@@ -46,15 +46,36 @@ __device__ __forceinline__ int sdot4(int a, int b, int c) {
   return __builtin_amdgcn_sdot4(a, b, c, false);
 }
 
-// P8.V of one 32-key block for the lanes' layout of phase 3: lane l holds
-// vw[cc] = the 4 int8 values of dims d0..d0+3 (d0 = 4 (l % 32)) of key
-// kh + cc (kh = 16 (l / 32)), and p8 of key c for head h sits in lane
-// 32 h + c.  acc[h][e] += sum over the 16 keys of p8[h][key] * v[key][d0+e],
-// exact in int32.  4x4 byte tiles (4 keys x 4 dims) are transposed with
-// v_perm_b32 so that v_dot4_i32_i8 multiplies 4 keys at once; the P8 bytes of
-// 4 consecutive keys are packed with DPP quad broadcasts.
+// The V words of one 32-key block as loaded (lane l: vw[cc] = the 4 int8
+// values of dims d0..d0+3, d0 = 4 (l % 32), of key kh + cc, kh = 16 (l / 32))
+// turned in place into 4x4 byte tiles transposed with v_perm_b32: afterwards
+// vw[4 g + e] holds dim d0 + e of keys kh + 4 g .. kh + 4 g + 3, so that
+// v_dot4_i32_i8 multiplies 4 keys at once.  It needs only the block's V, so
+// the kernel runs it for all but a wave's last block in phase 1, while that
+// wave waits for its next block's K rows, instead of in the VALU-bound
+// phase 3.
+__device__ __forceinline__ void v_transpose(int (&vw)[16]) {
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const uint32_t w0 = vw[4 * g], w1 = vw[4 * g + 1], w2 = vw[4 * g + 2], w3 = vw[4 * g + 3];
+    const uint32_t x01l = __builtin_amdgcn_perm(w1, w0, 0x06020400u);
+    const uint32_t x01h = __builtin_amdgcn_perm(w1, w0, 0x07030501u);
+    const uint32_t x23l = __builtin_amdgcn_perm(w3, w2, 0x06020400u);
+    const uint32_t x23h = __builtin_amdgcn_perm(w3, w2, 0x07030501u);
+    vw[4 * g] = static_cast<int>(__builtin_amdgcn_perm(x23l, x01l, 0x05040100u));
+    vw[4 * g + 1] = static_cast<int>(__builtin_amdgcn_perm(x23h, x01h, 0x05040100u));
+    vw[4 * g + 2] = static_cast<int>(__builtin_amdgcn_perm(x23l, x01l, 0x07060302u));
+    vw[4 * g + 3] = static_cast<int>(__builtin_amdgcn_perm(x23h, x01h, 0x07060302u));
+  }
+}
+
+// P8.V of one 32-key block for the lanes' layout of phase 3, on V words
+// transposed by v_transpose: p8 of key c for head h sits in lane 32 h + c,
+// and acc[h][e] += sum over the lane's 16 keys of p8[h][key] * v[key][d0+e],
+// exact in int32.  The P8 bytes of 4 consecutive keys are packed with DPP
+// quad broadcasts.
 template <int QPW>
-__device__ __forceinline__ void pv_dot(const int (&vw)[16], int p8, int lane, int (&acc)[QPW][4]) {
+__device__ __forceinline__ void pv_dot(const int (&vt)[16], int p8, int lane, int (&acc)[QPW][4]) {
   const int b = p8 & 0xff;
   const int q0 = __builtin_amdgcn_mov_dpp(b, 0x00, 0xf, 0xf, false);  // quad lane 0
   const int q1 = __builtin_amdgcn_mov_dpp(b, 0x55, 0xf, 0xf, false);  // quad lane 1
@@ -64,15 +85,7 @@ __device__ __forceinline__ void pv_dot(const int (&vw)[16], int p8, int lane, in
   const bool upper = lane >= 32;
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
-    const uint32_t w0 = vw[4 * g], w1 = vw[4 * g + 1], w2 = vw[4 * g + 2], w3 = vw[4 * g + 3];
-    const uint32_t x01l = __builtin_amdgcn_perm(w1, w0, 0x06020400u);
-    const uint32_t x01h = __builtin_amdgcn_perm(w1, w0, 0x07030501u);
-    const uint32_t x23l = __builtin_amdgcn_perm(w3, w2, 0x06020400u);
-    const uint32_t x23h = __builtin_amdgcn_perm(w3, w2, 0x07030501u);
-    const int r[4] = {static_cast<int>(__builtin_amdgcn_perm(x23l, x01l, 0x05040100u)),
-                      static_cast<int>(__builtin_amdgcn_perm(x23h, x01h, 0x05040100u)),
-                      static_cast<int>(__builtin_amdgcn_perm(x23l, x01l, 0x07060302u)),
-                      static_cast<int>(__builtin_amdgcn_perm(x23h, x01h, 0x07060302u))};
+    const int r[4] = {vt[4 * g], vt[4 * g + 1], vt[4 * g + 2], vt[4 * g + 3]};
 #pragma unroll
     for (int h = 0; h < QPW; ++h) {
       const int pa = __builtin_amdgcn_readlane(packed, 32 * h + 4 * g);
@@ -582,6 +595,7 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
         if ((lane & 1) == 0) sm.s[h][jb * 32 + kcl] = s;
         if (lane == 0) sm.bmax[h][jb] = bm;
       }
+      if (i < BPW - 1) v_transpose(vw[i]);
     }
     if constexpr (OFUSE) {
       __builtin_amdgcn_sched_barrier(0);
@@ -614,6 +628,10 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
       prev = cc == 0 ? runh : up;
       run0 = lane_read(nmm, nb - 1);
       if constexpr (QPW > 1) run1 = lane_read(nmm, 32 + nb - 1);
+      // corr_j = exp(nmm_{j-1} - nmm_j) of every block at once, in the last
+      // wave (which owns the fewest blocks while the chunk is not full):
+      // one exp per lane here instead of one per block in phase 3
+      if (wave == NW - 1 && hh < QPW && cc < nb) sm.corr[hh][cc] = exp_f32_le0_tab(__fsub_rn(prev, nmm), sm.tab);
     }
     // ---- phase 3: P, P8 and P8.V per block ----
 #pragma unroll
@@ -627,11 +645,10 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
       for (int hp = 0; hp < QPW; hp += 2) {
         const int h = hp + (lane >> 5);
         const bool hok = h < QPW;
-        // this block's nmm / prev of the lane's head (lanes jb and 32 + jb)
-        const float nm0 = lane_read(nmm, jb), pr0 = lane_read(prev, jb);
+        // this block's nmm of the lane's head (lanes jb and 32 + jb)
+        const float nm0 = lane_read(nmm, jb);
         const float nm1 = QPW > 1 ? lane_read(nmm, 32 + jb) : nm0;
-        const float pr1 = QPW > 1 ? lane_read(prev, 32 + jb) : pr0;
-        const float nmb = (lane & 32) ? nm1 : nm0, prb = (lane & 32) ? pr1 : pr0;
+        const float nmb = (lane & 32) ? nm1 : nm0;
         float p = 0.0f, pv = 0.0f;
         if (hok && valid) {
           p = exp_f32_le0_tab(__fsub_rn(sm.s[h][jb * 32 + c], nmb), sm.tab);
@@ -640,10 +657,8 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
         const float psum = tree_sum32(p);
         const float pm = __fmul_rn(max32(pv), inv127());
         const int p8 = hok ? quant1(pv, pm) : 0;
-        if (hok && c == 0) {
-          sm.psum[h][jb] = psum;
-          sm.corr[h][jb] = exp_f32_le0_tab(__fsub_rn(prb, nmb), sm.tab);
-        }
+        if (hok && c == 0) sm.psum[h][jb] = psum;
+        if (i == BPW - 1) v_transpose(vw[i]);
         int acc[2][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
         pv_dot<(QPW > 1 ? 2 : 1)>(vw[i], p8, lane, reinterpret_cast<int(&)[(QPW > 1 ? 2 : 1)][4]>(acc));
 #pragma unroll
