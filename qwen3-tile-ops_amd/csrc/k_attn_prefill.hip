@@ -27,8 +27,8 @@
 // Work: 8 waves per 16-row query block of one head.  The default workgroup
 // holds one query block (74 KiB of LDS, two workgroups per CU) and the grid
 // is ordered so that the two workgroups a CU usually receives, L and
-// L + heads * ceil(nqb / 2), take the causally complementary blocks qb and
-// nqb - 1 - qb.  The paired form (NI = 2, 16 waves) walks both blocks of a
+// L + heads * floor(nqb / 2), take the causally complementary blocks
+// nqb - 1 - qb and qb (the long one dispatched first).  The paired form (NI = 2, 16 waves) walks both blocks of a
 // pair at once: A's key blocks are a prefix of B's, so each K/V block is
 // copied once and serves both (two 16-column MFMA tiles) while A needs it.
 // Wave w owns block w of a chunk in phases 1 and 3 and, in phase 4, 16 output
@@ -166,15 +166,17 @@ __global__ void __launch_bounds__(Cfg<NI>::NW * 64, 4) attn_prefill_kernel(AttnA
     h = kvh * group + r_id % group;
     qbA = r_id / group;
     qbB = nqb - 1 - qbA;
-  } else {  // grid: heads x nqb; workgroups L and L + heads * ceil(nqb / 2)
+  } else {  // grid: heads x nqb; workgroups L and L + heads * floor(nqb / 2)
             // (dispatched one round apart, so usually on one CU) take
-            // complementary query blocks qb and nqb - 1 - qb of one head
-    const int half = (nqb + 1) / 2 * a.heads;
+            // complementary query blocks nqb - 1 - qb and qb of one head; the
+            // long (late) query blocks are dispatched first, since the last
+            // of them to end sets the launch
+    const int half = nqb / 2 * a.heads;
     const int idx = L_id < half ? L_id : L_id - half;
     const int hs = idx % a.heads;
     kvh = hs % a.kv_heads;
     h = kvh * group + hs / a.kv_heads;
-    qbB = L_id < half ? idx / a.heads : nqb - 1 - idx / a.heads;
+    qbB = L_id < half ? nqb - 1 - idx / a.heads : idx / a.heads;
     qbA = qbB;
   }
   int kv_len = static_cast<int>(a.kv_len);
