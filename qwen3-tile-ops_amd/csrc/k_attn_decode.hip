@@ -538,12 +538,14 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
       }
     }
     issue_block(BPW - 1);
-    // the new token (position kv_len - 1) comes from the prologue's LDS copy
-    if constexpr (FUSE) {
-#pragma unroll
-      for (int i = 0; i < BPW; ++i) {
-        const int j = (b0 + wave + NW * i) * 32;
-        if (wave + NW * i >= nb) continue;
+    // The new token (position kv_len - 1) comes from the prologue's LDS copy
+    // (FUSE), patched into a block's K words just before its scores and into
+    // its V words and scales just before their first use: the select reads
+    // the loaded register, so a patch waits for that load, and one placed in
+    // front of phase 1 made every wave wait for all of its chunk's loads
+    // (the last block's V included) before its first score.
+    auto patch_k = [&](int i, int j) {
+      if constexpr (FUSE) {
         const int *kn = reinterpret_cast<const int *>(sm.knew + kb16);
 #pragma unroll
         for (int e = 0; e < 4; ++e)
@@ -552,12 +554,16 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
             for (int t = 0; t < 4; ++t) kw[i][4 * e + t] = kn[t];
           }
         if (j + kcl == pos0) kscale[i] = sm.ksnew;
+      }
+    };
+    auto patch_v = [&](int i, int j) {
+      if constexpr (FUSE) {
 #pragma unroll
         for (int cc = 0; cc < 16; ++cc)
           if (j + kh + cc == pos0) vw[i][cc] = *reinterpret_cast<const int *>(sm.vnew + d0);
         if (j + (lane & 31) == pos0) vscale[i] = sm.vsnew;
       }
-    }
+    };
     // ---- phase 1: scores and block maxima ----
 #pragma unroll
     for (int i = 0; i < BPW; ++i) {
@@ -565,6 +571,7 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
       if (jb >= nb) continue;
       const int j = (b0 + jb) * 32;
       const bool valid = j + kcl < kv_end;
+      patch_k(i, j);
 #pragma unroll
       for (int h = 0; h < QPW; ++h) {
         int p[4];
@@ -595,7 +602,10 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
         if ((lane & 1) == 0) sm.s[h][jb * 32 + kcl] = s;
         if (lane == 0) sm.bmax[h][jb] = bm;
       }
-      if (i < BPW - 1) v_transpose(vw[i]);
+      if (i < BPW - 1) {
+        patch_v(i, j);
+        v_transpose(vw[i]);
+      }
     }
     if constexpr (OFUSE) {
       __builtin_amdgcn_sched_barrier(0);
@@ -641,6 +651,7 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
       const int j = (b0 + jb) * 32;
       const int c = lane & 31;
       const bool valid = j + c < kv_end;
+      if (i == BPW - 1) patch_v(i, j);  // (the others were patched in phase 1)
 #pragma unroll
       for (int hp = 0; hp < QPW; hp += 2) {
         const int h = hp + (lane >> 5);
