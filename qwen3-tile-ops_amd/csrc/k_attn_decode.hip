@@ -70,11 +70,11 @@ __device__ __forceinline__ void v_transpose(int (&vw)[16]) {
 }
 
 // P8.V of one 32-key block for the lanes' layout of phase 3, on V words
-// transposed by v_transpose: p8 of key c for head h sits in lane 32 h + c,
-// and acc[h][e] += sum over the lane's 16 keys of p8[h][key] * v[key][d0+e],
-// exact in int32.  The P8 bytes of 4 consecutive keys are packed with DPP
-// quad broadcasts.
-template <int QPW>
+// transposed by v_transpose: p8 of key c for head h sits in lane
+// 32 (h + HB) + c, and acc[h][e] += sum over the lane's 16 keys of
+// p8[h][key] * v[key][d0+e], exact in int32.  The P8 bytes of 4 consecutive
+// keys are packed with DPP quad broadcasts.
+template <int QPW, int HB = 0>
 __device__ __forceinline__ void pv_dot(const int (&vt)[16], int p8, int lane, int (&acc)[QPW][4]) {
   const int b = p8 & 0xff;
   const int q0 = __builtin_amdgcn_mov_dpp(b, 0x00, 0xf, 0xf, false);  // quad lane 0
@@ -88,8 +88,8 @@ __device__ __forceinline__ void pv_dot(const int (&vt)[16], int p8, int lane, in
     const int r[4] = {vt[4 * g], vt[4 * g + 1], vt[4 * g + 2], vt[4 * g + 3]};
 #pragma unroll
     for (int h = 0; h < QPW; ++h) {
-      const int pa = __builtin_amdgcn_readlane(packed, 32 * h + 4 * g);
-      const int pb = __builtin_amdgcn_readlane(packed, 32 * h + 16 + 4 * g);
+      const int pa = __builtin_amdgcn_readlane(packed, 32 * (h + HB) + 4 * g);
+      const int pb = __builtin_amdgcn_readlane(packed, 32 * (h + HB) + 16 + 4 * g);
       const int pk = upper ? pb : pa;
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc[h][e] = sdot4(pk, r[e], acc[h][e]);
@@ -644,10 +644,54 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
       if (wave == NW - 1 && hh < QPW && cc < nb) sm.corr[hh][cc] = exp_f32_le0_tab(__fsub_rn(prev, nmm), sm.tab);
     }
     // ---- phase 3: P, P8 and P8.V per block ----
+    // One head per workgroup and both of the wave's blocks in the chunk: their
+    // P, psum, pmax and P8 side by side in the two half-waves (block i in
+    // lanes 32 i ..), one exp and reduction chain for both; the phase is
+    // VALU-bound on the SIMDs that hold two-block waves.
+    bool paired = false;
+    if constexpr (QPW == 1 && BPW == 2) {
+      if (wave + NW < nb) {
+        paired = true;
+        const int c = lane & 31, hi = lane >> 5;
+        const int jbl = wave + NW * hi;
+        patch_v(1, (b0 + wave + NW) * 32);
+        const float nm0 = lane_read(nmm, wave), nm1 = lane_read(nmm, wave + NW);
+        const float nmb = hi ? nm1 : nm0;
+        float p = 0.0f, pv = 0.0f;
+        if ((b0 + jbl) * 32 + c < kv_end) {
+          p = exp_f32_le0_tab(__fsub_rn(sm.s[0][jbl * 32 + c], nmb), sm.tab);
+          pv = __fmul_rn(p, hi ? vscale[1] : vscale[0]);
+        }
+        const float psum = tree_sum32(p);
+        const float pm = __fmul_rn(max32(pv), inv127());
+        const int p8 = quant1(pv, pm);
+        if (c == 0) sm.psum[0][jbl] = psum;
+        v_transpose(vw[1]);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          int acc[1][4] = {{0, 0, 0, 0}};
+          if (i == 0)
+            pv_dot<1, 0>(vw[0], p8, lane, acc);
+          else
+            pv_dot<1, 1>(vw[1], p8, lane, acc);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[0][e] += lane_xor<32>(acc[0][e]);
+          const float pmh = i ? lane_bcast<32>(pm) : lane_bcast<0>(pm);
+          if (lane < 32) {
+            float4 o;
+            o.x = __fmul_rn(static_cast<float>(acc[0][0]), pmh);
+            o.y = __fmul_rn(static_cast<float>(acc[0][1]), pmh);
+            o.z = __fmul_rn(static_cast<float>(acc[0][2]), pmh);
+            o.w = __fmul_rn(static_cast<float>(acc[0][3]), pmh);
+            *reinterpret_cast<float4 *>(&sm.pv[0][wave + NW * i][d0]) = o;
+          }
+        }
+      }
+    }
 #pragma unroll
     for (int i = 0; i < BPW; ++i) {
       const int jb = wave + NW * i;
-      if (jb >= nb) continue;
+      if (paired || jb >= nb) continue;
       const int j = (b0 + jb) * 32;
       const int c = lane & 31;
       const bool valid = j + c < kv_end;
