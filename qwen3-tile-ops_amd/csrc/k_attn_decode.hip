@@ -51,9 +51,10 @@ __device__ __forceinline__ int sdot4(int a, int b, int c) {
 // turned in place into 4x4 byte tiles transposed with v_perm_b32: afterwards
 // vw[4 g + e] holds dim d0 + e of keys kh + 4 g .. kh + 4 g + 3, so that
 // v_dot4_i32_i8 multiplies 4 keys at once.  It needs only the block's V, so
-// the kernel runs it for all but a wave's last block in phase 1, while that
-// wave waits for its next block's K rows, instead of in the VALU-bound
-// phase 3.
+// the b = 1 kernel runs it for all but a wave's last block in phase 1, while
+// that wave waits for its next block's K rows, instead of in the VALU-bound
+// phase 3 (batches, bound by their loads, keep it in phase 3: 3.036 against
+// 3.063 ms per config-4 step).
 __device__ __forceinline__ void v_transpose(int (&vw)[16]) {
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
@@ -602,7 +603,7 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
         if ((lane & 1) == 0) sm.s[h][jb * 32 + kcl] = s;
         if (lane == 0) sm.bmax[h][jb] = bm;
       }
-      if (i < BPW - 1) {
+      if (FUSE && i < BPW - 1) {
         patch_v(i, j);
         v_transpose(vw[i]);
       }
@@ -713,7 +714,7 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
         const float pm = __fmul_rn(max32(pv), inv127());
         const int p8 = hok ? quant1(pv, pm) : 0;
         if (hok && c == 0) sm.psum[h][jb] = psum;
-        if (i == BPW - 1) v_transpose(vw[i]);
+        if (!FUSE || i == BPW - 1) v_transpose(vw[i]);
         int acc[2][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
         pv_dot<(QPW > 1 ? 2 : 1)>(vw[i], p8, lane, reinterpret_cast<int(&)[(QPW > 1 ? 2 : 1)][4]>(acc));
 #pragma unroll
