@@ -667,6 +667,7 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
         const float pm = __fmul_rn(max32(pv), inv127());
         const int p8 = quant1(pv, pm);
         if (c == 0) sm.psum[0][jbl] = psum;
+        if constexpr (!FUSE) v_transpose(vw[0]);  // (FUSE: done in phase 1)
         v_transpose(vw[1]);
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
