@@ -62,7 +62,7 @@ struct q3_model {
   double kt_ms[Q3_KT_COUNT] = {};              // folded totals
   uint32_t kt_n[Q3_KT_COUNT] = {};
   // decode: workgroups that prefetch the next kernels' weights during the
-  // attention kernel (Q3_DECODE_PREFETCH_WGS, default 128; 0 disables)
+  // attention kernel (Q3_DECODE_PREFETCH_WGS, default 176; 0 disables)
   int pf_wgs;
   // decode: O projection folded into the attention kernel
   // (Q3_DECODE_FUSE_OPROJ, default 1; 0 runs it as its own GEMV)
@@ -1101,7 +1101,7 @@ extern "C" int q3_model_open(void *blob, const q3_layout *lay, void *stream, q3_
   m->stream = static_cast<hipStream_t>(stream);
   m->n_pages = lay->max_seq / kPageTokens;
   m->keys_ld = lay->vocab / 16 + 64;  // one key per lm_head column block
-  m->pf_wgs = 128;
+  m->pf_wgs = 176;  // of 96-256: 96 0.754, 128 0.718, 176 0.712, 192 0.713, 256 0.716 ms/token
   if (const char *e = std::getenv("Q3_DECODE_PREFETCH_WGS")) m->pf_wgs = std::max(0, std::atoi(e));
   if (const char *e = std::getenv("Q3_DECODE_FUSE_OPROJ")) m->ofuse = std::atoi(e) != 0;
   if (const char *e = std::getenv("Q3_DECODE_GRAPH")) m->dgraph_on = std::atoi(e) != 0;
