@@ -55,7 +55,7 @@ import sys
 CLASS_OF = [
     (r"attn_decode_kernel<1, ", "attn_decode"),
     (r"attn_decode_kernel<2, ", "attn_decode_batch"),
-    (r"gemv_wr_kernel<[13], 1, 1, 4,", "gemv_qkv"),
+    (r"gemv_wr_kernel<[13], 1, 1, 2,", "gemv_qkv"),
     (r"gemv_wr_kernel<1, 1, 2, 3,", "gemv_gate_up"),
     (r"gemv_wr_kernel<2, 3, 1, 1,", "gemv_down"),
     (r"gemv_kernel<1, 4, 1, 1, [13], 0", "gemv_qkv"),
