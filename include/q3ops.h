@@ -344,6 +344,14 @@ int q3_model_close(q3_model *m);
  * counterpart in the reference, whose model is a set of global views). */
 int q3_model_info(const q3_model *m, q3_layout *lay, void **blob, void **stream);
 
+/* A decode token's Q|K|V projection and attention share one launch
+ * (Q3_DECODE_FUSE_QKV at open, default 1): *fused = 1 when enabled.  Their
+ * workgroups hand the projection rows over in device memory with a bounded
+ * wait; *gave_up = 1 when, since open, a wait ran out (a launch that lost a
+ * workgroup: its results are wrong), else 0.  Synchronises the model's
+ * stream.  No counterpart in the reference (a single hart). */
+int q3_model_fused_status(q3_model *m, uint32_t *fused, uint32_t *gave_up);
+
 /* ------------------------------------------------------------------------ */
 /* Host engine: tools/engine.py:81-250 (PagePool, Scheduler, Engine.step)   */
 /* ------------------------------------------------------------------------ */

@@ -35,6 +35,7 @@
 #include <type_traits>
 
 #include "q3_device.h"
+#include "q3_gemv_pro.h"
 #include "q3_kernels.h"
 
 namespace q3 {
@@ -213,13 +214,17 @@ struct FusedRegs {
 // Every wave issues the same six loads (waves past the heads repeat wave
 // 0's, the V wave loads gains it does not use): with a fixed count the
 // compiler's waits after them stay exact.
-template <int QPW>
+// POLL: the projection rows come from the exchange words instead (polled in
+// the prologue, attn_poll_rows), so only the gains and RoPE rows load here.
+template <int QPW, bool POLL = false>
 __device__ __forceinline__ void fused_load(const HotArgs &a, int kvh, int qh0, int wave, int lane,
                                            FusedRegs &r) {
   const int w = wave < 2 + QPW ? wave : 0;
-  const float *src = w == 0 ? a.fk + kvh * HD : w == 1 ? a.fv + kvh * HD : a.fq + (qh0 + w - 2) * HD;
-  r.t0 = src[lane];
-  r.t1 = src[lane + 64];
+  if constexpr (!POLL) {
+    const float *src = w == 0 ? a.fk + kvh * HD : w == 1 ? a.fv + kvh * HD : a.fq + (qh0 + w - 2) * HD;
+    r.t0 = src[lane];
+    r.t1 = src[lane + 64];
+  }
   const float *nw = w == 0 ? a.nk : a.nq;
   r.w0 = nw[lane];
   r.w1 = nw[lane + 64];
@@ -330,28 +335,54 @@ __device__ void prefetch_ranges(const AttnArgs &a, int w, int first) {
   }
 }
 
+// POLL (fused Q|K|V + attention launch): the K, V and Q waves of the
+// prologue take the new token's projection rows from AttnArgs::xin, polling
+// until the GEMV workgroups of the same launch have stored them, and clear
+// them for the next launch.  Every word has this one reader.
+constexpr int kPollLimit = 1 << 17;  // about 60 ms of round trips, then give up
+
+__device__ __forceinline__ unsigned long long xload(const unsigned long long *p) {
+  return __hip_atomic_load(const_cast<unsigned long long *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void xstore(unsigned long long *p, unsigned long long v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int QPW>
+__device__ __forceinline__ void attn_poll_rows(const AttnArgs &a, int qh0, int wave, int lane, FusedRegs &r) {
+  if (wave >= 2 + QPW) return;
+  // wave 0: K, wave 1: V, waves 2..: Q, of query head qh0 + (wave - 2)
+  const int sec = wave == 0 ? 1 : wave == 1 ? 2 : 0;
+  const int qh = qh0 + (wave >= 2 ? wave - 2 : 0);
+  unsigned long long *src = a.xin + (static_cast<int64_t>(sec) * a.heads + qh) * HD;
+  unsigned long long w0 = 0, w1 = 0;
+  for (int it = 0;; ++it) {
+    w0 = xload(src + lane);
+    w1 = xload(src + lane + 64);
+    if (__all((w0 >> 32) == 1u && (w1 >> 32) == 1u)) break;
+    if (it == kPollLimit) {
+      if (lane == 0) __hip_atomic_store(a.xerr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+  }
+  r.t0 = __uint_as_float(static_cast<uint32_t>(w0));
+  r.t1 = __uint_as_float(static_cast<uint32_t>(w1));
+  xstore(src + lane, 0ull);
+  xstore(src + lane + 64, 0ull);
+}
+
 // FUSE: the head epilogues run in the prologue (a.fuse_heads); a template
 // parameter rather than a branch so that both variants issue a fixed number
 // of loads.  OFUSE (with FUSE, QPW = 1): the O projection partials of the
-// head (AttnArgs::opart) are computed after the epilogue.
-template <int QPW, int NW, int BPW, bool FUSE, bool OFUSE = false>
-__global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
+// head (AttnArgs::opart) are computed after the epilogue.  (bx, by): the
+// workgroup's head group and sequence.
+template <int QPW, int NW, int BPW, bool FUSE, bool OFUSE = false, bool POLL = false>
+__device__ __forceinline__ void attn_decode_body(const AttnArgs &a, int bx, int by) {
   constexpr int CB = NW * BPW;
   static_assert(!OFUSE || (FUSE && QPW == 1), "O projection fusion: one head per workgroup");
+  static_assert(!POLL || OFUSE, "polled projection rows: the fused b = 1 variant");
   __shared__ __align__(16) Smem<QPW, CB> sm;
   __shared__ __align__(16) SmemO<OFUSE> smo;
-  // prefetch workgroups: grid rows y >= 1 of the fused (b = 1) variants, so
-  // that telling them apart needs no kernel argument; else x >= heads / QPW
-  if constexpr (FUSE) {
-    if (blockIdx.y > 0) {
-      const int w = static_cast<int>((blockIdx.y - 1) * gridDim.x + blockIdx.x);
-      if (w < a.pf_wgs) prefetch_ranges(a, w, static_cast<int>(gridDim.x));
-      return;
-    }
-  } else if (static_cast<int>(blockIdx.x) >= a.heads / QPW) {
-    prefetch_ranges(a, static_cast<int>(blockIdx.x) - a.heads / QPW, a.heads / QPW);
-    return;
-  }
   const HotArgs h = hot_args<FUSE, OFUSE>(a);
   // a batch of independent sequences: sequence blockIdx.y's length, pages
   // and rows of q8/qs/o8/os
@@ -361,7 +392,6 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
   // sectors and page table lines they have in common).
   // (the fused b = 1 variants never have row_pos: no test of it there)
   const bool batch = !FUSE && a.row_pos;
-  int bx = static_cast<int>(blockIdx.x), by = static_cast<int>(blockIdx.y);
   if (batch && (gridDim.y & 7) == 0) {
     const int nx = static_cast<int>(gridDim.x);
     const int id = bx + nx * by;
@@ -424,7 +454,7 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
   constexpr int kWosPerThread = (kORowsMax + NW * 64 - 1) / (NW * 64);
   float wosr[OFUSE ? kWosPerThread : 1];
   if constexpr (FUSE) {
-    fused_load<QPW>(h, kvh, qh0, wave, lane, fr);
+    fused_load<QPW, POLL>(h, kvh, qh0, wave, lane, fr);
     if constexpr (OFUSE) {
 #pragma unroll
       for (int i = 0; i < kWosPerThread; ++i) wosr[i] = h.wos[min(tid + i * NW * 64, h.o_rows - 1)];
@@ -512,11 +542,14 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
     // 22 loads per block: the last block is issued after the prologue, so
     // that the prologue does not stall on a full load counter (vmcnt holds
     // 63) waiting for the first block's data
+    // (POLL: all of them, the prologue waits for the projection anyway)
+    constexpr int NPRE = (FIRST && POLL) ? BPW : BPW - 1;
 #pragma unroll
-    for (int i = 0; i < BPW - 1; ++i) issue_block(i);
+    for (int i = 0; i < NPRE; ++i) issue_block(i);
     if constexpr (FIRST) __builtin_amdgcn_sched_barrier(0);
     if constexpr (FIRST) {
       // ---- prologue (overlaps the loads above) ----
+      if constexpr (POLL) attn_poll_rows<QPW>(a, qh0, wave, lane, fr);
       if constexpr (OFUSE) {
 #pragma unroll
         for (int i = 0; i < kWosPerThread; ++i)
@@ -538,7 +571,7 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
         qscale[h] = sm.qs[h];
       }
     }
-    issue_block(BPW - 1);
+    if constexpr (NPRE < BPW) issue_block(BPW - 1);
     // The new token (position kv_len - 1) comes from the prologue's LDS copy
     // (FUSE), patched into a block's K words just before its scores and into
     // its V words and scales just before their first use: the select reads
@@ -830,6 +863,124 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
   }
 }
 
+template <int QPW, int NW, int BPW, bool FUSE, bool OFUSE = false>
+__global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
+  // prefetch workgroups: grid rows y >= 1 of the fused (b = 1) variants, so
+  // that telling them apart needs no kernel argument; else x >= heads / QPW
+  if constexpr (FUSE) {
+    if (blockIdx.y > 0) {
+      const int w = static_cast<int>((blockIdx.y - 1) * gridDim.x + blockIdx.x);
+      if (w < a.pf_wgs) prefetch_ranges(a, w, static_cast<int>(gridDim.x));
+      return;
+    }
+  } else if (static_cast<int>(blockIdx.x) >= a.heads / QPW) {
+    prefetch_ranges(a, static_cast<int>(blockIdx.x) - a.heads / QPW, a.heads / QPW);
+    return;
+  }
+  attn_decode_body<QPW, NW, BPW, FUSE, OFUSE>(a, static_cast<int>(blockIdx.x), static_cast<int>(blockIdx.y));
+}
+
+// ---- one launch for a decode token's Q|K|V projection and attention -----
+// A kernel boundary costs a launch (~1.6 us) plus the next kernel's first
+// dependent loads (~1 us: its operands come from the other XCDs' writes),
+// and the attention's K/V blocks then stream into 16 CUs behind them.  Here
+// workgroups 0 .. heads - 1 are the b = 1 attention (as attn_decode_kernel
+// <1, 12, 2, true, true>), the next gemv_wgs compute the projection (the
+// whole-row GEMV of k_gemv.hip, 12 waves of kFusedR rows each), and the rest
+// prefetch.  The attention workgroups issue their K/V loads at once and
+// poll for their head's 384 projection values, which the GEMV workgroups
+// store as exchange words (AttnArgs::xin) besides the f32 rows.  The
+// producers never wait, so the launch completes whatever the dispatch order.
+constexpr int kFusedWaves = 12;
+constexpr int kFusedR = 2;  // projection rows per GEMV wave
+
+template <int PRO>
+__device__ __forceinline__ void qkv_gemv_role(const GemvArgs &a, const AttnArgs &t, int wg, int N) {
+  __shared__ float blk[32];
+  __shared__ __align__(16) int8_t a_lds[1024];
+  __shared__ float as_lds[4];
+  constexpr int R = kFusedR;
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_id();
+  ProSrc ps = read_src<PRO, false>(a);
+  int s_n0[3];
+  const int8_t *s_b[3];
+  const float *s_bs[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    s_n0[i] = a.seg[i].n0;
+    s_b[i] = a.seg[i].b;
+    s_bs[i] = a.seg[i].bs;
+  }
+  pin_src<PRO, false>(ps);
+  ProRow<1, 0> r0;
+  pro_load_row<PRO, 1, 0, kFusedWaves>(a, ps, 0, r0);
+  __builtin_amdgcn_sched_barrier(0);  // (issue order: prologue operands first)
+  const int row0 = (wg * kFusedWaves + wave) * R;
+  const int si = (row0 >= s_n0[1] ? 1 : 0) + (row0 >= s_n0[2] ? 1 : 0);
+  const int sg_n0 = si == 0 ? s_n0[0] : si == 1 ? s_n0[1] : s_n0[2];
+  const int8_t *const sg_b = si == 0 ? s_b[0] : si == 1 ? s_b[1] : s_b[2];
+  const float *const sg_bs = si == 0 ? s_bs[0] : si == 1 ? s_bs[1] : s_bs[2];
+  // the rows' scales and weights (rows past N reload row N - 1, unused)
+  int nr[R];
+  float bsn[R];
+  int4 w[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    nr[r] = min(row0 + r, N - 1) - sg_n0;
+    bsn[r] = sg_bs[nr[r]];
+    w[r] = *reinterpret_cast<const int4 *>(sg_b + static_cast<int64_t>(nr[r]) * 1024 + 16 * lane);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  pro_compute_row<PRO, 1, 0, kFusedWaves>(a, 0, r0, a_lds, as_lds, blk, wg == 0);  // ends with a barrier
+  const GemvSeg &sg = a.seg[si];
+  const int4 av = *reinterpret_cast<const int4 *>(a_lds + 16 * lane);
+  const float asg = as_lds[lane >> 4];
+  const int grp = t.heads / t.kv_heads;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    int acc = sdot4(w[r].x, av.x, 0);
+    acc = sdot4(w[r].y, av.y, acc);
+    acc = sdot4(w[r].z, av.z, acc);
+    acc = sdot4(w[r].w, av.w, acc);
+    acc += lane_xor<1>(acc);
+    acc += lane_xor<2>(acc);
+    acc += lane_xor<4>(acc);
+    acc += lane_xor<8>(acc);
+    // p_g = RN(RN(f32(I_g) * bs[n]) * as_g), summed in group order from +0
+    const float p = __fmul_rn(__fmul_rn(static_cast<float>(acc), bsn[r]), asg);
+    float out = 0.0f;
+    out = __fadd_rn(out, lane_bcast<0>(p));
+    out = __fadd_rn(out, lane_bcast<16>(p));
+    out = __fadd_rn(out, lane_bcast<32>(p));
+    out = __fadd_rn(out, lane_bcast<48>(p));
+    if (lane == 0 && row0 + r < N) {
+      sg.out[nr[r]] = out;
+      const unsigned long long word = (1ull << 32) | __float_as_uint(out);
+      if (si == 0) {
+        xstore(t.xin + nr[r], word);
+      } else {
+        const int kvh = nr[r] / HD, d = nr[r] % HD;
+        for (int c = 0; c < grp; ++c)
+          xstore(t.xin + (static_cast<int64_t>(si) * t.heads + kvh * grp + c) * HD + d, word);
+      }
+    }
+  }
+}
+
+template <int PRO>
+__global__ void __launch_bounds__(kFusedWaves * 64) qkv_attn_kernel(GemvArgs g, AttnArgs a, int gemv_wgs) {
+  const int bx = static_cast<int>(blockIdx.x);
+  if (bx < a.heads) {
+    attn_decode_body<1, kFusedWaves, 2, true, true, true>(a, bx, 0);
+  } else if (bx < a.heads + gemv_wgs) {
+    qkv_gemv_role<PRO>(g, a, bx - a.heads, g.seg[2].n1);
+  } else {
+    const int w = bx - a.heads - gemv_wgs;
+    if (w < a.pf_wgs) prefetch_ranges(a, w, a.heads + gemv_wgs);
+  }
+}
+
 // One workgroup per query head (QPW = 1): 16 workgroups for the 16/8-head
 // model instead of 8 halves the per-workgroup work, which matters more here
 // than reading each KV head's rows twice.  8 waves x 3 blocks (768 keys per
@@ -884,6 +1035,34 @@ bool attn_decode_supported(const AttnArgs &a) {
          (a.row_bytes % 16) == 0 && (a.page_tokens % 32) == 0 && al16(a.k) && al16(a.v) &&
          al16(a.q8) && (a.scale_row_bytes % 4) == 0 && (a.kv_len >= 1 || a.row_pos) && !a.kv_len_dev &&
          (!a.row_pos || (a.ldq % 16) == 0);
+}
+
+bool qkv_attn_supported(const GemvArgs &g, const AttnArgs &a) {
+  if (g.M != 1 || g.K != 1024 || g.group != 256 || g.bs_ld || g.part || g.nseg != 3) return false;
+  if (g.pro != PRO_NORM && g.pro != PRO_EMBED) return false;
+  const int HW = a.heads * HD, KW = a.kv_heads * HD;
+  if (g.seg[0].n0 != 0 || g.seg[0].n1 != HW || g.seg[1].n0 != HW || g.seg[1].n1 != HW + KW ||
+      g.seg[2].n0 != HW + KW || g.seg[2].n1 != HW + 2 * KW)
+    return false;
+  for (int i = 0; i < 3; ++i)
+    if (g.seg[i].epi != EPI_STORE || !g.seg[i].b || !g.seg[i].bs || !g.seg[i].out) return false;
+  if (HW % kFusedR || KW % kFusedR) return false;
+  // the attention: one query row, head epilogues and O projection fused,
+  // one workgroup per query head (launch_decode's b = 1 variant)
+  if (!a.xin || !a.xerr || !a.fuse_heads || !a.opart || a.row_pos || a.rows != 1 || a.heads % a.kv_heads) return false;
+  return attn_decode_supported(a);
+}
+
+hipError_t launch_qkv_attn(const GemvArgs &g, const AttnArgs &a, hipStream_t s) {
+  const int N = g.seg[2].n1;
+  const int gw = (N + kFusedWaves * kFusedR - 1) / (kFusedWaves * kFusedR);
+  const int extra = a.pf_n > 0 ? a.pf_wgs : 0;
+  const dim3 grid(a.heads + gw + extra);
+  if (g.pro == PRO_EMBED)
+    Q3_LAUNCH((qkv_attn_kernel<PRO_EMBED>), grid, dim3(kFusedWaves * 64), 0, s, g, a, gw);
+  else
+    Q3_LAUNCH((qkv_attn_kernel<PRO_NORM>), grid, dim3(kFusedWaves * 64), 0, s, g, a, gw);
+  return hipGetLastError();
 }
 
 hipError_t launch_attn_decode(const AttnArgs &a, hipStream_t s) {

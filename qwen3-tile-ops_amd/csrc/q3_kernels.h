@@ -292,6 +292,15 @@ struct AttnArgs {
   // workgroups on XCD x read the HD-byte slices of the kv heads of the query
   // heads h = x (mod 8) (of pf_kv_heads) of every row, and all the scales.
   int pf_kv_heads;
+  // fused Q|K|V + attention launch only (launch_qkv_attn): the projection's
+  // outputs as 64-bit words ((1 << 32) | f32 bits) stored by the GEMV
+  // workgroups and polled by the attention workgroups, which read them in
+  // place of fq/fk/fv and write 0 back: [Q: heads][K: heads][V: heads] x 128
+  // (K and V once per query head of their kv head, so that every word has
+  // one reader).  3 * heads * 128 zero-initialised words.  A poll that gives
+  // up (a lost workgroup: every wave still exits) sets *xerr to 1.
+  unsigned long long *xin;
+  uint32_t *xerr;
 };
 hipError_t launch_attention(const AttnArgs &a, hipStream_t s);
 // the two multi-row kernels behind launch_attention: the phase-parallel one
@@ -402,6 +411,15 @@ hipError_t launch_qkv_heads(const QkvHeadArgs &a, hipStream_t s);
 // ---- decode attention (one query row per head) ---------------------------
 bool attn_decode_supported(const AttnArgs &a);
 hipError_t launch_attn_decode(const AttnArgs &a, hipStream_t s);
+// One launch for a decode token's Q|K|V projection (g: M = 1, K = 1024,
+// group 256, three EPI_STORE segments Q | K | V, PRO_NORM or PRO_EMBED, as
+// launch_gemv takes them) and its attention with the head epilogues and the
+// O projection (a: fuse_heads, opart, one query row, a.xin set): the
+// attention workgroups load their K/V blocks and prefetch while the GEMV
+// workgroups (the rest of the grid) compute the projection, then take
+// their head's Q/K/V from a.xin.  g still writes its f32 outputs.
+bool qkv_attn_supported(const GemvArgs &g, const AttnArgs &a);
+hipError_t launch_qkv_attn(const GemvArgs &g, const AttnArgs &a, hipStream_t s);
 
 // ---- greedy pick over a logits row (main_big.cpp:300-322) ---------------
 hipError_t launch_argmax_logits(const float *logits, int vocab,

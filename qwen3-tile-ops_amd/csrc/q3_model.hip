@@ -55,6 +55,12 @@ struct q3_model {
   // decode (b = 1): the O projection's per-head partials [heads][hidden],
   // written by the attention kernel, summed by the gate/up and down GEMVs
   float *opart = nullptr;
+  // decode (b = 1): the Q|K|V projection in the attention's launch
+  // (Q3_DECODE_FUSE_QKV, default 1), its exchange words and give-up flag
+  // (AttnArgs::xin / xerr)
+  bool qkvfuse = true;
+  unsigned long long *xin = nullptr;
+  uint32_t *xerr = nullptr;
   // event timing of decode kernel classes (q3_model_set_kernel_timing)
   uint32_t kt_mask = 0;
   std::vector<hipEvent_t> kt_ev[Q3_KT_COUNT];  // start, end pairs
@@ -429,6 +435,8 @@ int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int opti
     const int M = static_cast<int>(tr);
 
     // Q | K | V projections; prologue = (embedding +) RMSNorm n1 + quant
+    // (launched below: with the attention when one launch takes both)
+    q3::GemvArgs gq;
     {
       q3::GemvArgs g = gemv_args(R, H, 256);
       if (L == 0) {
@@ -452,8 +460,7 @@ int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int opti
       g.seg[0] = gemv_seg(0, QW, q3::EPI_STORE, lp.wq, lp.wqs, q, QW);
       g.seg[1] = gemv_seg(QW, QW + KW, q3::EPI_STORE, lp.wk, lp.wks, k, KW);
       g.seg[2] = gemv_seg(QW + KW, QW + 2 * KW, q3::EPI_STORE, lp.wv, lp.wvs, v, KW);
-      KTimer kt(m, Q3_KT_GEMV_QKV);
-      Q3_HIP(q3::launch_gemv(g, s));
+      gq = g;
     }
     // paged GQA attention over kv_len = pos + rows keys
     q3::AttnArgs t{};
@@ -575,7 +582,19 @@ int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int opti
         t.pf_n = 0;
         t.pf_kv_heads = 0;
       }
-    } else {
+    }
+    bool qkvfuse = false;
+    if (ofuse && m->qkvfuse) {
+      t.xin = m->xin;
+      t.xerr = m->xerr;
+      qkvfuse = q3::qkv_attn_supported(gq, t);
+      if (!qkvfuse) t.xin = nullptr, t.xerr = nullptr;
+    }
+    if (!qkvfuse) {
+      KTimer kt(m, Q3_KT_GEMV_QKV);
+      Q3_HIP(q3::launch_gemv(gq, s));
+    }
+    if (!fuse) {
       // head epilogues: K (norm+RoPE+quant) and V (quant) of every row into
       // the page slots; Q (norm+RoPE+quant) of the tail rows
       q3::QkvHeadArgs e;
@@ -620,7 +639,10 @@ int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int opti
       }
     }
     if (!do_tail) continue;
-    if (q3::attn_decode_supported(t)) {
+    if (qkvfuse) {
+      KTimer kt(m, Q3_KT_ATTN_DECODE);
+      Q3_HIP(q3::launch_qkv_attn(gq, t, s));
+    } else if (q3::attn_decode_supported(t)) {
       KTimer kt(m, Q3_KT_ATTN_DECODE);
       Q3_HIP(q3::launch_attn_decode(t, s));
     } else {
@@ -1105,6 +1127,7 @@ extern "C" int q3_model_open(void *blob, const q3_layout *lay, void *stream, q3_
   if (const char *e = std::getenv("Q3_DECODE_PREFETCH_WGS")) m->pf_wgs = std::max(0, std::atoi(e));
   if (const char *e = std::getenv("Q3_DECODE_FUSE_OPROJ")) m->ofuse = std::atoi(e) != 0;
   if (const char *e = std::getenv("Q3_DECODE_GRAPH")) m->dgraph_on = std::atoi(e) != 0;
+  if (const char *e = std::getenv("Q3_DECODE_FUSE_QKV")) m->qkvfuse = std::atoi(e) != 0;
   m->bkeys_ld = lay->vocab / 128 + 64;  // one key per 128-column block of the lm GEMM
   m->btab_off = (sizeof(int32_t) * lay->seq + 255) & ~size_t(255);
   const size_t bstate_bytes = m->btab_off + sizeof(uint16_t) * static_cast<size_t>(lay->seq) * m->n_pages;
@@ -1122,6 +1145,14 @@ extern "C" int q3_model_open(void *blob, const q3_layout *lay, void *stream, q3_
       hipMalloc(&m->opart, sizeof(float) * lay->heads * lay->hidden) != hipSuccess) {
     q3_model_close(m);
     return Q3_ERR_HIP;
+  }
+  {
+    const size_t xbytes = sizeof(unsigned long long) * 3 * lay->heads * lay->head_dim;
+    if (hipMalloc(&m->xin, xbytes) != hipSuccess || hipMalloc(&m->xerr, sizeof(uint32_t)) != hipSuccess ||
+        hipMemset(m->xin, 0, xbytes) != hipSuccess || hipMemset(m->xerr, 0, sizeof(uint32_t)) != hipSuccess) {
+      q3_model_close(m);
+      return Q3_ERR_HIP;
+    }
   }
   m->bpos = reinterpret_cast<int32_t *>(m->bstate);
   m->btab = reinterpret_cast<uint16_t *>(m->bstate + m->btab_off);
@@ -1487,6 +1518,14 @@ extern "C" int q3_model_kernel_time(q3_model *m, int kclass, double *total_ms, u
   return Q3_OK;
 }
 
+extern "C" int q3_model_fused_status(q3_model *m, uint32_t *fused, uint32_t *gave_up) {
+  if (!m || !fused || !gave_up) return Q3_ERR_ARG;
+  *fused = m->qkvfuse ? 1u : 0u;
+  Q3_HIP(hipStreamSynchronize(m->stream));
+  Q3_HIP(hipMemcpy(gave_up, m->xerr, sizeof(uint32_t), hipMemcpyDeviceToHost));
+  return Q3_OK;
+}
+
 extern "C" int q3_model_set_page_table(q3_model *m, const uint16_t *table, uint32_t n) {
   if (!m || !table || n != m->n_pages) return Q3_ERR_ARG;
   for (uint32_t i = 0; i < n; ++i)
@@ -1594,6 +1633,8 @@ extern "C" int q3_model_close(q3_model *m) {
   if (m->bkeys) (void)hipFree(m->bkeys);
   if (m->bbest) (void)hipFree(m->bbest);
   if (m->opart) (void)hipFree(m->opart);
+  if (m->xin) (void)hipFree(m->xin);
+  if (m->xerr) (void)hipFree(m->xerr);
   if (m->dgraph) (void)hipGraphExecDestroy(m->dgraph);
   if (m->packed) (void)hipFree(m->packed);
   for (int c = 0; c < Q3_KT_COUNT; ++c)

@@ -89,6 +89,15 @@ class Model:
             out[name] = (ms.value, n.value)
         return out
 
+    def fused_status(self) -> tuple[int, int]:
+        """(1 if a decode token's Q|K|V projection shares the attention's
+        launch, 1 if one of its bounded waits ever ran out since open);
+        synchronises the model's stream."""
+        fused, gave_up = C.c_uint32(0), C.c_uint32(0)
+        check(lib().q3_model_fused_status(self.handle, C.byref(fused), C.byref(gave_up)),
+              "q3_model_fused_status")
+        return fused.value, gave_up.value
+
     def close(self) -> None:
         if self.handle:
             check(lib().q3_model_close(self.handle), "q3_model_close")

@@ -86,19 +86,23 @@ def test_cfg0_generate(cuda, mode, gold_meta):
     assert not probs, probs
 
 
-@pytest.mark.parametrize("fuse_oproj", ["0", "1"])
-def test_cfg0_generate_oproj_modes(cuda, gold_meta, fuse_oproj, monkeypatch):
+@pytest.mark.parametrize("fuse_oproj,fuse_qkv", [("0", "1"), ("1", "0"), ("1", "1")])
+def test_cfg0_generate_oproj_modes(cuda, gold_meta, fuse_oproj, fuse_qkv, monkeypatch):
     """Decode with the O projection inside the attention kernel (default) and
-    as its own GEMV (Q3_DECODE_FUSE_OPROJ=0, read when the model opens): the
+    as its own GEMV (Q3_DECODE_FUSE_OPROJ=0), and with the Q|K|V projection in
+    the attention's launch (default; it needs the fused O projection) or as
+    its own GEMV (Q3_DECODE_FUSE_QKV=0), both read when the model opens: the
     generated ids, logits and the last forward's stages match the goldens
-    either way."""
-    note(f"cfg0 generate fuse_oproj={fuse_oproj}")
+    either way, and no bounded wait of the fused launch ran out."""
+    note(f"cfg0 generate fuse_oproj={fuse_oproj} fuse_qkv={fuse_qkv}")
     monkeypatch.setenv("Q3_DECODE_FUSE_OPROJ", fuse_oproj)
+    monkeypatch.setenv("Q3_DECODE_FUSE_QKV", fuse_qkv)
     lay, blob = host_blob("cfg0")
     g = load_cfg("cfg0")
     m = Model(lay, blob)
     m.set_ctrl(40, 2, 1)
     m.generate()
+    assert m.fused_status() == (int(fuse_qkv), 0)
     ids = m.ids()
     assert np.array_equal(ids[40:42], g["generated"]), (ids[40:42], g["generated"])
     got = m.stage("logits", 1)[0]
@@ -206,6 +210,7 @@ def test_cfg3_greedy(cuda, gold_meta):
     g = load_cfg("cfg3")
     m = Model(lay, blob)
     m.generate()
+    assert m.fused_status() == (1, 0)  # decode on the fused Q|K|V + attention launch
     ids = m.ids()
     assert np.array_equal(ids[15:21], g["generated"]), (ids[15:21], g["generated"])
     best, idx = m.argmax()
