@@ -383,6 +383,16 @@ __device__ __forceinline__ void attn_decode_body(const AttnArgs &a, int bx, int 
   static_assert(!POLL || OFUSE, "polled projection rows: the fused b = 1 variant");
   __shared__ __align__(16) Smem<QPW, CB> sm;
   __shared__ __align__(16) SmemO<OFUSE> smo;
+  // workgroup barriers: POLL waits only for LDS (s_waitcnt lgkmcnt(0)), not
+  // for every outstanding vector memory operation as __syncthreads does,
+  // so that the O projection's weight pieces and the page-slot stores stay
+  // in flight across phases that do not read them
+  auto wg_barrier = []() {
+    if constexpr (POLL)
+      lds_barrier();
+    else
+      __syncthreads();
+  };
   const HotArgs h = hot_args<FUSE, OFUSE>(a);
   // a batch of independent sequences: sequence blockIdx.y's length, pages
   // and rows of q8/qs/o8/os
@@ -562,7 +572,7 @@ __device__ __forceinline__ void attn_decode_body(const AttnArgs &a, int bx, int 
         sm.q8[wave][lane + 64] = q8b;
         if (lane == 0) sm.qs[wave] = qsa;
       }
-      __syncthreads();
+      wg_barrier();
 #pragma unroll
       for (int h = 0; h < QPW; ++h) {
         const int *qp = reinterpret_cast<const int *>(sm.q8[h] + kb16);
@@ -646,7 +656,7 @@ __device__ __forceinline__ void attn_decode_body(const AttnArgs &a, int bx, int 
       issue_wo(0, kOPiecesEarly, b0 + CB >= nblocks);
       __builtin_amdgcn_sched_barrier(0);
     }
-    __syncthreads();
+    wg_barrier();
     // ---- phase 2: prefix max (attention_gqa.h:476-477) ----
     // nmm_j = max(run, bmax_0, ..., bmax_j), prev_j = nmm_{j-1} (run for
     // j = 0): every wave scans the block maxima itself (lanes 32 h + j hold
@@ -779,7 +789,7 @@ __device__ __forceinline__ void attn_decode_body(const AttnArgs &a, int bx, int 
       issue_wo(kOPiecesEarly, kOPieces, b0 + CB >= nblocks);
       __builtin_amdgcn_sched_barrier(0);
     }
-    __syncthreads();
+    wg_barrier();
     // ---- phase 4: the sequential den/res chain (attention_gqa.h:476-519) ----
     // Batches: operands of 8 blocks are read before their 8 chain steps
     // (entries past nb are read, in bounds, and not used); at b = 1 (up to
@@ -826,7 +836,7 @@ __device__ __forceinline__ void attn_decode_body(const AttnArgs &a, int bx, int 
     const float m = max64(fabsf(out));
     if (lane == 0) sm.absmax[ph][(tid % HD) / 64] = m;
   }
-  __syncthreads();
+  wg_barrier();
   if (tid < QPW * HD) {
     const int qh = qh0 + ph;
     const float scale = __fmul_rn(fmaxf(sm.absmax[ph][0], sm.absmax[ph][1]), inv127());
@@ -843,7 +853,7 @@ __device__ __forceinline__ void attn_decode_body(const AttnArgs &a, int bx, int 
     // O projection partials of this head: 8 lanes per row n, 16 columns
     // each (exact int32 dot products, summed across the 8 lanes), then the
     // two dequant roundings of the group GEMM
-    __syncthreads();
+    wg_barrier();
     const int *op = reinterpret_cast<const int *>(sm.o8 + 16 * (tid & 7));
     const int o0 = op[0], o1 = op[1], o2 = op[2], o3 = op[3];
     const float osh = sm.os;
