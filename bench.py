@@ -499,8 +499,9 @@ def host_cores() -> tuple[int, int]:
 def cpu_baseline(threads: int, nproc: int, runs: int = 5) -> dict:
     """The CPU oracle (oracle/, the C port of tools/ref_qwen3.py) on the same
     workload: the median of `runs` timed generations on `threads` OpenMP
-    threads, and a 1-thread line on a bounded sample (32-token prefill + 4
-    greedy steps, median of 3), both after one untimed warm run."""
+    threads after one untimed warm run, and a 1-thread line on the same
+    workload (512-token prefill + 64 greedy steps, one run of ~25 s; the
+    threaded runs warmed the caches)."""
     import numpy as np
     import oracle
     from q3ops.layout import CONFIGS, Layout, init_random_blob
@@ -511,30 +512,33 @@ def cpu_baseline(threads: int, nproc: int, runs: int = 5) -> dict:
     om = oracle.OracleModel(blob, lay.offsets, dict(shape.__dict__))
     ids = lay.global_views(blob)["ids"]
 
-    def timed(n_prompt, n_gen, reps):
+    def timed(n_prompt, n_gen, reps, warm=True):
         out, ts = None, []
-        for _ in range(reps + 1):  # the first run warms caches and pages
+        for _ in range(reps + (1 if warm else 0)):  # a first run warms caches and pages
             om.reset_cache()
             t0 = time.perf_counter()
             _, gen, _, _ = om.generate(ids, n_prompt, n_gen, record=False)
             ts.append(time.perf_counter() - t0)
             out = gen
-        return sorted(ts[1:])[len(ts[1:]) // 2], ts[1:], out
+        ts = ts[1:] if warm else ts
+        return sorted(ts)[len(ts) // 2], ts, out
 
     oracle.set_threads(threads)
     med, ts, gen = timed(N_PROMPT, N_GEN, runs)
     oracle.set_threads(1)
-    med1, ts1, _ = timed(32, 4, 3)
+    med1, ts1, gen1 = timed(N_PROMPT, N_GEN, 1, warm=False)
     oracle.set_threads(threads)
+    assert np.array_equal(np.asarray(gen1), np.asarray(gen)), "1-thread oracle run differs"
     return {"value": (N_PROMPT + N_GEN) / med, "unit": "tok/s", "cores": threads, "kind": "port",
             "sample": (f"the full workload (512-token prefill + 64 greedy decode steps), median of "
                        f"{runs} runs ({med:.2f} s) after a warm run: oracle/ C port of "
                        f"tools/ref_qwen3.py on {threads} OpenMP threads (nproc {nproc}; one GPU's "
                        f"share of the box is 16 CPUs)"),
             "nproc": nproc, "runs_s": [round(t, 3) for t in ts],
-            "one_thread": {"value": 36 / med1, "unit": "tok/s", "cores": 1,
-                           "sample": (f"32-token prefill + 4 greedy steps of the same model and "
-                                      f"prompt, median of 3 runs ({med1:.2f} s), 1 thread"),
+            "one_thread": {"value": (N_PROMPT + N_GEN) / med1, "unit": "tok/s", "cores": 1,
+                           "sample": (f"the same workload (512-token prefill + 64 greedy decode "
+                                      f"steps), one run ({med1:.2f} s) on 1 thread after the "
+                                      f"threaded runs; same generated ids"),
                            "runs_s": [round(t, 3) for t in ts1]},
             "generated": [int(v) for v in np.asarray(gen)]}
 

@@ -18,7 +18,14 @@
  *    allocates, except that the first call on a stream of
  *    q3_gemm_nt_group_argmax, or of q3_gemm_gate_up_swiglu_quant with at most
  *    64 rows, allocates that stream's 4 MiB workspace (kept until the
- *    process ends; calls on one stream share it in stream order).
+ *    process ends; calls on one stream share it in stream order).  The
+ *    workspace is keyed by the hipStream_t value: a stream created after
+ *    another was destroyed may get the same handle and then shares its
+ *    workspace, so work still queued on a destroyed stream must finish
+ *    first.  Under graph capture on a stream that has no workspace yet, the
+ *    gate/up op takes its fused kernel instead (no workspace, no allocation),
+ *    while q3_gemm_nt_group_argmax would allocate: call it once on the stream
+ *    before capturing, or use q3_gemm_nt_group_argmax_noalloc.
  *  - Every function returns an int status: Q3_OK (0) or a negative Q3_ERR_*.
  *    The reference silently returns on unsupported shapes
  *    (kernels/group_gemm.h:47-49, kernels/lm_argmax.h:82); that behaviour is
@@ -186,7 +193,9 @@ int q3_attention_heads_gqa_tokscale_paged(const q3_view *q8,
  * into s8 [M][I] / ss [M][I/256].  With M <= 64 (contiguous weight rows,
  * per-row weight scales, I < 65536, M * I * 4 bytes within the 4 MiB
  * workspace) the SwiGLU rows pass through the stream's workspace between a
- * GEMV over every CU and the quantisation. */
+ * GEMV over every CU and the quantisation; on a stream capturing a graph
+ * that has no workspace yet it runs the fused kernel of larger M instead
+ * (bit-identical results). */
 int q3_gemm_gate_up_swiglu_quant(const q3_view *a, const q3_view *a_scale,
                                  const q3_view *wg, const q3_view *wgs,
                                  const q3_view *wu, const q3_view *wus,

@@ -75,9 +75,28 @@ def build(jobs: int = 0, verbose: bool = False) -> Path:
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
           *map(str, objs), "-pthread"])
     os.replace(tmp, OUT)
+    build_c_driver()
     if verbose:
         print(f"built {OUT}")
     return OUT
+
+
+C_DRIVER_SRC = REPO / "tests" / "c_abi" / "generate_cfg0.cpp"
+C_DRIVER = REPO / "tests" / "c_abi" / "bin" / "generate_cfg0"
+
+
+def build_c_driver() -> Path | None:
+    """A C++ caller of the model-level ABI (tests/c_abi/generate_cfg0.cpp),
+    linked against libq3ops.so and the HIP runtime; the GPU test runs it."""
+    if not C_DRIVER_SRC.exists():
+        return None
+    C_DRIVER.parent.mkdir(parents=True, exist_ok=True)
+    rel = os.path.relpath(OUT.parent, C_DRIVER.parent)
+    _run(["g++", "-std=c++17", "-O2", "-Wall", "-Werror", "-D__HIP_PLATFORM_AMD__",
+          f"-I{ROCM / 'include'}", f"-I{REPO / 'include'}", str(C_DRIVER_SRC),
+          f"-L{OUT.parent}", "-lq3ops", f"-L{ROCM / 'lib'}", "-lamdhip64",
+          f"-Wl,-rpath,$ORIGIN/{rel}:{ROCM / 'lib'}", "-o", str(C_DRIVER)])
+    return C_DRIVER
 
 
 def main() -> int:

@@ -582,10 +582,10 @@ bool attn_prefill_supported(const AttnArgs &a) {
 hipError_t launch_attn_prefill(const AttnArgs &a, hipStream_t s) {
   if (a.rows <= 0) return hipSuccess;
   if (!attn_prefill_supported(a)) return hipErrorInvalidValue;
-  static const bool pair = [] {
-    const char *e = std::getenv("Q3_PREFILL_ATTN");
-    return e && std::strcmp(e, "pair") == 0;
-  }();
+  // Q3_PREFILL_ATTN=pair: both blocks of a causal pair in one 16-wave
+  // workgroup (a measured alternative; read at every launch)
+  const char *ev = std::getenv("Q3_PREFILL_ATTN");
+  const bool pair = ev && std::strcmp(ev, "pair") == 0;
   static bool attr_set[2] = {false, false};  // more than 64 KiB of dynamic LDS must be allowed once
   const int nqb = (a.rows + QB - 1) / QB;
   if (pair) {
@@ -609,10 +609,11 @@ hipError_t launch_attn_prefill(const AttnArgs &a, hipStream_t s) {
 }
 
 hipError_t launch_attention(const AttnArgs &a, hipStream_t s) {
-  static const bool walk = [] {
-    const char *e = std::getenv("Q3_PREFILL_ATTN");
-    return e && std::strcmp(e, "walk") == 0;
-  }();
+  // Q3_PREFILL_ATTN=walk: the block-order walk (k_attention.hip) even where
+  // the phase-parallel kernel applies (read at every launch); page sizes the
+  // latter does not take (not a power of two) always walk
+  const char *ev = std::getenv("Q3_PREFILL_ATTN");
+  const bool walk = ev && std::strcmp(ev, "walk") == 0;
   if (walk || !attn_prefill_supported(a)) return launch_attention_walk(a, s);
   return launch_attn_prefill(a, s);
 }

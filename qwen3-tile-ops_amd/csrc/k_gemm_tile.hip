@@ -481,10 +481,10 @@ bool gemm_tile_supported(const TileArgs &a, int epi) {
 
 hipError_t launch_gemm_tile(const TileArgs &a, int epi, hipStream_t s) {
   if (a.M <= 0) return hipSuccess;
-  static const bool stream_ok = [] {
-    const char *e = std::getenv("Q3_PREFILL_GEMM");
-    return !(e && std::strcmp(e, "tile") == 0);
-  }();
+  // Q3_PREFILL_GEMM=tile: the LDS-staged tile kernel for row-major weights
+  // even where the stream kernel applies (read at every launch)
+  const char *ev = std::getenv("Q3_PREFILL_GEMM");
+  const bool stream_ok = !(ev && std::strcmp(ev, "tile") == 0);
   if ((stream_ok || a.b_packed) && gemm_stream_supported(a, epi)) return launch_gemm_stream(a, epi, s);
   if (a.b_packed) return hipErrorInvalidValue;  // only the stream kernel reads packed weights
   if (!gemm_tile_supported(a, epi)) return hipErrorInvalidValue;

@@ -197,6 +197,9 @@ int check_paged(const q3_paged_kv *kv) {
 // process ends.  Defined with the argmax entry points below.
 constexpr int64_t kWorkspaceBytes = int64_t(8) << 19;  // 4 MiB
 unsigned long long *stream_keys(hipStream_t s);
+// The stream's workspace if it has one already, or if it may be allocated
+// now (the stream is not capturing a graph); else null.
+unsigned long long *stream_keys_if_free(hipStream_t s);
 
 }  // namespace
 
@@ -523,8 +526,10 @@ int q3_gemm_gate_up_swiglu_quant(const q3_view *a, const q3_view *a_scale,
   // those rows (quant.h:89-138, the same arithmetic as swiglu_quant.h:197-231)
   if (u.ldw == u.K && u.ws_stride == 1 && u.ss_col == 1 && q3::gemv_rows_supported(u.M, u.K, u.group, u.N) &&
       static_cast<int64_t>(u.M) * u.N * 4 <= kWorkspaceBytes) {
-    float *tmp = reinterpret_cast<float *>(stream_keys(s));
-    if (!tmp) return Q3_ERR_HIP;
+    // (a stream capturing a graph without a workspace yet takes the fused
+    // kernel below instead: no allocation inside a capture)
+    float *tmp = reinterpret_cast<float *>(stream_keys_if_free(s));
+    if (!tmp) return hip_status(q3::launch_gate_up(u, s));
     q3::GemvArgs v;
     std::memset(&v, 0, sizeof(v));
     v.M = u.M;
@@ -586,17 +591,24 @@ struct StreamKeys {
 std::mutex g_stream_keys_mu;
 std::vector<StreamKeys> g_stream_keys;
 
-unsigned long long *stream_keys(hipStream_t s) {
+unsigned long long *stream_keys_impl(hipStream_t s, bool only_if_free) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return nullptr;
   std::lock_guard<std::mutex> lock(g_stream_keys_mu);
   for (const StreamKeys &e : g_stream_keys)
     if (e.dev == dev && e.stream == s) return e.keys;
+  if (only_if_free) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
+  }
   void *p = nullptr;
   if (hipMalloc(&p, sizeof(unsigned long long) * kArgmaxSlots) != hipSuccess) return nullptr;
   g_stream_keys.push_back({dev, s, static_cast<unsigned long long *>(p)});
   return static_cast<unsigned long long *>(p);
 }
+
+unsigned long long *stream_keys(hipStream_t s) { return stream_keys_impl(s, false); }
+unsigned long long *stream_keys_if_free(hipStream_t s) { return stream_keys_impl(s, true); }
 
 // q3_gemm_nt_group_argmax_noalloc: a fixed key array in the library's own
 // device image (each device holds its own copy until the process ends).  In

@@ -309,6 +309,86 @@ def test_cfg3_prefill_512_generate(cuda):
     m.close()
 
 
+def oracle_span(om, ids, pos, rows, record):
+    """The oracle over positions [pos, pos + rows) in chunks of at most 32
+    rows (its layout's seq), logits of the last row; records concatenated."""
+    recs, logits, p = [], None, pos
+    while p < pos + rows:
+        n = min(32, pos + rows - p)
+        last = p + n == pos + rows
+        lg, rec = om.forward_chunk(ids[p:p + n], p, n, last, record=record)
+        if record:
+            recs.append(rec)
+        if last:
+            logits = lg
+        p += n
+    ref = {k: np.concatenate([r[k] for r in recs]) for k in recs[0]} if record else None
+    return ref, logits
+
+
+@pytest.mark.parametrize("packed", ["1", "0"])
+@pytest.mark.parametrize("pos,rows", [(0, 100), (512, 88)])
+def test_prefill_partial_tiles_and_offset(cuda, monkeypatch, packed, pos, rows):
+    """Prefill chunks that do not fill the stream GEMM's 32-row tiles (rows
+    past the chunk are computed on clamped rows and not stored), at position
+    0 and at 512 after a 512-row chunk, on the weights packed at model open
+    (default) and on the row-major blob (Q3_PACKED_WEIGHTS=0): every recorded
+    stage of the chunk's last layer, both layers' K/V pages and scales for
+    all positions so far, and the logits, against the oracle in 32-row chunks."""
+    note(f"prefill chunk pos={pos} rows={rows} packed={packed}")
+    monkeypatch.setenv("Q3_PACKED_WEIGHTS", packed)
+    lay, blob = host_blob("cfg3_perf", shape=SHAPE_512, init=INIT_512)
+    om = oracle_512(blob, lay)
+    ids = lay.global_views(blob)["ids"][:pos + rows].copy()
+    if pos:
+        oracle_span(om, ids, 0, pos, record=False)
+    ref, logits = oracle_span(om, ids, pos, rows, record=True)
+    m = Model(lay, blob)
+    tab = np.arange(lay.max_seq // 32, dtype=np.uint16)
+    np.random.default_rng(9).shuffle(tab)
+    m.set_page_table(tab)
+    if pos:
+        m.forward_chunk(0, pos, LM_NONE, optimize_tail=False)
+    m.forward_chunk(pos, rows, LM_LOGITS, optimize_tail=False)
+    probs = []
+    got = m.stage("logits", 1)[0]
+    if not bits_equal(got, logits):
+        probs.append(f"logits: {describe_diff(got, logits)}")
+    for st in ("h", "h8", "hs", "q8", "qs", "o8", "os", "s8", "ss", "x"):
+        g, e = m.stage(st, rows), ref[st]
+        if st in ("q8", "qs"):  # row 0 doubles as the final-norm scratch (compare.py:197-205)
+            g, e = g[1:], e[1:]
+        if not bits_equal(g, e):
+            probs.append(f"{st}: {describe_diff(g, e)}")
+    for li in range(lay.layers):
+        caches = m.kv_cache(li, pos + rows)
+        for st, arr in (("kc", om.k8), ("ks", om.k_s), ("vc", om.v8), ("vs", om.v_s)):
+            e = arr[li, :pos + rows]
+            if not bits_equal(caches[st], e):
+                probs.append(f"layer {li} {st}: {describe_diff(caches[st], e)}")
+    m.close()
+    assert not probs, probs
+
+
+def test_generate_300_token_prompt(cuda):
+    """q3_generate with CTRL [300, 4, mode 0]: one 300-row prefill chunk (a
+    partial last tile of the stream GEMMs, packed weights) and four greedy
+    decode steps: the ids and the fused argmax equal the oracle's."""
+    note("300-token prompt + 4 greedy tokens, 2 layers")
+    lay, blob = host_blob("cfg3_perf", shape=SHAPE_512, init=INIT_512)
+    om = oracle_512(blob, lay)
+    logits, gen, _, _ = om.generate(lay.global_views(blob)["ids"], 300, 4, record=False)
+    m = Model(lay, blob)
+    m.set_ctrl(300, 4, 0)
+    m.generate()
+    got = m.ids()[300:304].copy()
+    best, idx = m.argmax()
+    assert m.fused_status() == (1, 0)
+    m.close()
+    assert np.array_equal(got, gen), (got, gen)
+    assert idx == int(np.argmax(logits)) and bits_equal(np.float32(best), logits.max())
+
+
 def test_generate_decode_graph_replays(cuda, monkeypatch):
     """On a stream of its own, q3_generate captures its decode steps as one
     HIP graph and replays it while CTRL and the page table stay the same.

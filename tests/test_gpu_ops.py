@@ -72,6 +72,41 @@ def test_gemm_2048_rows(cuda, K, N, group):
     assert bits_equal(got, ref), describe_diff(got, ref)
 
 
+@pytest.mark.parametrize("M", [100, 512])
+@pytest.mark.parametrize("K,N,group", [(1024, 2048, 256), (3072, 1024, 256), (2048, 1024, 128)])
+def test_gemm_tile_variant(cuda, monkeypatch, M, K, N, group):
+    """Q3_PREFILL_GEMM=tile (read at every launch): the LDS-staged tile
+    kernel in place of the stream kernel for row-major weights, with the
+    plain store, the residual add and the per-head quant epilogues, and the
+    gate/up SwiGLU + quant at M = 512, against the oracle."""
+    note(f"gemm tile variant M={M} K={K} N={N} g={group}")
+    monkeypatch.setenv("Q3_PREFILL_GEMM", "tile")
+    rng = np.random.default_rng(3 * M + K + N)
+    a, as_, b, bs = rand_gemm(rng, M, K, N, group)
+    ref = oracle.gemm_nt_group(a, as_, b, bs, group)
+    out = torch.zeros((M, N), dtype=torch.float32, device=cuda)
+    ops.gemm_nt_group_store(dev(a), dev(as_), dev(b), dev(bs), out, group)
+    assert bits_equal(host(out), ref), describe_diff(host(out), ref)
+    x = rng.normal(size=(M, N)).astype(F)
+    xt = dev(x)
+    ops.gemm_nt_group_store(dev(a), dev(as_), dev(b), dev(bs), None, group, add=xt)
+    assert bits_equal(host(xt), (ref + x).astype(F))
+    q8 = torch.zeros((M, N), dtype=torch.int8, device=cuda)
+    qs = torch.zeros((M, N // 128), dtype=torch.float32, device=cuda)
+    ops.gemm_nt_group_store(dev(a), dev(as_), dev(b), dev(bs), None, group, q8=q8, qs=qs)
+    rq, rs = oracle.quant_rows_heads(ref, 128)
+    assert bits_equal(host(q8), rq) and bits_equal(host(qs), rs)
+    if K == 1024 and M == 512:
+        _, _, wu, wus = rand_gemm(rng, M, 1024, 3072, 256)
+        _, _, wg, wgs = rand_gemm(rng, M, 1024, 3072, 256)
+        s8 = torch.zeros((M, 3072), dtype=torch.int8, device=cuda)
+        ss = torch.zeros((M, 12), dtype=torch.float32, device=cuda)
+        ops.gemm_gate_up_swiglu_quant(dev(a), dev(as_), dev(wg), dev(wgs), dev(wu), dev(wus), s8, ss, 256)
+        rs8, rss = oracle.quant_rows_heads(oracle.swiglu(oracle.gemm_nt_group(a, as_, wg, wgs, 256),
+                                                         oracle.gemm_nt_group(a, as_, wu, wus, 256)), 256)
+        assert bits_equal(host(s8), rs8) and bits_equal(host(ss), rss)
+
+
 def test_gemm_golden_guest_fixture(cuda):
     g = golden("ops.npz")
     for group, key, ns in ((128, "gg_out128", 2), (256, "gg_out256", 1)):
@@ -194,24 +229,80 @@ def test_norm_rope_quant_heads_unfused(cuda):
     assert bits_equal(host(q8), rq) and bits_equal(host(qs), rs)
 
 
-def make_pages(rng, kv_len, kv_dim, kv_heads, n_pages, shuffle=True):
+def make_pages(rng, kv_len, kv_dim, kv_heads, n_pages, shuffle=True, page_tokens=32):
     table = np.arange(n_pages, dtype=np.uint16)
     if shuffle:
         rng.shuffle(table)
+    P = page_tokens
     k8 = rng.integers(-127, 128, (kv_len, kv_dim)).astype(np.int8)
     v8 = rng.integers(-127, 128, (kv_len, kv_dim)).astype(np.int8)
     ks = rng.uniform(1e-3, 5e-2, (kv_len, kv_heads)).astype(F)
     vs = rng.uniform(1e-3, 5e-2, (kv_len, kv_heads)).astype(F)
-    kp = rng.integers(-127, 128, (n_pages, 32, kv_dim)).astype(np.int8)  # garbage elsewhere
-    vp = rng.integers(-127, 128, (n_pages, 32, kv_dim)).astype(np.int8)
-    ksp = np.full((n_pages, 32, kv_heads), np.nan, F)
-    vsp = np.full((n_pages, 32, kv_heads), np.nan, F)
+    kp = rng.integers(-127, 128, (n_pages, P, kv_dim)).astype(np.int8)  # garbage elsewhere
+    vp = rng.integers(-127, 128, (n_pages, P, kv_dim)).astype(np.int8)
+    ksp = np.full((n_pages, P, kv_heads), np.nan, F)
+    vsp = np.full((n_pages, P, kv_heads), np.nan, F)
     t = np.arange(kv_len)
-    kp[table[t // 32], t % 32] = k8
-    vp[table[t // 32], t % 32] = v8
-    ksp[table[t // 32], t % 32] = ks
-    vsp[table[t // 32], t % 32] = vs
+    kp[table[t // P], t % P] = k8
+    vp[table[t // P], t % P] = v8
+    ksp[table[t // P], t % P] = ks
+    vsp[table[t // P], t % P] = vs
     return (k8, v8, ks, vs), (kp, vp, ksp, vsp, table)
+
+
+@pytest.mark.parametrize("page_tokens", [64, 96, 128])
+@pytest.mark.parametrize("rows,kv_len", [(1, 1), (1, 200), (1, 1100), (40, 40), (33, 250),
+                                         (100, 700)])
+def test_attention_page_sizes(cuda, page_tokens, rows, kv_len):
+    """PagedKV.page_tokens other than 32 (kernels/kv_pages.h:13-24; the walk
+    divides by it, attention_gqa.h:462-463): 64 and 128 take the
+    phase-parallel prefill kernel, 96 the block-order walk (not a power of
+    two); one row takes the decode kernel; blocks start mid-page, and pages
+    come from a shuffled table with garbage in the unused slots."""
+    note(f"attention page_tokens={page_tokens} rows={rows} kv_len={kv_len}")
+    rng = np.random.default_rng(page_tokens * 7 + rows * 1000 + kv_len)
+    heads, kvh = 16, 8
+    n_pages = (kv_len + page_tokens - 1) // page_tokens + 2
+    (k8, v8, ks, vs), (kp, vp, ksp, vsp, table) = make_pages(rng, kv_len, kvh * 128, kvh, n_pages,
+                                                             page_tokens=page_tokens)
+    q8 = rng.integers(-127, 128, (rows, heads * 128)).astype(np.int8)
+    qs = rng.uniform(1e-3, 5e-2, (rows, heads)).astype(F)
+    kv = ops.paged_kv(dev(kp), dev(vp), dev(ksp), dev(vsp), dev(table.view(np.int16)), page_tokens)
+    o8 = torch.zeros((rows, heads * 128), dtype=torch.int8, device=cuda)
+    os_ = torch.zeros((rows, heads), dtype=torch.float32, device=cuda)
+    ops.attention_heads_gqa_tokscale_paged(dev(q8), dev(qs), kv, kv_len, o8, os_, heads, kvh, 128,
+                                           True, QK)
+    attn = oracle.attention_heads_gqa_tokscale(q8, qs, k8, ks, v8, vs, heads, kvh, 128, True, QK)
+    ro8, ros = oracle.quant_rows_heads(attn, 128)
+    assert bits_equal(host(o8), ro8), describe_diff(host(o8), ro8)
+    assert bits_equal(host(os_), ros), describe_diff(host(os_), ros)
+
+
+@pytest.mark.parametrize("variant", ["walk", "pair"])
+@pytest.mark.parametrize("rows,kv_len,causal", [(512, 512, True), (100, 1000, True), (48, 300, True),
+                                                (40, 300, False)])
+def test_attention_prefill_variants(cuda, monkeypatch, variant, rows, kv_len, causal):
+    """The multi-row attention forms Q3_PREFILL_ATTN selects (read at every
+    launch): the block-order walk and the causal pair in one workgroup give
+    the oracle's bytes like the default phase-parallel kernel."""
+    note(f"attention prefill variant={variant} rows={rows} kv_len={kv_len} causal={causal}")
+    monkeypatch.setenv("Q3_PREFILL_ATTN", variant)
+    rng = np.random.default_rng(rows * 13 + kv_len)
+    heads, kvh = 16, 8
+    n_pages = (kv_len + 31) // 32 + 2
+    (k8, v8, ks, vs), (kp, vp, ksp, vsp, table) = make_pages(rng, kv_len, kvh * 128, kvh, n_pages)
+    q8 = rng.integers(-127, 128, (rows, heads * 128)).astype(np.int8)
+    qs = rng.uniform(1e-3, 5e-2, (rows, heads)).astype(F)
+    kv = ops.paged_kv(dev(kp), dev(vp), dev(ksp), dev(vsp), dev(table.view(np.int16)))
+    o8 = torch.zeros((rows, heads * 128), dtype=torch.int8, device=cuda)
+    os_ = torch.zeros((rows, heads), dtype=torch.float32, device=cuda)
+    ops.attention_heads_gqa_tokscale_paged(dev(q8), dev(qs), kv, kv_len, o8, os_, heads, kvh, 128,
+                                           causal, QK)
+    torch.cuda.synchronize()
+    attn = oracle.attention_heads_gqa_tokscale(q8, qs, k8, ks, v8, vs, heads, kvh, 128, causal, QK)
+    ro8, ros = oracle.quant_rows_heads(attn, 128)
+    assert bits_equal(host(o8), ro8), describe_diff(host(o8), ro8)
+    assert bits_equal(host(os_), ros), describe_diff(host(os_), ros)
 
 
 @pytest.mark.parametrize("rows,kv_len", [(1, 1), (1, 33), (1, 600), (4, 80), (8, 48),
@@ -392,6 +483,34 @@ def test_gate_up_swiglu_quant_strided_weights_two_streams(cuda):
     torch.cuda.synchronize()
     for o8, os_ in outs:
         assert bits_equal(host(o8), rs8) and bits_equal(host(os_), rss)
+
+
+@pytest.mark.parametrize("M", [1, 16, 64])
+def test_gate_up_swiglu_quant_graph_capture_fresh_stream(cuda, M):
+    """The decode-shaped gate/up captured in a HIP graph on a stream that has
+    never run it (so it has no workspace and must not allocate inside the
+    capture: it takes the fused kernel), then replayed three times with eager
+    work in between: every replay gives the oracle's bytes."""
+    rng = np.random.default_rng(90 + M)
+    a, as_, wg, wgs = rand_gemm(rng, M, 1024, 3072, 256)
+    _, _, wu, wus = rand_gemm(rng, M, 1024, 3072, 256)
+    rs8, rss = oracle.quant_rows_heads(oracle.swiglu(oracle.gemm_nt_group(a, as_, wg, wgs, 256),
+                                                     oracle.gemm_nt_group(a, as_, wu, wus, 256)), 256)
+    args = (dev(a), dev(as_), dev(wg), dev(wgs), dev(wu), dev(wus))
+    s8 = torch.zeros((M, 3072), dtype=torch.int8, device=cuda)
+    ss = torch.zeros((M, 12), dtype=torch.float32, device=cuda)
+    torch.cuda.synchronize()
+    st = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=st):
+        ops.gemm_gate_up_swiglu_quant(*args, s8, ss, 256, stream=st)
+    for rep in range(3):
+        s8.fill_(0)
+        ss.fill_(0.0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert bits_equal(host(s8), rs8) and bits_equal(host(ss), rss), (M, rep)
 
 
 def test_gate_up_guest_fixture(cuda):

@@ -62,3 +62,36 @@ def test_noalloc_matches_allocating_entry(cuda, first, second):
         assert bits_equal(nb, ab), (M, N)
         assert ai.tolist() == [int(i) for i in np.argmax(logits, axis=1)], (M, N)
         assert bits_equal(ab, logits.max(axis=1)), (M, N)
+
+
+def test_noalloc_under_graph_capture_fresh_stream(cuda):
+    """The entry point inside a HIP graph captured on a stream that never ran
+    an argmax (an allocation there would break the capture), replayed twice
+    with (best, bidx) reset eagerly in between, each replay against the
+    oracle; then a smaller eager call on the same device."""
+    rng = np.random.default_rng(7)
+    M, N, K, group = 4, 151936, 1024, 256
+    a = rng.integers(-127, 128, (M, K)).astype(np.int8)
+    b = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    as_ = rng.uniform(1e-3, 1e-1, (M, K // group)).astype(F)
+    bs = rng.uniform(1e-3, 1e-1, N).astype(F)
+    logits = oracle.gemm_nt_group(a, as_, b, bs, group)
+    ta, tas, tb, tbs = dev(a), dev(as_), dev(b), dev(bs)
+    best = torch.full((M,), -3.0e38, dtype=torch.float32, device="cuda")
+    bidx = torch.full((M,), -1, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    st = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    note("argmax noalloc captured on a fresh stream")
+    with torch.cuda.graph(graph, stream=st):
+        ops.gemm_nt_group_argmax_noalloc(ta, tas, tb, tbs, best, bidx, group, stream=st)
+    for rep in range(2):
+        best.fill_(-3.0e38)
+        bidx.fill_(-1)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert bidx.cpu().numpy().tolist() == [int(i) for i in np.argmax(logits, axis=1)], rep
+        assert bits_equal(best.cpu().numpy(), logits.max(axis=1)), rep
+    (ab, ai), (nb, ni) = run_both(rng, 2, 4096)[0]
+    assert np.array_equal(ni, ai) and bits_equal(nb, ab)
