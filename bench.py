@@ -496,6 +496,35 @@ def host_cores() -> tuple[int, int]:
     return min(16, nproc), nproc
 
 
+def shuffled_table_run(m, lay, steps: int, stream, ref_ids) -> dict:
+    """The cfg3 workload with the pages in a random order instead of the
+    default reversed table (main_big.cpp:168-171), then the default
+    restored: step, prefill and decode times, and whether the ids match."""
+    import numpy as np
+    import torch
+    from q3ops import LM_ARGMAX
+
+    n = lay.max_seq // 32
+    tab = np.random.default_rng(11).permutation(n).astype(np.uint16)
+    m.set_page_table(tab)
+    m.generate()  # warm: the decode graph is captured anew for the new table
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        m.generate()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    ids = m.ids()[N_PROMPT:N_PROMPT + N_GEN]
+    prefill = time_events(lambda: m.forward_chunk(0, N_PROMPT, LM_ARGMAX, True), steps, stream)
+    m.set_page_table((n - 1 - np.arange(n)).astype(np.uint16))
+    m.generate()
+    torch.cuda.synchronize()
+    return {"table": f"random permutation of the {n} pages (seed 11)", "steps": steps,
+            "ms_per_step": dt * 1e3, "prefill_ms": prefill,
+            "decode_ms_per_token": (dt * 1e3 - prefill) / N_GEN,
+            "same_ids": bool(np.array_equal(np.asarray(ids), np.asarray(ref_ids)))}
+
+
 def cpu_baseline(threads: int, nproc: int, runs: int = 5) -> dict:
     """The CPU oracle (oracle/, the C port of tools/ref_qwen3.py) on the same
     workload: the median of `runs` timed generations on `threads` OpenMP
@@ -733,6 +762,9 @@ def main() -> int:
         "path_roofline": path_roofline(prefill_ms, decode_ms),
         "generated": [int(v) for v in gen_ids],
     }
+    # the same workload over a fragmented page table (every logical page at a
+    # random physical one): the decode prefetch walks the sequence's pages
+    out["shuffled_table"] = shuffled_table_run(m, lay, max(3, args.steps), stream, gen_ids)
     # in-situ kernel timing: one more (untimed) generation with every decode
     # launch bracketed by HIP events on the model's stream
     if not args.no_roofline:

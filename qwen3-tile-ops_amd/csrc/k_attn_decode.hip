@@ -278,12 +278,12 @@ __device__ void fused_compute(const AttnArgs &a, const HotArgs &h, SM &sm, Fused
 // every (nthreads * 16)-byte chunk w, w + pf_wgs, ... of each range.  Four
 // loads are in flight per thread; the values only feed an empty asm
 // statement so that the loads are kept.  With pf_kv_heads, the last four
-// ranges go to the L2s instead (AttnArgs::pf_kv_heads): the workgroup has
-// grid id first + w, on XCD (first + w) % 8, and the XCD's prefetch
-// workgroups split the rows; thread t reads 16 bytes of row t / 16 + 48 k of
-// the slice of the ((t / 8) % nh)-th of the XCD's nh query heads' kv heads
-// (every slice for nh <= 2), one load in flight per thread (measured faster
-// than two: the attention's own loads meet less of this traffic).
+// ranges are the next attention's K/V pools and scale pools instead, read
+// page by page through the page table (AttnArgs::pf_kv_heads): the
+// workgroup has grid id first + w, on XCD (first + w) % 8, and the XCD's
+// prefetch workgroups take whole pages in turn, reading of each the
+// HD-byte slices of the XCD's nh query heads' kv heads (every slice for
+// nh <= 2) in its K and V pool and its scale rows.
 __device__ void prefetch_ranges(const AttnArgs &a, int w, int first) {
   const int nkv = a.pf_kv_heads > 0 ? 4 : 0;
   for (int r = 0; r < a.pf_n - nkv; ++r) {
@@ -303,7 +303,7 @@ __device__ void prefetch_ranges(const AttnArgs &a, int w, int first) {
       asm volatile("" ::"v"(v0.x));
     }
   }
-  if (nkv == 0 || a.pf_n < nkv) return;
+  if (nkv == 0 || a.pf_n < nkv || a.pf_pages <= 0) return;
   const int xcd = (first + w) % 8;
   const int w0 = ((xcd - first) % 8 + 8) % 8;  // first prefetch workgroup on this XCD
   const int nsub = (a.pf_wgs - w0 + 7) / 8;
@@ -311,26 +311,31 @@ __device__ void prefetch_ranges(const AttnArgs &a, int w, int first) {
   const int nh = (a.pf_kv_heads - xcd + 7) / 8;
   const int grp = a.pf_kv_heads / a.kv_heads;
   if (nh <= 0 || grp <= 0) return;
-  const int t = threadIdx.x;
-  const int rpp = static_cast<int>(blockDim.x) / 16;  // rows per pass
-  const int kvh = (xcd + 8 * ((t >> 3) % nh)) / grp;
-  // (32-bit row arithmetic: a span is far below 2^31 bytes, checked on the host)
-  const uint32_t rb = static_cast<uint32_t>(a.row_bytes);
-  for (int r = a.pf_n - nkv; r < a.pf_n - 2; ++r) {
-    const int8_t *base = a.pf[r] + kvh * HD + 16 * (t & 7);
-    const uint32_t rows = static_cast<uint32_t>(a.pf_bytes[r]) / rb;
-    for (uint32_t row = static_cast<uint32_t>(sub * rpp + t / 16); row < rows; row += static_cast<uint32_t>(nsub * rpp)) {
-      const int4 v = *reinterpret_cast<const int4 *>(base + row * rb);
-      asm volatile("" ::"v"(v.x));
+  const int T = static_cast<int>(blockDim.x);
+  const int t = static_cast<int>(threadIdx.x);
+  // whole pages per workgroup (page sub, sub + nsub, ...): the page id is
+  // read once per page; a page's K and V slices (page_tokens rows x nh
+  // slices x 8 chunks of 16 bytes each) and its scale rows spread over the
+  // threads
+  const int per_page = static_cast<int>(a.page_tokens) * nh * 8;
+  const int sp16 = static_cast<int>(a.scale_page_bytes / 16);
+  const int8_t *kp = a.pf[a.pf_n - 4], *vp = a.pf[a.pf_n - 3];
+  const int8_t *ksp = a.pf[a.pf_n - 2], *vsp = a.pf[a.pf_n - 1];
+  for (int page = sub; page < a.pf_pages; page += nsub) {
+    const int64_t phys = a.pf_table[page];
+    for (int i = t; i < per_page; i += T) {
+      const int row = i / (nh * 8), slice = (i >> 3) % nh;
+      const int kvh = (xcd + 8 * slice) / grp;
+      const int64_t off = phys * a.page_bytes + static_cast<int64_t>(row) * a.row_bytes + kvh * HD + 16 * (i & 7);
+      const int4 v0 = *reinterpret_cast<const int4 *>(kp + off);
+      const int4 v1 = *reinterpret_cast<const int4 *>(vp + off);
+      asm volatile("" ::"v"(v0.x), "v"(v1.x));
     }
-  }
-  for (int r = a.pf_n - 2; r < a.pf_n; ++r) {
-    const int8_t *base = a.pf[r];
-    const int64_t n16 = a.pf_bytes[r] / 16;
-    for (int64_t i = static_cast<int64_t>(sub) * blockDim.x + t; i < n16;
-         i += static_cast<int64_t>(nsub) * blockDim.x) {
-      const int4 v0 = reinterpret_cast<const int4 *>(base)[i];
-      asm volatile("" ::"v"(v0.x));
+    for (int i = t; i < sp16; i += T) {
+      const int64_t off = phys * a.scale_page_bytes + 16 * i;
+      const int4 v0 = *reinterpret_cast<const int4 *>(ksp + off);
+      const int4 v1 = *reinterpret_cast<const int4 *>(vsp + off);
+      asm volatile("" ::"v"(v0.x), "v"(v1.x));
     }
   }
 }
@@ -1030,9 +1035,12 @@ bool attn_decode_supported(const AttnArgs &a) {
   for (int r = 0; r < a.pf_n; ++r)
     if ((reinterpret_cast<uintptr_t>(a.pf[r]) & 15) != 0 || a.pf_bytes[r] < 0) return false;
   if (a.row_pos && (a.rows < 1 || a.rows > 65535 || a.fuse_heads || a.pf_n || !a.row_tables)) return false;
-  if (a.pf_kv_heads > 0 && (!a.fuse_heads || a.pf_n < 4 || a.kv_heads <= 0 || a.pf_kv_heads % a.kv_heads != 0 ||
-                            static_cast<int64_t>(a.kv_heads) * HD > a.row_bytes ||
-                            a.pf_bytes[a.pf_n - 4] >= (int64_t{1} << 31) || a.pf_bytes[a.pf_n - 3] >= (int64_t{1} << 31)))
+  if (a.pf_kv_heads > 0 &&
+      (!a.fuse_heads || a.pf_n < 4 || a.kv_heads <= 0 || a.pf_kv_heads % a.kv_heads != 0 ||
+       static_cast<int64_t>(a.kv_heads) * HD > a.row_bytes || !a.pf_table || a.pf_pages < 0 ||
+       a.scale_page_bytes % 16 != 0 ||
+       static_cast<int64_t>(a.page_tokens) * ((a.pf_kv_heads + 7) / 8) * 8 >= (int64_t{1} << 31) ||
+       a.scale_page_bytes / 16 >= (int64_t{1} << 31)))
     return false;
   // O projection fusion: b = 1 with the head epilogues; rows of wo cover
   // every head's 128 columns and are 16-byte aligned

@@ -284,13 +284,17 @@ struct AttnArgs {
   // (else the table is read)
   int blk_page_n;
   // (last, so that the fields above keep their kernel-argument offsets)
-  // fused b = 1 variant only: pf_kv_heads > 0 marks the last four ranges as
-  // the next attention's K pages, V pages, K scales and V scales (K/V rows
-  // row_bytes apart, as in this call), read into the L2 of the XCD that will
-  // read them: query head h's workgroup is workgroup h of the grid's first
-  // row, which the round-robin dispatch puts on XCD h % 8, so the prefetch
-  // workgroups on XCD x read the HD-byte slices of the kv heads of the query
-  // heads h = x (mod 8) (of pf_kv_heads) of every row, and all the scales.
+  // fused b = 1 variant only: pf_kv_heads > 0 marks the last four ranges'
+  // pf[] as the next attention's K pool, V pool, K scale pool and V scale
+  // pool (their pf_bytes unused), whose logical pages 0 .. pf_pages - 1
+  // (page ids from the device table pf_table; page and row strides as in
+  // this call) are read into the L2 of the XCD that will read them: query
+  // head h's workgroup is workgroup h of the grid's first row, which the
+  // round-robin dispatch puts on XCD h % 8, so the prefetch workgroups on
+  // XCD x read the HD-byte slices of the kv heads of the query heads
+  // h = x (mod 8) (of pf_kv_heads) of every row of those pages, and their
+  // scale rows.  Only the sequence's own pages are read, however the table
+  // is fragmented.
   int pf_kv_heads;
   // fused Q|K|V + attention launch only (launch_qkv_attn): the projection's
   // outputs as 64-bit words ((1 << 32) | f32 bits) stored by the GEMV
@@ -301,6 +305,9 @@ struct AttnArgs {
   // up (a lost workgroup: every wave still exits) sets *xerr to 1.
   unsigned long long *xin;
   uint32_t *xerr;
+  // the prefetch's page table and page count (pf_kv_heads)
+  const uint16_t *pf_table;
+  int pf_pages;
 };
 hipError_t launch_attention(const AttnArgs &a, hipStream_t s);
 // the two multi-row kernels behind launch_attention: the phase-parallel one

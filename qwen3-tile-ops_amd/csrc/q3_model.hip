@@ -210,20 +210,6 @@ class KTimer {
   bool active_ = false;
 };
 
-// Physical page span [lo, hi] holding tokens [0, len) under the page table.
-bool kv_page_span(const q3_model *m, uint32_t len, uint32_t *lo, uint32_t *hi) {
-  const uint32_t used = (len + kPageTokens - 1) / kPageTokens;
-  if (used == 0 || used > m->htab.size()) return false;
-  uint32_t a = m->htab[0], b = m->htab[0];
-  for (uint32_t i = 1; i < used; ++i) {
-    a = std::min<uint32_t>(a, m->htab[i]);
-    b = std::max<uint32_t>(b, m->htab[i]);
-  }
-  *lo = a;
-  *hi = b;
-  return true;
-}
-
 void set_paged(q3::QDest &d, const q3_model *m, int8_t *pool, float *spool, uint32_t pos0) {
   const q3_layout &y = m->lay;
   const int64_t KW = static_cast<int64_t>(y.kv_heads) * y.head_dim;
@@ -562,20 +548,17 @@ int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int opti
       // the K/V pages (and scales) the next attention reads: the next
       // layer's, or layer 0's for the next token after the last layer; each
       // kv head's slices go to the L2 of the XCDs whose heads read them
+      // (its own pages through the device table, whatever their order)
       {
         const LayerPtrs nx = layer_ptrs(m, is_last ? 0 : L + 1);
-        const uint32_t span_len = std::min<uint32_t>(pos + rows + (is_last ? 1 : 0), y.max_seq);
-        uint32_t lo = 0, hi = 0;
-        if (kv_page_span(m, span_len, &lo, &hi)) {
-          const int64_t pgb = static_cast<int64_t>(kPageTokens) * KW;
-          const int64_t spb = static_cast<int64_t>(kPageTokens) * y.kv_heads * 4;
-          const int64_t np = hi - lo + 1;
-          add_pf(nx.kc + lo * pgb, np * pgb);
-          add_pf(nx.vc + lo * pgb, np * pgb);
-          add_pf(reinterpret_cast<const int8_t *>(nx.kcs) + lo * spb, np * spb);
-          add_pf(reinterpret_cast<const int8_t *>(nx.vcs) + lo * spb, np * spb);
-          t.pf_kv_heads = static_cast<int>(y.heads);
-        }
+        const uint32_t len = std::min<uint32_t>(pos + rows + (is_last ? 1 : 0), y.max_seq);
+        add_pf(nx.kc, 0);
+        add_pf(nx.vc, 0);
+        add_pf(reinterpret_cast<const int8_t *>(nx.kcs), 0);
+        add_pf(reinterpret_cast<const int8_t *>(nx.vcs), 0);
+        t.pf_table = m->ptab;
+        t.pf_pages = static_cast<int>(std::min<uint32_t>((len + kPageTokens - 1) / kPageTokens, m->n_pages));
+        t.pf_kv_heads = static_cast<int>(y.heads);
       }
       t.pf_wgs = m->pf_wgs;
       if (m->pf_wgs == 0) {
