@@ -38,6 +38,10 @@ LD_TABLE = 8  # pages per sequence table (contexts up to 254 tokens + 2 steps)
 LONG_CTX = [383, 384, 385, 767, 768, 769, 1535, 2046, 2047, 2048]
 LD_TABLE_LONG = 66
 SHAPE = ModelShape(layers=2, vocab=1024, seq=96, max_seq=32768)
+# config 4's own shape (on 2 layers): 64 rows at 2046-2048 keys, 65 pages
+# each, in a pool of 4224 pages (4160 in use) under a random permutation,
+# so that page ids far above 1024 are read
+SHAPE_CFG4 = ModelShape(layers=2, vocab=1024, seq=96, max_seq=4224 * 32)
 INIT = InitConfig(n_prompt=1, n_gen=0, mode=0)
 _cache = {}
 
@@ -61,13 +65,14 @@ def pool_views(lay: Layout, raw: np.ndarray) -> dict[str, np.ndarray]:
     }
 
 
-def make_case(n: int, seed: int, edge: list[int] | None = None, ld_table: int = LD_TABLE):
+def make_case(n: int, seed: int, edge: list[int] | None = None, ld_table: int = LD_TABLE,
+              shape: ModelShape = SHAPE):
     """Blob with n random contexts in disjoint random pages; per-row positions
     and tables; the contexts in dense form for the oracle."""
-    key = (n, seed, tuple(edge or ()), ld_table)
+    key = (n, seed, tuple(edge or ()), ld_table, shape)
     if key in _cache:
         return _cache[key]
-    lay = Layout(SHAPE)
+    lay = Layout(shape)
     blob = init_random_blob(lay, INIT)
     rng = np.random.default_rng(seed)
     # edge contexts first: empty, one short of a page, exactly one page, one over
@@ -113,7 +118,7 @@ def oracle_steps(lay: Layout, blob: np.ndarray, ctx, dense, ids, steps: int):
     """Per sequence: load its context into the oracle cache and run `steps`
     one-row forwards (greedy).  Returns per step: ids, new K/V rows, last-layer
     records."""
-    om = oracle.OracleModel(blob, lay.offsets, dict(SHAPE.__dict__))
+    om = oracle.OracleModel(blob, lay.offsets, dict(lay.shape.__dict__))
     n = len(ctx)
     out = [{"ids": np.zeros(n, np.int32), "rec": [], "kv": []} for _ in range(steps)]
     for r in range(n):
@@ -201,6 +206,21 @@ def test_decode_batch_long_contexts(cuda, n):
     note(f"decode_batch long contexts n={n}")
     run_batch_case(cuda, n, *make_case(n, seed=300 + n, edge=list(LONG_CTX),
                                        ld_table=LD_TABLE_LONG))
+
+
+def test_decode_batch_cfg4_shape(cuda):
+    """BASELINE config 4's batch at its own shape: 64 sequences, every one at
+    2046-2048 keys (65 pages of 32 tokens), their pages drawn from a pool of
+    4224 through a random permutation (ids up to 4223), two greedy steps:
+    ids, every layer's new K/V rows and the last layer's x/o8/os/s8/ss
+    against the oracle run one sequence at a time."""
+    note("decode_batch config 4 shape: 64 x 2046-2048 keys, 4224-page pool")
+    edge = [2046 + r % 3 for r in range(64)]
+    case = make_case(64, seed=404, edge=edge, ld_table=LD_TABLE_LONG, shape=SHAPE_CFG4)
+    lay, blob, ctx, tables, dense, ids = case
+    assert int(tables[tables != 0xFFFF].max()) > 1024
+    run_batch_case(cuda, 64, *case)
+    _cache.pop((64, 404, tuple(edge), LD_TABLE_LONG, SHAPE_CFG4), None)  # 0.6 GB blob
 
 
 def test_decode_batch_rejects_bad_rows(cuda):
