@@ -315,6 +315,20 @@ typedef struct q3_model q3_model;
  * called through the handle allocates afterwards.  stream may be NULL. */
 int q3_model_open(void *blob, const q3_layout *lay, void *stream,
                   q3_model **out);
+/* (When the layout's seq exceeds 64 rows, open also copies every layer's
+ * weights into a second device buffer in the matrix cores' fragment order,
+ * for prefill chunks of more than 64 rows: about the size of the layer
+ * weights, 0.44 GB at the Qwen3-0.6B shape; Q3_PACKED_WEIGHTS=0 at open, or
+ * a failed allocation, keeps every read on the blob.  Decode and chunks of
+ * up to 64 rows always read the blob.  The copy is a snapshot: after writing
+ * new layer weights into the blob, call q3_model_repack before the next
+ * forward.) */
+
+/* Refreshes the packed weight copy from the blob's current layer weights
+ * (a no-op without a copy).  Stream-ordered on the model's stream;
+ * synchronises it.  No counterpart in the reference, whose ops read the
+ * blob only. */
+int q3_model_repack(q3_model *m);
 
 /* Replaces the logical->physical page table (max_seq/32 entries, host
  * array).  Each entry must be < max_seq/32. */

@@ -1063,6 +1063,8 @@ int forward_chunk_impl(q3_model *m, uint32_t pos, uint32_t rows, int lm_out,
 
 // The packed copy of every layer's seven weight matrices (q3::launch_pack_b
 // layout), made once on the model's stream.
+static int repack_weights(q3_model *m);
+
 static int pack_weights(q3_model *m) {
   const q3_layout &y = m->lay;
   const int64_t H = y.hidden, QW = static_cast<int64_t>(y.heads) * y.head_dim;
@@ -1076,9 +1078,21 @@ static int pack_weights(q3_model *m) {
   }
   m->pk_layer = off;
   if (hipMalloc(&m->packed, static_cast<size_t>(off) * y.layers) != hipSuccess) {
+    // no room for the copy: prefill reads the row-major blob instead
+    (void)hipGetLastError();
     m->packed = nullptr;
-    return Q3_ERR_HIP;
+    return Q3_OK;
   }
+  return repack_weights(m);
+}
+
+// The layer weights of the blob into the packed copy (fragment order).
+static int repack_weights(q3_model *m) {
+  const q3_layout &y = m->lay;
+  const int64_t H = y.hidden, QW = static_cast<int64_t>(y.heads) * y.head_dim;
+  const int64_t KW = static_cast<int64_t>(y.kv_heads) * y.head_dim, I = y.inter;
+  const int64_t rows[7] = {QW, KW, KW, H, I, I, H}, cols[7] = {H, H, H, QW, H, H, I};
+  const int64_t off = m->pk_layer;
   for (uint32_t L = 0; L < y.layers; ++L) {
     const int64_t w = static_cast<int64_t>(L) * y.kLAYERW_STRIDE;
     const int64_t src[7] = {y.kLQ, y.kLK, y.kLV, y.kLO, y.kLG, y.kLU, y.kLD};
@@ -1499,6 +1513,12 @@ extern "C" int q3_model_kernel_time(q3_model *m, int kclass, double *total_ms, u
   *total_ms = m->kt_ms[kclass];
   *launches = m->kt_n[kclass];
   return Q3_OK;
+}
+
+extern "C" int q3_model_repack(q3_model *m) {
+  if (!m) return Q3_ERR_ARG;
+  if (!m->packed) return Q3_OK;
+  return repack_weights(m);
 }
 
 extern "C" int q3_model_fused_status(q3_model *m, uint32_t *fused, uint32_t *gave_up) {

@@ -105,6 +105,7 @@ SIGNATURES = {
     "q3_decode_batch": (_I, [_VP, _U, _VP, _VP, _VP, _U, _VP]),
     "q3_model_info": (_I, [_VP, C.POINTER(CLayout), C.POINTER(_VP), C.POINTER(_VP)]),
     "q3_model_fused_status": (_I, [_VP, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]),
+    "q3_model_repack": (_I, [_VP]),
     "q3_sched_create": (_I, [_U, _U, C.POINTER(_VP)]),
     "q3_sched_destroy": (_I, [_VP]),
     "q3_sched_add": (_I, [_VP, _U, _U, _VP]),

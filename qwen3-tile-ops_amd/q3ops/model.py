@@ -89,6 +89,18 @@ class Model:
             out[name] = (ms.value, n.value)
         return out
 
+    def repack(self) -> None:
+        """Refresh the packed weight copy after writing new layer weights
+        into the device blob (q3_model_repack)."""
+        check(lib().q3_model_repack(self.handle), "q3_model_repack")
+
+    def write(self, off: int, data: np.ndarray) -> None:
+        """Host bytes into the device blob at byte offset off, ordered with
+        the model's launches."""
+        a = np.ascontiguousarray(data).view(np.uint8).ravel()
+        with torch.cuda.stream(self.stream):
+            self.blob[off:off + a.size].copy_(torch.from_numpy(a))
+
     def fused_status(self) -> tuple[int, int]:
         """(1 if a decode token's Q|K|V projection shares the attention's
         launch, 1 if one of its bounded waits ever ran out since open);

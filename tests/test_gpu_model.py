@@ -370,6 +370,35 @@ def test_prefill_partial_tiles_and_offset(cuda, monkeypatch, packed, pos, rows):
     assert not probs, probs
 
 
+def test_repack_after_weight_write(cuda):
+    """The packed copy is a snapshot taken at open: after new layer weights
+    are written into the device blob, q3_model_repack refreshes it, and a
+    100-row prefill chunk (packed path) then equals the oracle on the new
+    weights bit for bit, logits and K/V pages."""
+    note("weights rewritten after open + q3_model_repack")
+    lay, blob = host_blob("cfg3_perf", shape=SHAPE_512, init=INIT_512)
+    _, other = host_blob("cfg3_perf", shape=SHAPE_512,
+                         init=InitConfig(weight_seed=0x5EED0100, n_prompt=512, n_gen=4, mode=0))
+    o = lay.offsets
+    w0, w1 = o["kLAYERW_BASE"], o["kLAYERW_BASE"] + lay.layers * o["kLAYERW_STRIDE"]
+    hybrid = blob.copy()
+    hybrid[w0:w1] = other[w0:w1]
+    om = oracle_512(hybrid, lay)
+    ids = lay.global_views(hybrid)["ids"][:100].copy()
+    _, logits = oracle_span(om, ids, 0, 100, record=False)
+    m = Model(lay, blob)
+    m.write(w0, other[w0:w1])
+    m.repack()
+    m.forward_chunk(0, 100, LM_LOGITS, optimize_tail=False)
+    got = m.stage("logits", 1)[0]
+    caches = [m.kv_cache(li, 100) for li in range(lay.layers)]
+    m.close()
+    assert bits_equal(got, logits), describe_diff(got, logits)
+    for li in range(lay.layers):
+        for st, arr in (("kc", om.k8), ("ks", om.k_s), ("vc", om.v8), ("vs", om.v_s)):
+            assert bits_equal(caches[li][st], arr[li, :100]), (li, st)
+
+
 def test_generate_300_token_prompt(cuda):
     """q3_generate with CTRL [300, 4, mode 0]: one 300-row prefill chunk (a
     partial last tile of the stream GEMMs, packed weights) and four greedy
