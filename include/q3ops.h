@@ -368,11 +368,16 @@ int q3_model_close(q3_model *m);
 int q3_model_info(const q3_model *m, q3_layout *lay, void **blob, void **stream);
 
 /* A decode token's Q|K|V projection and attention share one launch
- * (Q3_DECODE_FUSE_QKV at open, default 1): *fused = 1 when enabled.  Their
- * workgroups hand the projection rows over in device memory with a bounded
- * wait; *gave_up = 1 when, since open, a wait ran out (a launch that lost a
- * workgroup: its results are wrong), else 0.  Synchronises the model's
- * stream.  No counterpart in the reference (a single hart). */
+ * (Q3_DECODE_FUSE_QKV at open, default 1): bit 0 of *fused is set when
+ * enabled.  With it, layer L's down projection can run in layer L + 1's
+ * launch (Q3_DECODE_MERGE_DOWN at open, default 0): bit 1.  Their workgroups hand
+ * the projection rows and the new residual row over in device memory with
+ * bounded waits, and the merged launch's GEMV workgroups wait for each
+ * other, so they must all be resident at once (another kernel holding most
+ * CUs of the device meanwhile can starve them); *gave_up = 1 when, since
+ * open, a wait ran out (its launch's results are wrong), else 0.
+ * Synchronises the model's stream.  No counterpart in the reference (a
+ * single hart). */
 int q3_model_fused_status(q3_model *m, uint32_t *fused, uint32_t *gave_up);
 
 /* ------------------------------------------------------------------------ */

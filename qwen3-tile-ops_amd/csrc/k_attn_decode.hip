@@ -353,6 +353,24 @@ __device__ __forceinline__ void xstore(unsigned long long *p, unsigned long long
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// 16 bytes a lane at p + 16 lane + {0, 1, 2, 3} KB with the cache policy of
+// xload (sc1: the agent-coherent level, so that stores from other XCDs are
+// seen), all four in flight, then a wait for them.  Inline assembly: the
+// compiler treats its buffer-load builtins as plain reads and hoists them
+// out of a polling loop.
+typedef unsigned v4u32 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void xload_4k(const uint32_t *p, v4u32 &a, v4u32 &b, v4u32 &c, v4u32 &d) {
+  asm volatile(
+      "global_load_dwordx4 %0, %4, off sc1\n\t"
+      "global_load_dwordx4 %1, %4, off offset:1024 sc1\n\t"
+      "global_load_dwordx4 %2, %4, off offset:2048 sc1\n\t"
+      "global_load_dwordx4 %3, %4, off offset:3072 sc1\n\t"
+      "s_waitcnt vmcnt(0)"
+      : "=&v"(a), "=&v"(b), "=&v"(c), "=&v"(d)
+      : "v"(p + 4 * (threadIdx.x & 63))
+      : "memory");
+}
+
 template <int QPW>
 __device__ __forceinline__ void attn_poll_rows(const AttnArgs &a, int qh0, int wave, int lane, FusedRegs &r) {
   if (wave >= 2 + QPW) return;
@@ -909,15 +927,18 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_kernel(AttnArgs a) {
 constexpr int kFusedWaves = 12;
 constexpr int kFusedR = 2;  // projection rows per GEMV wave
 
-template <int PRO>
-__device__ __forceinline__ void qkv_gemv_role(const GemvArgs &a, const AttnArgs &t, int wg, int N) {
-  __shared__ float blk[32];
-  __shared__ __align__(16) int8_t a_lds[1024];
-  __shared__ float as_lds[4];
-  constexpr int R = kFusedR;
+// A GEMV wave's kFusedR projection rows: their segment, rows within it,
+// scales and 1 KB weight rows (rows past N reload row N - 1, not stored).
+struct QkvRows {
+  int si, row0;
+  int nr[kFusedR];
+  float bsn[kFusedR];
+  int4 w[kFusedR];
+};
+
+__device__ __forceinline__ void qkv_load_rows(const GemvArgs &a, int wg, int N, QkvRows &q) {
   const int lane = threadIdx.x & 63;
   const int wave = wave_id();
-  ProSrc ps = read_src<PRO, false>(a);
   int s_n0[3];
   const int8_t *s_b[3];
   const float *s_bs[3];
@@ -927,60 +948,75 @@ __device__ __forceinline__ void qkv_gemv_role(const GemvArgs &a, const AttnArgs 
     s_b[i] = a.seg[i].b;
     s_bs[i] = a.seg[i].bs;
   }
-  pin_src<PRO, false>(ps);
-  ProRow<1, 0> r0;
-  pro_load_row<PRO, 1, 0, kFusedWaves>(a, ps, 0, r0);
-  __builtin_amdgcn_sched_barrier(0);  // (issue order: prologue operands first)
-  const int row0 = (wg * kFusedWaves + wave) * R;
-  const int si = (row0 >= s_n0[1] ? 1 : 0) + (row0 >= s_n0[2] ? 1 : 0);
-  const int sg_n0 = si == 0 ? s_n0[0] : si == 1 ? s_n0[1] : s_n0[2];
-  const int8_t *const sg_b = si == 0 ? s_b[0] : si == 1 ? s_b[1] : s_b[2];
-  const float *const sg_bs = si == 0 ? s_bs[0] : si == 1 ? s_bs[1] : s_bs[2];
-  // the rows' scales and weights (rows past N reload row N - 1, unused)
-  int nr[R];
-  float bsn[R];
-  int4 w[R];
+  q.row0 = (wg * kFusedWaves + wave) * kFusedR;
+  q.si = (q.row0 >= s_n0[1] ? 1 : 0) + (q.row0 >= s_n0[2] ? 1 : 0);
+  const int sg_n0 = q.si == 0 ? s_n0[0] : q.si == 1 ? s_n0[1] : s_n0[2];
+  const int8_t *const sg_b = q.si == 0 ? s_b[0] : q.si == 1 ? s_b[1] : s_b[2];
+  const float *const sg_bs = q.si == 0 ? s_bs[0] : q.si == 1 ? s_bs[1] : s_bs[2];
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    nr[r] = min(row0 + r, N - 1) - sg_n0;
-    bsn[r] = sg_bs[nr[r]];
-    w[r] = *reinterpret_cast<const int4 *>(sg_b + static_cast<int64_t>(nr[r]) * 1024 + 16 * lane);
+  for (int r = 0; r < kFusedR; ++r) {
+    q.nr[r] = min(q.row0 + r, N - 1) - sg_n0;
+    q.bsn[r] = sg_bs[q.nr[r]];
+    q.w[r] = *reinterpret_cast<const int4 *>(sg_b + static_cast<int64_t>(q.nr[r]) * 1024 + 16 * lane);
   }
-  __builtin_amdgcn_sched_barrier(0);
-  pro_compute_row<PRO, 1, 0, kFusedWaves>(a, 0, r0, a_lds, as_lds, blk, wg == 0);  // ends with a barrier
-  const GemvSeg &sg = a.seg[si];
+}
+
+// The rows' dot products with the int8 A row in LDS (the whole-row GEMV's
+// arithmetic), stored as f32 and as exchange words for the attention
+// workgroups: Q once, K and V once per query head of their KV head.
+__device__ __forceinline__ void qkv_store_rows(const GemvArgs &a, const AttnArgs &t, const QkvRows &q,
+                                               const int8_t *a_lds, const float *as_lds, int N) {
+  const int lane = threadIdx.x & 63;
+  const GemvSeg &sg = a.seg[q.si];
   const int4 av = *reinterpret_cast<const int4 *>(a_lds + 16 * lane);
   const float asg = as_lds[lane >> 4];
   const int grp = t.heads / t.kv_heads;
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    int acc = sdot4(w[r].x, av.x, 0);
-    acc = sdot4(w[r].y, av.y, acc);
-    acc = sdot4(w[r].z, av.z, acc);
-    acc = sdot4(w[r].w, av.w, acc);
+  for (int r = 0; r < kFusedR; ++r) {
+    int acc = sdot4(q.w[r].x, av.x, 0);
+    acc = sdot4(q.w[r].y, av.y, acc);
+    acc = sdot4(q.w[r].z, av.z, acc);
+    acc = sdot4(q.w[r].w, av.w, acc);
     acc += lane_xor<1>(acc);
     acc += lane_xor<2>(acc);
     acc += lane_xor<4>(acc);
     acc += lane_xor<8>(acc);
     // p_g = RN(RN(f32(I_g) * bs[n]) * as_g), summed in group order from +0
-    const float p = __fmul_rn(__fmul_rn(static_cast<float>(acc), bsn[r]), asg);
+    const float p = __fmul_rn(__fmul_rn(static_cast<float>(acc), q.bsn[r]), asg);
     float out = 0.0f;
     out = __fadd_rn(out, lane_bcast<0>(p));
     out = __fadd_rn(out, lane_bcast<16>(p));
     out = __fadd_rn(out, lane_bcast<32>(p));
     out = __fadd_rn(out, lane_bcast<48>(p));
-    if (lane == 0 && row0 + r < N) {
-      sg.out[nr[r]] = out;
+    if (lane == 0 && q.row0 + r < N) {
+      sg.out[q.nr[r]] = out;
       const unsigned long long word = (1ull << 32) | __float_as_uint(out);
-      if (si == 0) {
-        xstore(t.xin + nr[r], word);
+      if (q.si == 0) {
+        xstore(t.xin + q.nr[r], word);
       } else {
-        const int kvh = nr[r] / HD, d = nr[r] % HD;
+        const int kvh = q.nr[r] / HD, d = q.nr[r] % HD;
         for (int c = 0; c < grp; ++c)
-          xstore(t.xin + (static_cast<int64_t>(si) * t.heads + kvh * grp + c) * HD + d, word);
+          xstore(t.xin + (static_cast<int64_t>(q.si) * t.heads + kvh * grp + c) * HD + d, word);
       }
     }
   }
+}
+
+template <int PRO>
+__device__ __forceinline__ void qkv_gemv_role(const GemvArgs &a, const AttnArgs &t, int wg, int N) {
+  __shared__ float blk[32];
+  __shared__ __align__(16) int8_t a_lds[1024];
+  __shared__ float as_lds[4];
+  ProSrc ps = read_src<PRO, false>(a);
+  pin_src<PRO, false>(ps);
+  ProRow<1, 0> r0;
+  pro_load_row<PRO, 1, 0, kFusedWaves>(a, ps, 0, r0);
+  __builtin_amdgcn_sched_barrier(0);  // (issue order: prologue operands first)
+  QkvRows q;
+  qkv_load_rows(a, wg, N, q);
+  __builtin_amdgcn_sched_barrier(0);
+  pro_compute_row<PRO, 1, 0, kFusedWaves>(a, 0, r0, a_lds, as_lds, blk, wg == 0);  // ends with a barrier
+  qkv_store_rows(a, t, q, a_lds, as_lds, N);
 }
 
 template <int PRO>
@@ -990,6 +1026,138 @@ __global__ void __launch_bounds__(kFusedWaves * 64) qkv_attn_kernel(GemvArgs g, 
     attn_decode_body<1, kFusedWaves, 2, true, true, true>(a, bx, 0);
   } else if (bx < a.heads + gemv_wgs) {
     qkv_gemv_role<PRO>(g, a, bx - a.heads, g.seg[2].n1);
+  } else {
+    const int w = bx - a.heads - gemv_wgs;
+    if (w < a.pf_wgs) prefetch_ranges(a, w, a.heads + gemv_wgs);
+  }
+}
+
+// ---- the previous layer's down projection in the same launch ------------
+// The G GEMV workgroups first finish the previous layer's MLP: waves 0..5
+// of workgroup wg own down column n = wave * G + wg (n < N_down): the SwiGLU
+// row quantised per 256 (d's PRO_QUANT prologue, K = 3072), its dot with
+// the 3 KB weight row, then x[n] = (x[n] + O) + down with the O partials
+// summed in head order, as the whole-row GEMV's EPI_ADD epilogue computes
+// it.  Each column goes to x and, as f32 bits, to each copy of
+// AttnArgs::xw.  After the workgroup's own stores, the last wave waits for
+// all 1024 words of copy wg % kXwCopies (4 KB a round, 16 bytes a lane and
+// load, all in flight before any check), puts the row into LDS and the
+// workgroup continues as qkv_gemv_role with the new x.  kXwEmpty marks a
+// word not yet stored: a NaN with every payload bit set, which the down
+// epilogue produces only from such a NaN among its inputs (then the wait
+// runs out and reports it).  Every GEMV workgroup waits for every other
+// one, so all of them must be resident together (G + heads workgroups of
+// one per CU: the launch checks G + heads <= CUs); the wait is bounded like
+// the attention's.  The Q|K|V weights and the down operands are all
+// requested before the first wait.
+__device__ __forceinline__ void down_qkv_role(const GemvArgs &d, const GemvArgs &a, const AttnArgs &t, int wg,
+                                              int G) {
+  __shared__ float blk[32];
+  __shared__ __align__(16) int8_t a_lds[3072];
+  __shared__ float as_lds[12];
+  __shared__ __align__(16) float x_lds[1024];
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_id();
+  const int N = a.seg[2].n1;
+  const int Nd = d.seg[0].n1;
+  ProSrc dps = read_src<PRO_QUANT, true>(d);
+  const int8_t *db = d.seg[0].b;
+  const float *dbs = d.seg[0].bs;
+  float *dx = d.seg[0].out;
+  const float *gain = a.w_pre;
+  pin_src<PRO_QUANT, true>(dps);
+  // the SwiGLU row (waves w and w + 4, w + 8 load group set w & 3)
+  ProRow<3, 0> rd;
+  pro_load_row<PRO_QUANT, 3, 0, kFusedWaves>(d, dps, 0, rd);
+  __builtin_amdgcn_sched_barrier(0);
+  // this wave's down column: weights, scale, residual, O partials
+  const int n = wave * G + wg;
+  const bool down = n < Nd;
+  const int nc = min(n, Nd - 1);
+  int4 dw[3];
+#pragma unroll
+  for (int j = 0; j < 3; ++j) dw[j] = make_int4(0, 0, 0, 0);
+  float dbsn = 0.0f, xn = 0.0f, pv = 0.0f;
+  if (down) {
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+      dw[j] = *reinterpret_cast<const int4 *>(db + static_cast<int64_t>(nc) * 3072 + 1024 * j + 16 * lane);
+    dbsn = dbs[nc];
+    xn = dx[nc];
+    pv = dps.part[min(lane & 15, dps.npart - 1) * dps.ld_part + nc];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // the Q|K|V rows and the n1 gains of this wave's RMSNorm group
+  QkvRows q;
+  qkv_load_rows(a, wg, N, q);
+  ProRow<1, 0> r0;
+  r0.w[0] = *reinterpret_cast<const float4 *>(gain + (wave & 3) * 256 + 4 * lane);
+  __builtin_amdgcn_sched_barrier(0);
+  pro_compute_row<PRO_QUANT, 3, 0, kFusedWaves>(d, 0, rd, a_lds, as_lds, blk, wg == 0);  // ends with a barrier
+  if (down) {
+    float out = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int4 av = *reinterpret_cast<const int4 *>(a_lds + 1024 * j + 16 * lane);
+      const float asg = as_lds[4 * j + (lane >> 4)];
+      int acc = sdot4(dw[j].x, av.x, 0);
+      acc = sdot4(dw[j].y, av.y, acc);
+      acc = sdot4(dw[j].z, av.z, acc);
+      acc = sdot4(dw[j].w, av.w, acc);
+      acc += lane_xor<1>(acc);
+      acc += lane_xor<2>(acc);
+      acc += lane_xor<4>(acc);
+      acc += lane_xor<8>(acc);
+      const float p = __fmul_rn(__fmul_rn(static_cast<float>(acc), dbsn), asg);
+      out = __fadd_rn(out, lane_bcast<0>(p));
+      out = __fadd_rn(out, lane_bcast<16>(p));
+      out = __fadd_rn(out, lane_bcast<32>(p));
+      out = __fadd_rn(out, lane_bcast<48>(p));
+    }
+    float o = 0.0f;  // the O projection, partials in head order
+#pragma unroll
+    for (int h = 0; h < kMaxPart; ++h)
+      if (h < dps.npart) o = __fadd_rn(o, __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(pv), h)));
+    const float v = __fadd_rn(__fadd_rn(xn, o), out);
+    if (lane == 0) dx[n] = v;
+    if (lane < kXwCopies)
+      __hip_atomic_store(t.xw + lane * kXwStride + n, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  lds_barrier();  // (the first round of polls after the workgroup's own stores)
+  if (wave == kFusedWaves - 1) {
+    // columns 256 i + 4 lane .. + 3 are v[i]
+    v4u32 v[4];
+    for (int it = 0;; ++it) {
+      xload_4k(t.xw + (wg % kXwCopies) * kXwStride, v[0], v[1], v[2], v[3]);
+      bool ok = true;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        ok = ok && v[i].x != kXwEmpty && v[i].y != kXwEmpty && v[i].z != kXwEmpty && v[i].w != kXwEmpty;
+      if (__all(ok)) break;
+      if (it == kPollLimit) {
+        if (lane == 0) __hip_atomic_store(t.xerr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<v4u32 *>(x_lds + 256 * i + 4 * lane) = v[i];
+  }
+  lds_barrier();
+  if (wave < 4) r0.x[0] = *reinterpret_cast<const float4 *>(x_lds + wave * 256 + 4 * lane);
+  // (the A row of the projection reuses a_lds: every wave read its down
+  // operand before the prologue's first barrier)
+  pro_compute_row<PRO_NORM, 1, 0, kFusedWaves>(a, 0, r0, a_lds, as_lds, blk, wg == 0);  // ends with a barrier
+  qkv_store_rows(a, t, q, a_lds, as_lds, N);
+}
+
+__global__ void __launch_bounds__(kFusedWaves * 64) down_qkv_attn_kernel(GemvArgs d, GemvArgs g, AttnArgs a,
+                                                                          int gemv_wgs) {
+  const int bx = static_cast<int>(blockIdx.x);
+  if (bx < a.heads) {
+    attn_decode_body<1, kFusedWaves, 2, true, true, true>(a, bx, 0);
+  } else if (bx < a.heads + gemv_wgs) {
+    down_qkv_role(d, g, a, bx - a.heads, gemv_wgs);
   } else {
     const int w = bx - a.heads - gemv_wgs;
     if (w < a.pf_wgs) prefetch_ranges(a, w, a.heads + gemv_wgs);
@@ -1055,6 +1223,13 @@ bool attn_decode_supported(const AttnArgs &a) {
          (!a.row_pos || (a.ldq % 16) == 0);
 }
 
+namespace {
+// the GEMV workgroups of the fused launches: kFusedR rows per wave
+int qkv_gemv_wgs(const GemvArgs &g) {
+  return (g.seg[2].n1 + kFusedWaves * kFusedR - 1) / (kFusedWaves * kFusedR);
+}
+}  // namespace
+
 bool qkv_attn_supported(const GemvArgs &g, const AttnArgs &a) {
   if (g.M != 1 || g.K != 1024 || g.group != 256 || g.bs_ld || g.part || g.nseg != 3) return false;
   if (g.pro != PRO_NORM && g.pro != PRO_EMBED) return false;
@@ -1072,14 +1247,43 @@ bool qkv_attn_supported(const GemvArgs &g, const AttnArgs &a) {
 }
 
 hipError_t launch_qkv_attn(const GemvArgs &g, const AttnArgs &a, hipStream_t s) {
-  const int N = g.seg[2].n1;
-  const int gw = (N + kFusedWaves * kFusedR - 1) / (kFusedWaves * kFusedR);
+  const int gw = qkv_gemv_wgs(g);
   const int extra = a.pf_n > 0 ? a.pf_wgs : 0;
   const dim3 grid(a.heads + gw + extra);
   if (g.pro == PRO_EMBED)
     Q3_LAUNCH((qkv_attn_kernel<PRO_EMBED>), grid, dim3(kFusedWaves * 64), 0, s, g, a, gw);
   else
     Q3_LAUNCH((qkv_attn_kernel<PRO_NORM>), grid, dim3(kFusedWaves * 64), 0, s, g, a, gw);
+  return hipGetLastError();
+}
+
+bool down_qkv_attn_supported(const GemvArgs &d, const GemvArgs &g, const AttnArgs &a) {
+  if (g.pro != PRO_NORM || !a.xw || !qkv_attn_supported(g, a)) return false;
+  auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  const GemvSeg &s0 = d.seg[0];
+  if (d.M != 1 || d.K != 3072 || d.group != 256 || d.bs_ld || d.pro != PRO_QUANT || d.nseg != 1 ||
+      s0.epi != EPI_ADD || s0.n0 != 0 || !s0.b || !s0.bs || !s0.out)
+    return false;
+  // the down output is the row g normalises (K = 1024 = four 256-column
+  // groups, one per polling wave), its partials are not the ones this
+  // launch's attention writes
+  if (s0.n1 != g.K || s0.out != g.x || !d.x || !al16(d.x) || !al16(g.w_pre) || !d.part || d.npart < 1 ||
+      d.npart > kMaxPart || d.ld_part < s0.n1 || d.part == a.opart)
+    return false;
+  // every down column has a wave, and every GEMV workgroup is resident with
+  // the attention's (one 12-wave workgroup per CU)
+  const int gw = qkv_gemv_wgs(g);
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return false;
+  return static_cast<int64_t>(gw) * kFusedWaves >= s0.n1 && a.heads + gw <= cus;
+}
+
+hipError_t launch_down_qkv_attn(const GemvArgs &d, const GemvArgs &g, const AttnArgs &a, hipStream_t s) {
+  const int gw = qkv_gemv_wgs(g);
+  const int extra = a.pf_n > 0 ? a.pf_wgs : 0;
+  Q3_LAUNCH(down_qkv_attn_kernel, dim3(a.heads + gw + extra), dim3(kFusedWaves * 64), 0, s, d, g, a, gw);
   return hipGetLastError();
 }
 

@@ -45,9 +45,9 @@ __device__ __forceinline__ v4i zero4() {
   return z;
 }
 
-// The O projection partials (GemvArgs::part, M = 1): PART = kPartPro adds
-// them in the PRO_NORM prologue, PART = kPartEpi in the EPI_ADD epilogue.
-constexpr int kMaxPart = 16;
+// The O projection partials (GemvArgs::part, M = 1, at most kMaxPart):
+// PART = kPartPro adds them in the PRO_NORM prologue, PART = kPartEpi in the
+// EPI_ADD epilogue.
 constexpr int kPartPro = 1, kPartEpi = 2;
 // BSG: per-(row, K-group) B scales seg[0].bs[n * bs_ld + g], loaded with
 // the other scales before the weight stream (PRO_NONE, one matrix).
@@ -764,6 +764,10 @@ __global__ void __launch_bounds__(256) gemv_wr_kernel(GemvArgs a, int N) {
     }
     if (lane == 0 && row0 + r < N) *dst = v;
   }
+  if (a.clear) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < a.nclear) a.clear[i] = kXwEmpty;
+  }
 }
 
 // Per (row, head) wave: the head epilogues of the Q/K/V projections
@@ -960,35 +964,44 @@ hipError_t launch_wr(const GemvArgs &a, int ncols, hipStream_t s) {
   return hipGetLastError();
 }
 
-bool wr_launch(const GemvArgs &a, int ncols, hipStream_t s, hipError_t *err) {
-  if (a.M != 1 || a.group != 256 || a.bs_ld || a.pro == PRO_NONE) return false;
+// R for the whole-row kernel, or 0 where it does not apply
+int wr_rows(const GemvArgs &a, int ncols) {
+  if (a.M != 1 || a.group != 256 || a.bs_ld || a.pro == PRO_NONE) return 0;
   const int epi = a.seg[0].epi;
   const bool two = epi == EPI_SWIGLU;
   int R;
   if (two) {
-    if (a.K != 1024 || a.pro != PRO_NORM || a.nseg != 1) return false;
+    if (a.K != 1024 || a.pro != PRO_NORM || a.nseg != 1) return 0;
     R = 3;
   } else if (a.K == 3072) {
-    if (a.pro != PRO_QUANT || a.nseg != 1 || epi != EPI_ADD) return false;
+    if (a.pro != PRO_QUANT || a.nseg != 1 || epi != EPI_ADD) return 0;
     R = 1;
   } else if (a.K == 1024) {
-    if (a.pro != PRO_NORM && a.pro != PRO_EMBED) return false;
+    if (a.pro != PRO_NORM && a.pro != PRO_EMBED) return 0;
     R = 2;  // Q|K|V: 512 workgroups (0.7138 -> 0.7108 ms/token against 4 columns per wave)
   } else {
-    return false;
+    return 0;
   }
-  if (ncols % (4 * R)) return false;
+  if (ncols % (4 * R)) return 0;
+  if (a.clear && (a.nclear < 0 || static_cast<int64_t>(a.nclear) > static_cast<int64_t>(ncols / (4 * R)) * 256))
+    return 0;
   for (int i = 0; i < a.nseg; ++i) {
     const int e = a.seg[i].epi;
     if (a.seg[i].n0 % (4 * R) || (two != (e == EPI_SWIGLU)) || (e != EPI_STORE && e != EPI_ADD && e != EPI_SWIGLU))
-      return false;
+      return 0;
   }
   if (a.part) {  // O partials: gate/up's prologue or down's epilogue, as dispatch_part takes them
     const bool pro = a.pro == PRO_NORM;
     if (a.npart < 1 || a.npart > kMaxPart || a.nseg != 1 || pro != two || (!pro && epi != EPI_ADD) ||
         a.ld_part < (pro ? a.K : ncols) || (reinterpret_cast<uintptr_t>(a.part) & 15) != 0 || (a.ld_part % 4) != 0)
-      return false;
+      return 0;
   }
+  return R;
+}
+
+bool wr_launch(const GemvArgs &a, int ncols, hipStream_t s, hipError_t *err) {
+  if (!wr_rows(a, ncols)) return false;
+  const bool two = a.seg[0].epi == EPI_SWIGLU;
   const bool part = a.part != nullptr;
   if (two)
     *err = part ? launch_wr<PRO_NORM, 1, 2, 3, kMaxPart, 0>(a, ncols, s) : launch_wr<PRO_NORM, 1, 2, 3, 0, 0>(a, ncols, s);
@@ -1050,6 +1063,10 @@ bool gemv_group_bscale_supported(const GemvArgs &a) {
                                       : gemv_rows_supported(a.M, a.K, a.group, ncols_of(a)));
 }
 
+bool gemv_clear_supported(const GemvArgs &a) {
+  return a.M == 1 && a.pro != PRO_NONE && a.K % 1024 == 0 && !use_stream(a) && wr_rows(a, ncols_of(a)) > 0;
+}
+
 int gemv_argmax_slots(const GemvArgs &a) {
   const int ncols = ncols_of(a);
   if (use_stream(a)) return stream_grid(ncols / 64);
@@ -1058,6 +1075,7 @@ int gemv_argmax_slots(const GemvArgs &a) {
 
 hipError_t launch_gemv(const GemvArgs &a, hipStream_t s) {
   if (a.M <= 0) return hipSuccess;
+  if (a.clear && !gemv_clear_supported(a)) return hipErrorInvalidValue;
   if (a.bs_ld && !gemv_group_bscale_supported(a)) return hipErrorInvalidValue;
   if (a.pro != PRO_NONE && (a.K % 1024 != 0 || a.M > 16)) return hipErrorInvalidValue;
   const int ncols = ncols_of(a);

@@ -13,6 +13,9 @@
 namespace q3 {
 namespace {
 
+// the most O projection partials (query heads) a decode GEMV adds
+constexpr int kMaxPart = 16;
+
 // The prologue builds the int8 A operand of M rows (K = 1024*QW columns,
 // 256-column groups) in LDS.  Thread layout: wave w owns groups w, w+4, ...
 // (QW of them); lane l owns columns 4l..4l+3 of a group, so a 32-column

@@ -216,6 +216,15 @@ struct GateUpArgs {
 hipError_t launch_gate_up(const GateUpArgs &a, hipStream_t s);
 
 // ---- paged GQA attention -------------------------------------------------
+// the merged launch's x exchange words (AttnArgs::xw): kXwCopies copies of
+// the row, kXwStride words apart, each read by 1 / kXwCopies of the
+// pollers (one copy's lines read by all of them are served one request at
+// a time); kXwEmpty marks a word not yet stored
+constexpr uint32_t kXwEmpty = 0xFFFFFFFFu;
+constexpr int kXwCopies = 8;
+constexpr int kXwStride = 1024 + 64;
+constexpr int kXwWords = kXwCopies * kXwStride;
+
 struct AttnArgs {
   int rows, heads, kv_heads;  // head_dim is 128
   uint32_t kv_len;
@@ -308,6 +317,13 @@ struct AttnArgs {
   // the prefetch's page table and page count (pf_kv_heads)
   const uint16_t *pf_table;
   int pf_pages;
+  // merged launch (launch_down_qkv_attn): the residual row after the
+  // previous layer's down projection as f32 bits (kXwWords: kXwCopies
+  // copies), stored by the workgroup that computed each column and read by
+  // all projection workgroups; 0xFFFFFFFF (kXwEmpty, a NaN no arithmetic
+  // here produces from other inputs) before the launch, set by the launch
+  // that follows (GemvArgs::clear)
+  uint32_t *xw;
 };
 hipError_t launch_attention(const AttnArgs &a, hipStream_t s);
 // the two multi-row kernels behind launch_attention: the phase-parallel one
@@ -385,8 +401,15 @@ struct GemvArgs {
   // per-(row, K-group) B scales of segment 0 (PRO_NONE, EPI_STORE / EPI_ADD,
   // one segment): seg[0].bs[n * bs_ld + g]; 0: per-row scales
   int64_t bs_ld;
+  // M = 1 whole-row launches: thread i of the grid writes kXwEmpty to
+  // clear[i], i < nclear (the decode launch after a merged down + Q|K|V +
+  // attention launch empties its x exchange words, which have many readers)
+  uint32_t *clear;
+  int nclear;
 };
 bool gemv_supported(int M, int K, int group);
+// launch_gemv accepts GemvArgs::clear for a (the whole-row kernel runs it)
+bool gemv_clear_supported(const GemvArgs &a);
 // 17-64 rows (also 1-16): plain A operand, no partials, fewer than 65536 columns
 bool gemv_rows_supported(int M, int K, int group, int ncols);
 // whether launch_gemv takes per-(row, K-group) B scales for this launch
@@ -427,6 +450,15 @@ hipError_t launch_attn_decode(const AttnArgs &a, hipStream_t s);
 // their head's Q/K/V from a.xin.  g still writes its f32 outputs.
 bool qkv_attn_supported(const GemvArgs &g, const AttnArgs &a);
 hipError_t launch_qkv_attn(const GemvArgs &g, const AttnArgs &a, hipStream_t s);
+// launch_qkv_attn with the previous layer's down projection in the same
+// launch: d is that GEMV (M = 1, K = inter, group 256, PRO_QUANT of the
+// SwiGLU row, one EPI_ADD segment into x with the O partials, d.part, in
+// its epilogue, N = hidden), g's PRO_NORM reads the new x from a.xw.  The
+// GEMV workgroups compute d's columns, store them to x and a.xw, wait for
+// all of a.xw, then compute g; a.opart must not be d.part (the attention of
+// this launch writes it while d reads the previous layer's).
+bool down_qkv_attn_supported(const GemvArgs &d, const GemvArgs &g, const AttnArgs &a);
+hipError_t launch_down_qkv_attn(const GemvArgs &d, const GemvArgs &g, const AttnArgs &a, hipStream_t s);
 
 // ---- greedy pick over a logits row (main_big.cpp:300-322) ---------------
 hipError_t launch_argmax_logits(const float *logits, int vocab,

@@ -52,8 +52,10 @@ struct q3_model {
   unsigned long long *bkeys = nullptr;  // [seq][bkeys_ld]
   int64_t bkeys_ld = 0;
   float *bbest = nullptr;          // [seq] per-row argmax value
-  // decode (b = 1): the O projection's per-head partials [heads][hidden],
-  // written by the attention kernel, summed by the gate/up and down GEMVs
+  // decode (b = 1): the O projection's per-head partials [2][heads][hidden],
+  // written by the attention kernel, summed by the gate/up and down GEMVs;
+  // layer L uses half L & 1 (its down projection can run in layer L + 1's
+  // launch, whose attention writes the other half)
   float *opart = nullptr;
   // decode (b = 1): the Q|K|V projection in the attention's launch
   // (Q3_DECODE_FUSE_QKV, default 1), its exchange words and give-up flag
@@ -61,6 +63,14 @@ struct q3_model {
   bool qkvfuse = true;
   unsigned long long *xin = nullptr;
   uint32_t *xerr = nullptr;
+  // decode (b = 1): layer L's down projection in layer L + 1's Q|K|V +
+  // attention launch (Q3_DECODE_MERGE_DOWN, default 0: the in-launch
+  // exchange of the new residual row costs about what the kernel boundary
+  // does, 0.6456 against 0.6455 ms/token), its new residual row as exchange
+  // words (AttnArgs::xw, kXwWords), cleared by the gate/up launch of every
+  // b = 1 layer while enabled
+  bool merge = false;
+  uint32_t *xw = nullptr;
   // event timing of decode kernel classes (q3_model_set_kernel_timing)
   uint32_t kt_mask = 0;
   std::vector<hipEvent_t> kt_ev[Q3_KT_COUNT];  // start, end pairs
@@ -411,9 +421,13 @@ int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int opti
   const float inv_hd = 1.0f / static_cast<float>(HD);
   const float qk_scale = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(HD)));
 
+  // layer L - 1's down projection when layer L's launch is to run it
+  q3::GemvArgs pend;
+  bool have_pend = false;
   for (uint32_t L = 0; L < y.layers; ++L) {
     const LayerPtrs lp = layer_ptrs(m, L);
     const bool is_last = (L + 1 == y.layers);
+    float *op = m->opart + static_cast<int64_t>(L & 1) * y.heads * H;
     const bool do_tail = !is_last || lm_out != Q3_LM_NONE;
     const bool tail_last_row = optimize_tail && is_last;
     const uint32_t tr0 = tail_last_row ? rows - 1 : 0;
@@ -495,7 +509,7 @@ int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int opti
       to.wos = lp.wos;
       to.ldwo = QW;
       to.o_rows = H;
-      to.opart = m->opart;
+      to.opart = op;
       to.ld_opart = H;
       ofuse = m->ofuse && q3::attn_decode_supported(to);
     }
@@ -511,7 +525,7 @@ int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int opti
         t.wos = lp.wos;
         t.ldwo = QW;
         t.o_rows = H;
-        t.opart = m->opart;
+        t.opart = op;
         t.ld_opart = H;
       }
       t.fuse_heads = 1;
@@ -573,6 +587,50 @@ int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int opti
       qkvfuse = q3::qkv_attn_supported(gq, t);
       if (!qkvfuse) t.xin = nullptr, t.xerr = nullptr;
     }
+    // gate/up + SwiGLU; prologue = RMSNorm n2 + quant (launched below); with
+    // the down projection merged into the next launch it also clears the
+    // exchange words of x
+    q3::GemvArgs gu = gemv_args(M, H, 256);
+    {
+      q3::GemvArgs &g = gu;
+      g.pro = q3::PRO_NORM;
+      g.x = x + static_cast<int64_t>(tr0) * H;
+      g.ldx = H;
+      g.w_pre = lp.n2;
+      g.inv_pre = inv_h;
+      g.h_out = h + static_cast<int64_t>(tr0) * H;
+      g.h8_out = h8 + static_cast<int64_t>(tr0) * H;
+      g.hs_out = hs + static_cast<int64_t>(tr0) * (H / 256);
+      g.nseg = 1;
+      g.seg[0] = gemv_seg(0, I, q3::EPI_SWIGLU, lp.wg, lp.wgs, sw + static_cast<int64_t>(tr0) * I, I);
+      g.seg[0].b2 = lp.wu;
+      g.seg[0].bs2 = lp.wus;
+      if (ofuse) {  // normalises x + O
+        g.part = op;
+        g.npart = static_cast<int>(y.heads);
+        g.ld_part = H;
+      }
+      if (m->merge && rows == 1) {
+        g.clear = m->xw;
+        g.nclear = q3::kXwWords;
+        if (!q3::gemv_clear_supported(g)) g.clear = nullptr, g.nclear = 0;
+      }
+    }
+    // layer L - 1's down projection: in this launch when it can take it
+    // (the gate/up launch after it clears x's words), else on its own first
+    bool merged = false;
+    if (have_pend) {
+      if (qkvfuse && gu.clear) {
+        t.xw = m->xw;
+        merged = q3::down_qkv_attn_supported(pend, gq, t);
+        if (!merged) t.xw = nullptr;
+      }
+      if (!merged) {
+        KTimer kt(m, Q3_KT_GEMV_DOWN);
+        Q3_HIP(q3::launch_gemv(pend, s));
+      }
+      have_pend = false;
+    }
     if (!qkvfuse) {
       KTimer kt(m, Q3_KT_GEMV_QKV);
       Q3_HIP(q3::launch_gemv(gq, s));
@@ -622,7 +680,10 @@ int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int opti
       }
     }
     if (!do_tail) continue;
-    if (qkvfuse) {
+    if (merged) {
+      KTimer kt(m, Q3_KT_ATTN_DECODE);
+      Q3_HIP(q3::launch_down_qkv_attn(pend, gq, t, s));
+    } else if (qkvfuse) {
       KTimer kt(m, Q3_KT_ATTN_DECODE);
       Q3_HIP(q3::launch_qkv_attn(gq, t, s));
     } else if (q3::attn_decode_supported(t)) {
@@ -645,28 +706,9 @@ int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int opti
       KTimer kt(m, Q3_KT_GEMV_O);
       Q3_HIP(q3::launch_gemv(g, s));
     }
-    // gate/up + SwiGLU; prologue = RMSNorm n2 + quant
     {
-      q3::GemvArgs g = gemv_args(M, H, 256);
-      g.pro = q3::PRO_NORM;
-      g.x = xt;
-      g.ldx = H;
-      g.w_pre = lp.n2;
-      g.inv_pre = inv_h;
-      g.h_out = h + static_cast<int64_t>(tr0) * H;
-      g.h8_out = h8 + static_cast<int64_t>(tr0) * H;
-      g.hs_out = hs + static_cast<int64_t>(tr0) * (H / 256);
-      g.nseg = 1;
-      g.seg[0] = gemv_seg(0, I, q3::EPI_SWIGLU, lp.wg, lp.wgs, sw + static_cast<int64_t>(tr0) * I, I);
-      g.seg[0].b2 = lp.wu;
-      g.seg[0].bs2 = lp.wus;
-      if (ofuse) {  // normalises x + O
-        g.part = m->opart;
-        g.npart = static_cast<int>(y.heads);
-        g.ld_part = H;
-      }
       KTimer kt(m, Q3_KT_GEMV_GATE_UP);
-      Q3_HIP(q3::launch_gemv(g, s));
+      Q3_HIP(q3::launch_gemv(gu, s));
     }
     // down projection + residual; prologue = per-256 quant of SwiGLU
     {
@@ -679,13 +721,22 @@ int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int opti
       g.nseg = 1;
       g.seg[0] = gemv_seg(0, H, q3::EPI_ADD, lp.wd, lp.wds, xt, H);
       if (ofuse) {  // x = (x + O) + down
-        g.part = m->opart;
+        g.part = op;
         g.npart = static_cast<int>(y.heads);
         g.ld_part = H;
       }
-      KTimer kt(m, Q3_KT_GEMV_DOWN);
-      Q3_HIP(q3::launch_gemv(g, s));
+      if (!is_last && qkvfuse && gu.clear) {  // offered to the next layer's launch
+        pend = g;
+        have_pend = true;
+      } else {
+        KTimer kt(m, Q3_KT_GEMV_DOWN);
+        Q3_HIP(q3::launch_gemv(g, s));
+      }
     }
+  }
+  if (have_pend) {
+    KTimer kt(m, Q3_KT_GEMV_DOWN);
+    Q3_HIP(q3::launch_gemv(pend, s));
   }
 
   return lm_head(m, rows, lm_out, id_dst);
@@ -1125,6 +1176,7 @@ extern "C" int q3_model_open(void *blob, const q3_layout *lay, void *stream, q3_
   if (const char *e = std::getenv("Q3_DECODE_FUSE_OPROJ")) m->ofuse = std::atoi(e) != 0;
   if (const char *e = std::getenv("Q3_DECODE_GRAPH")) m->dgraph_on = std::atoi(e) != 0;
   if (const char *e = std::getenv("Q3_DECODE_FUSE_QKV")) m->qkvfuse = std::atoi(e) != 0;
+  if (const char *e = std::getenv("Q3_DECODE_MERGE_DOWN")) m->merge = std::atoi(e) != 0;
   m->bkeys_ld = lay->vocab / 128 + 64;  // one key per 128-column block of the lm GEMM
   m->btab_off = (sizeof(int32_t) * lay->seq + 255) & ~size_t(255);
   const size_t bstate_bytes = m->btab_off + sizeof(uint16_t) * static_cast<size_t>(lay->seq) * m->n_pages;
@@ -1139,14 +1191,16 @@ extern "C" int q3_model_open(void *blob, const q3_layout *lay, void *stream, q3_
       hipMalloc(&m->bkeys, sizeof(unsigned long long) * static_cast<size_t>(lay->seq) * m->bkeys_ld) !=
           hipSuccess ||
       hipMalloc(&m->bbest, sizeof(float) * lay->seq) != hipSuccess ||
-      hipMalloc(&m->opart, sizeof(float) * lay->heads * lay->hidden) != hipSuccess) {
+      hipMalloc(&m->opart, sizeof(float) * 2 * lay->heads * lay->hidden) != hipSuccess) {
     q3_model_close(m);
     return Q3_ERR_HIP;
   }
   {
     const size_t xbytes = sizeof(unsigned long long) * 3 * lay->heads * lay->head_dim;
+    const size_t wbytes = sizeof(uint32_t) * q3::kXwWords;
     if (hipMalloc(&m->xin, xbytes) != hipSuccess || hipMalloc(&m->xerr, sizeof(uint32_t)) != hipSuccess ||
-        hipMemset(m->xin, 0, xbytes) != hipSuccess || hipMemset(m->xerr, 0, sizeof(uint32_t)) != hipSuccess) {
+        hipMalloc(&m->xw, wbytes) != hipSuccess || hipMemset(m->xin, 0, xbytes) != hipSuccess ||
+        hipMemset(m->xw, 0xFF, wbytes) != hipSuccess || hipMemset(m->xerr, 0, sizeof(uint32_t)) != hipSuccess) {
       q3_model_close(m);
       return Q3_ERR_HIP;
     }
@@ -1523,7 +1577,7 @@ extern "C" int q3_model_repack(q3_model *m) {
 
 extern "C" int q3_model_fused_status(q3_model *m, uint32_t *fused, uint32_t *gave_up) {
   if (!m || !fused || !gave_up) return Q3_ERR_ARG;
-  *fused = m->qkvfuse ? 1u : 0u;
+  *fused = (m->qkvfuse ? 1u : 0u) | (m->qkvfuse && m->merge ? 2u : 0u);
   Q3_HIP(hipStreamSynchronize(m->stream));
   Q3_HIP(hipMemcpy(gave_up, m->xerr, sizeof(uint32_t), hipMemcpyDeviceToHost));
   return Q3_OK;
@@ -1638,6 +1692,7 @@ extern "C" int q3_model_close(q3_model *m) {
   if (m->opart) (void)hipFree(m->opart);
   if (m->xin) (void)hipFree(m->xin);
   if (m->xerr) (void)hipFree(m->xerr);
+  if (m->xw) (void)hipFree(m->xw);
   if (m->dgraph) (void)hipGraphExecDestroy(m->dgraph);
   if (m->packed) (void)hipFree(m->packed);
   for (int c = 0; c < Q3_KT_COUNT; ++c)

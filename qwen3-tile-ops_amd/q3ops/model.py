@@ -102,9 +102,10 @@ class Model:
             self.blob[off:off + a.size].copy_(torch.from_numpy(a))
 
     def fused_status(self) -> tuple[int, int]:
-        """(1 if a decode token's Q|K|V projection shares the attention's
-        launch, 1 if one of its bounded waits ever ran out since open);
-        synchronises the model's stream."""
+        """(bit 0: a decode token's Q|K|V projection shares the attention's
+        launch, bit 1: the previous layer's down projection runs in it too;
+        1 if one of their bounded waits ever ran out since open, else 0).
+        Synchronises the model's stream."""
         fused, gave_up = C.c_uint32(0), C.c_uint32(0)
         check(lib().q3_model_fused_status(self.handle, C.byref(fused), C.byref(gave_up)),
               "q3_model_fused_status")

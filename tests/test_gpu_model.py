@@ -204,13 +204,19 @@ def test_cfg2_full_depth(cuda, gold_meta):
     assert not probs, probs
 
 
-def test_cfg3_greedy(cuda, gold_meta):
-    note("cfg3 28 layers, 15-token prompt + 6 greedy tokens, mode 0")
+@pytest.mark.parametrize("merge", ["1", "0"])
+def test_cfg3_greedy(cuda, gold_meta, merge, monkeypatch):
+    """Config 3's greedy generation on the decode graph, with each layer's
+    down projection on its own (default) and in the next layer's Q|K|V +
+    attention launch (Q3_DECODE_MERGE_DOWN=1)."""
+    note(f"cfg3 28 layers, 15-token prompt + 6 greedy tokens, mode 0, merge={merge}")
+    monkeypatch.setenv("Q3_DECODE_MERGE_DOWN", merge)
     lay, blob = host_blob("cfg3")
     g = load_cfg("cfg3")
     m = Model(lay, blob)
     m.generate()
-    assert m.fused_status() == (1, 0)  # decode on the fused Q|K|V + attention launch
+    # decode on the fused Q|K|V + attention launch (+ the merged down)
+    assert m.fused_status() == (3 if merge == "1" else 1, 0)
     ids = m.ids()
     assert np.array_equal(ids[15:21], g["generated"]), (ids[15:21], g["generated"])
     best, idx = m.argmax()
@@ -220,6 +226,34 @@ def test_cfg3_greedy(cuda, gold_meta):
     probs = stage_problems(g, f"f{last}_", m, 1, 21, lay.layers - 1, last_row_only=True)
     m.close()
     assert not probs, probs
+
+
+def test_cfg3_merged_down_launches(cuda, gold_meta, monkeypatch):
+    """The merged launch runs: with kernel timing on (eager launches), the
+    down GEMV launches drop by layers - 1 per decode token against
+    Q3_DECODE_MERGE_DOWN=0, the fused launches stay, and both runs give the
+    golden ids and fused argmax."""
+    lay, blob = host_blob("cfg3")
+    g = load_cfg("cfg3")
+    counts = {}
+    for merge in ("1", "0"):
+        note(f"cfg3 generate with kernel timing, merge={merge}")
+        monkeypatch.setenv("Q3_DECODE_MERGE_DOWN", merge)
+        m = Model(lay, blob)
+        m.set_kernel_timing(True)
+        m.generate()
+        counts[merge] = {k: n for k, (_, n) in m.kernel_times().items()}
+        assert m.fused_status()[1] == 0
+        ids = m.ids()
+        assert np.array_equal(ids[15:21], g["generated"]), (merge, ids[15:21], g["generated"])
+        best, idx = m.argmax()
+        assert idx == int(np.argmax(g["logits"])) and bits_equal(np.float32(best), g["logits"].max())
+        m.close()
+    on, off = counts["1"], counts["0"]
+    assert on["attn_decode"] == off["attn_decode"] > 0
+    saved = off["gemv_down"] - on["gemv_down"]
+    assert saved > 0 and saved % (lay.layers - 1) == 0, (on, off)
+    assert saved // (lay.layers - 1) == on["attn_decode"] // lay.layers, (on, off)
 
 
 # Config 3's perf prefill as one 512-row chunk (layout seq = 512) on a
