@@ -231,7 +231,12 @@ def run_cfg1(stream, reps_min: int = 64) -> dict:
 # shape of the workload): every operand read once, every result written once.
 # ofused: the O projection runs inside the attention kernel (per-head f32
 # partials, NH x H, written there and read by the gate/up and down GEMVs).
-def decode_class_bytes(name: str, kv_len: int, ofused: bool = True) -> int:
+def decode_class_bytes(name: str, kv_len: int, ofused: bool = True, qkv_fused: bool = False,
+                       merged: float = 0.0) -> int:
+    """Algorithmic HBM bytes of one launch of a decode kernel class at
+    kv_len keys.  qkv_fused: the attention launch also runs the Q|K|V
+    projection; merged: the fraction of attention launches that also run
+    the previous layer's down projection."""
     H, QW, KW, KVH, NH, I, V = 1024, 2048, 1024, 8, 16, 3072, 151936
     part = NH * H * 4 if ofused else 0
     if name == "attn_decode":
@@ -239,7 +244,9 @@ def decode_class_bytes(name: str, kv_len: int, ofused: bool = True) -> int:
         ins = (QW + 2 * KW) * 4 + 2 * 128 * 4 + 2 * 64 * 4  # f32 q|k|v rows, q/k gains, cos/sin
         outs = (QW + NH * 4) * 2 + 2 * (KW + KVH * 4)  # q8/qs + o8/os, new K/V rows + scales
         o = (H * QW + 4 * H) + part if ofused else 0   # Wo and its scales, the partials
-        return kv_rows + ins + outs + o
+        qkv = decode_class_bytes("gemv_qkv", kv_len) - 4 * (QW + 2 * KW) if qkv_fused else 0  # (rows counted in ins)
+        down = merged * decode_class_bytes("gemv_down", kv_len, ofused)
+        return int(kv_rows + ins + outs + o + qkv + down)
     if name == "gemv_qkv":     # RMSNorm prologue (x, gain) + Q|K|V weights, f32 outputs
         N = QW + 2 * KW
         return N * H + 4 * N + 2 * 4 * H + 4 * N + (H + 4 * H + 16)
@@ -671,6 +678,63 @@ def run_prefill(args) -> dict:
             "path_roofline": pr, "argmax": [float(best), idx]}
 
 
+def calib_copies(mib: int) -> int:
+    """Three device-to-device copies of `mib` MiB: the known-size kernel the
+    PMC byte counters are scaled by.  Returns the bytes of one copy."""
+    import torch
+    n = mib << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return n
+
+
+def run_decode(args) -> dict:
+    """Config 3's b = 1 decode launches alone, eagerly (no decode graph):
+    the 512-token prefill, then `warmup` + `steps` single-token
+    q3_forward_chunk calls at positions 512, 513, ... with the fused
+    lm_head+argmax, each synchronised and reported on stderr; the steps
+    timed with HIP events.  The workload profiled for the decode kernels'
+    counters (every launch of a step is its own dispatch)."""
+    import torch
+    from q3ops import LM_ARGMAX
+    from q3ops.layout import CONFIGS, Layout, init_random_blob
+    from q3ops.model import Model
+
+    shape, init = CONFIGS["cfg3_perf"]
+    lay = Layout(shape)
+    blob = init_random_blob(lay, init)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        m = Model(lay, blob, stream=stream)
+    m.forward_chunk(0, N_PROMPT, LM_ARGMAX, True)
+    m.synchronize()
+    log("prefill done")
+    pos = N_PROMPT
+    for i in range(args.warmup):
+        m.forward_chunk(pos, 1, LM_ARGMAX, True)
+        m.synchronize()
+        log(f"warmup token {i} done")
+        pos += 1
+    total = 0.0
+    for i in range(args.steps):
+        total += time_events(lambda: m.forward_chunk(pos, 1, LM_ARGMAX, True), 1, stream)
+        log(f"token {i} done")
+        pos += 1
+    fused, gave_up = m.fused_status()
+    m.close()
+    ms = total / max(1, args.steps)
+    return {"metric": "ms per b=1 decode token (eager), Qwen3-0.6B W8A8, 1 MI355X",
+            "value": ms, "unit": "ms/token", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": ms, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+            "dtype": "int8", "data": "synthetic (random-init weights N(0,0.02) int8 per-row)",
+            "config": {"workload": f"cfg3 decode: 28-layer Qwen3-0.6B shape, tokens at {N_PROMPT}.. "
+                                   "after a 512-token prefill, one q3_forward_chunk each"},
+            "fused_status": [fused, gave_up]}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -683,23 +747,26 @@ def main() -> int:
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="finish with 3 device-to-device copies of MIB MiB (PMC calibration)")
-    ap.add_argument("--workload", choices=("cfg3", "cfg4", "engine", "prefill"), default="cfg3",
+    ap.add_argument("--workload", choices=("cfg3", "cfg4", "engine", "prefill", "decode"), default="cfg3",
                     help="cfg3: 512-token prefill + 64 b=1 decode steps (the headline line); "
                          "cfg4: 64-sequence batched paged decode; engine: continuous batching; "
-                         "prefill: the 512-token chunk alone")
+                         "prefill: the 512-token chunk alone; decode: eager b=1 decode tokens")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (this build has no multi-GPU path); "
               f"got --gpus {args.gpus}", file=sys.stderr)
         return 2
-    if args.workload in ("cfg4", "engine", "prefill"):
+    if args.workload in ("cfg4", "engine", "prefill", "decode"):
         import torch
         assert torch.cuda.is_available(), "bench.py needs a ROCm device"
         torch.cuda.set_device(0)
-        run = {"cfg4": run_cfg4, "engine": run_engine, "prefill": run_prefill}[args.workload]
+        run = {"cfg4": run_cfg4, "engine": run_engine, "prefill": run_prefill,
+               "decode": run_decode}[args.workload]
         res = run(args)
         if "cpu_check" in res:  # the standalone cfg4 line reports it as its CPU baseline
             res["cpu_baseline"] = res.pop("cpu_check")
+        if args.calib_copy > 0:
+            res["calib_copy_bytes"] = calib_copies(args.calib_copy)
         print(json.dumps(res), flush=True)
         return 0
 
@@ -778,6 +845,9 @@ def main() -> int:
         n_steps = max(1, kt["attn_decode"][1] // layers)
         kv_lens = [N_PROMPT + 1 + i for i in range(n_steps)]
         ofused = kt.get("gemv_o", (0.0, 0))[1] == 0  # no O GEMV launches: fused
+        qkv_fused = kt.get("gemv_qkv", (0.0, 0))[1] == 0  # no Q|K|V GEMV launches: in the attention's
+        # the attention launches that also ran the previous layer's down projection
+        merged = max(0.0, 1.0 - kt.get("gemv_down", (0.0, 0))[1] / max(1, kt["attn_decode"][1]))
         classes = {}
         for name, (tot_ms, n) in kt.items():
             if n == 0:
@@ -785,7 +855,8 @@ def main() -> int:
             if name == "lm_head":
                 byts = decode_class_bytes(name, 0)
             else:
-                byts = sum(decode_class_bytes(name, kv, ofused) for kv in kv_lens) / len(kv_lens)
+                byts = sum(decode_class_bytes(name, kv, ofused, qkv_fused, merged)
+                           for kv in kv_lens) / len(kv_lens)
             avg = tot_ms / n
             classes[name] = {"launches": n, "avg_us": avg * 1e3, "total_ms": tot_ms,
                              "bytes_per_launch": int(byts), "GBs": byts / avg / 1e6}
@@ -837,14 +908,7 @@ def main() -> int:
         cb["ids_compared"] = len(cb_gen)
         out["cpu_baseline"] = cb
     if args.calib_copy > 0:
-        n = args.calib_copy << 20
-        src = torch.empty(n, dtype=torch.uint8, device="cuda")
-        dst = torch.empty_like(src)
-        with torch.cuda.stream(stream):
-            for _ in range(3):
-                dst.copy_(src)
-        torch.cuda.synchronize()
-        out["calib_copy_bytes"] = n
+        out["calib_copy_bytes"] = calib_copies(args.calib_copy)
     print(json.dumps(out), flush=True)
     return 0
 

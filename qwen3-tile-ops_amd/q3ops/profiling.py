@@ -54,6 +54,8 @@ import sys
 # 7 the three-segment Q|K|V launch).
 CLASS_OF = [
     (r"attn_decode_kernel<1, ", "attn_decode"),
+    (r"qkv_attn_kernel<", "attn_decode"),        # Q|K|V projection + attention, one launch
+    (r"down_qkv_attn_kernel", "attn_decode"),    # the same with the previous layer's down projection
     (r"attn_decode_kernel<2, ", "attn_decode_batch"),
     (r"gemv_wr_kernel<[13], 1, 1, 2,", "gemv_qkv"),
     (r"gemv_wr_kernel<1, 1, 2, 3,", "gemv_gate_up"),
