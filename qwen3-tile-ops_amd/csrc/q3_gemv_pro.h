@@ -149,7 +149,12 @@ __device__ __forceinline__ void pro_load_row(const GemvArgs &a, const ProSrc &ps
   }
 }
 
-// NWV: waves per workgroup (4, or 12 in the fused decode kernel)
+// NWV: waves per workgroup (4, or 12 in the fused decode kernel).  The
+// barriers wait for LDS only (lds_barrier), not for every outstanding
+// vector load as __syncthreads does: the weight rows the kernel issued
+// after the row's operands keep arriving while the prologue computes, and
+// each wave's own loads are waited for where their registers are used.
+// Nothing global that one wave stores here is read by another.
 template <int PRO, int QW, int NP, int NWV = 4>
 __device__ void pro_compute_row(const GemvArgs &a, int m, const ProRow<QW, NP> &r, int8_t *a_lds,
                                 float *as_lds, float *blk, bool stage_writer) {
@@ -210,7 +215,7 @@ __device__ void pro_compute_row(const GemvArgs &a, int m, const ProRow<QW, NP> &
       if ((lane & 7) == 0) blk[(wave + 4 * q) * 8 + (lane >> 3)] = s;
     }
     }
-    __syncthreads();
+    lds_barrier();
     if (act) {
     float ss = 0.0f;
 #pragma unroll
@@ -248,7 +253,7 @@ __device__ void pro_compute_row(const GemvArgs &a, int m, const ProRow<QW, NP> &
     }
   }
   }
-  __syncthreads();  // blk is reused by the next row; A is complete
+  lds_barrier();  // blk is reused by the next row; A is complete
 }
 
 }  // namespace
