@@ -343,33 +343,8 @@ __device__ void prefetch_ranges(const AttnArgs &a, int w, int first) {
 // POLL (fused Q|K|V + attention launch): the K, V and Q waves of the
 // prologue take the new token's projection rows from AttnArgs::xin, polling
 // until the GEMV workgroups of the same launch have stored them, and clear
-// them for the next launch.  Every word has this one reader.
-constexpr int kPollLimit = 1 << 17;  // about 60 ms of round trips, then give up
-
-__device__ __forceinline__ unsigned long long xload(const unsigned long long *p) {
-  return __hip_atomic_load(const_cast<unsigned long long *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void xstore(unsigned long long *p, unsigned long long v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// 16 bytes a lane at p + 16 lane + {0, 1, 2, 3} KB with the cache policy of
-// xload (sc1: the agent-coherent level, so that stores from other XCDs are
-// seen), all four in flight, then a wait for them.  Inline assembly: the
-// compiler treats its buffer-load builtins as plain reads and hoists them
-// out of a polling loop.
-typedef unsigned v4u32 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ void xload_4k(const uint32_t *p, v4u32 &a, v4u32 &b, v4u32 &c, v4u32 &d) {
-  asm volatile(
-      "global_load_dwordx4 %0, %4, off sc1\n\t"
-      "global_load_dwordx4 %1, %4, off offset:1024 sc1\n\t"
-      "global_load_dwordx4 %2, %4, off offset:2048 sc1\n\t"
-      "global_load_dwordx4 %3, %4, off offset:3072 sc1\n\t"
-      "s_waitcnt vmcnt(0)"
-      : "=&v"(a), "=&v"(b), "=&v"(c), "=&v"(d)
-      : "v"(p + 4 * (threadIdx.x & 63))
-      : "memory");
-}
+// them for the next launch.  Every word has this one reader (xload /
+// xstore, q3_device.h).
 
 template <int QPW>
 __device__ __forceinline__ void attn_poll_rows(const AttnArgs &a, int qh0, int wave, int lane, FusedRegs &r) {

@@ -37,11 +37,6 @@ __device__ __forceinline__ v4i zero4() {
   return z;
 }
 
-__device__ __forceinline__ float key_value(uint32_t k) {
-  const uint32_t b = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
-  return bits_f32(b);
-}
-
 // Row destination of the int8 head output (dense view or paged KV slot).
 __device__ __forceinline__ void qdest_row(const QDest &d, int m, int head,
                                           int8_t **row8, float **scale) {

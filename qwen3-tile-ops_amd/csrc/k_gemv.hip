@@ -765,7 +765,8 @@ __global__ void __launch_bounds__(256) gemv_wr_kernel(GemvArgs a, int N) {
     if (lane == 0 && row0 + r < N) *dst = v;
   }
   if (a.clear) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    // (256 = the block size; blockDim.x would be one more argument read)
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
     if (i < a.nclear) a.clear[i] = kXwEmpty;
   }
 }

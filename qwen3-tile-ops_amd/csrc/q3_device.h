@@ -63,6 +63,45 @@ __device__ __forceinline__ uint32_t ordered_key(float v) {
   if (b == 0x80000000u) b = 0u;
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
+// the value an ordered key stands for
+__device__ __forceinline__ float key_value(uint32_t k) {
+  const uint32_t b = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+  return __uint_as_float(b);
+}
+
+// ---- words handed between workgroups of one launch ----------------------
+// Relaxed agent-scope atomics compile to global loads and stores with the
+// sc1 cache policy and no cache writeback or invalidate: a store becomes
+// visible to loads of that policy on every XCD, with no fence.  A word
+// carries its own "stored" mark (a value that cannot be empty), so a reader
+// polls it until the mark appears, with every load of a round in flight
+// before the check, and gives up after kPollLimit rounds (the launch then
+// reports it through a flag; no wait is unbounded).
+constexpr int kPollLimit = 1 << 17;  // about 60 ms of round trips
+
+__device__ __forceinline__ unsigned long long xload(const unsigned long long *p) {
+  return __hip_atomic_load(const_cast<unsigned long long *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void xstore(unsigned long long *p, unsigned long long v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// 16 bytes a lane at p + 16 lane + {0, 1, 2, 3} KB with the cache policy of
+// xload (sc1), all four in flight, then a wait for them.  Inline assembly:
+// the compiler treats its buffer-load builtins as plain reads and hoists them
+// out of a polling loop.
+typedef unsigned v4u32 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void xload_4k(const uint32_t *p, v4u32 &a, v4u32 &b, v4u32 &c, v4u32 &d) {
+  asm volatile(
+      "global_load_dwordx4 %0, %4, off sc1\n\t"
+      "global_load_dwordx4 %1, %4, off offset:1024 sc1\n\t"
+      "global_load_dwordx4 %2, %4, off offset:2048 sc1\n\t"
+      "global_load_dwordx4 %3, %4, off offset:3072 sc1\n\t"
+      "s_waitcnt vmcnt(0)"
+      : "=&v"(a), "=&v"(b), "=&v"(c), "=&v"(d)
+      : "v"(p + 4 * (threadIdx.x & 63))
+      : "memory");
+}
 
 // ---- LDS staging ------------------------------------------------------
 // Generic pointer to an LDS object as the address-space-3 pointer that

@@ -407,6 +407,9 @@ struct GemvArgs {
   uint32_t *clear;
   int nclear;
 };
+// (GemvArgs is read by every decode GEMV workgroup: fields added past its
+// sixth 64-byte line of kernel arguments cost each workgroup a dependent
+// scalar-cache miss, ~0.25 us, where the kernel reads them)
 bool gemv_supported(int M, int K, int group);
 // launch_gemv accepts GemvArgs::clear for a (the whole-row kernel runs it)
 bool gemv_clear_supported(const GemvArgs &a);
