@@ -32,6 +32,8 @@
 // K/V page slot of position kv_len - 1 (one workgroup per KV head) and the Q
 // int8 row for the record, and keep copies in LDS that the attention uses in
 // place of the global K/V of that position.
+#include <cstdlib>
+#include <cstring>
 #include <type_traits>
 
 #include "q3_device.h"
@@ -391,6 +393,13 @@ __device__ __forceinline__ void attn_decode_body(const AttnArgs &a, int bx, int 
     else
       __syncthreads();
   };
+  // FUSE: the first chunk's page ids (see pgs0 below), issued before the
+  // hot arguments' reads so that both are in flight together
+  uint32_t pre_pg[BPW];
+  if constexpr (FUSE) {
+#pragma unroll
+    for (int i = 0; i < BPW; ++i) pre_pg[i] = a.blk_page[wave_id() + NW * i];
+  }
   const HotArgs h = hot_args<FUSE, OFUSE>(a);
   // a batch of independent sequences: sequence blockIdx.y's length, pages
   // and rows of q8/qs/o8/os
@@ -416,10 +425,13 @@ __device__ __forceinline__ void attn_decode_body(const AttnArgs &a, int bx, int 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = wave_id();
-  const int grp = a.heads / a.kv_heads;
+  // query heads per kv head: 1 or 2 (attn_decode_supported), found with a
+  // compare and applied with shifts (an integer division here would be
+  // scheduled first and make the first batch of argument reads wait)
+  const int gshift = a.heads == a.kv_heads ? 0 : 1;
   const int qh0 = bx * QPW;
-  const int kvh = qh0 / grp;
-  const bool kv_writer = (qh0 % grp) == 0;
+  const int kvh = qh0 >> gshift;
+  const bool kv_writer = (qh0 & ((1 << gshift) - 1)) == 0;
   const uint32_t kv_len = batch ? static_cast<uint32_t>(a.row_pos[brow]) + 1 : h.kv_len;
   // one query row: pos0 = kv_len - 1, so kv_end = kv_len and the causal mask
   // only removes keys >= kv_len (attention_gqa.h:454-458)
@@ -447,15 +459,22 @@ __device__ __forceinline__ void attn_decode_body(const AttnArgs &a, int bx, int 
   // The exp table into LDS from immediates (no load to wait for; first
   // read in phase 3, after barriers), the first chunk's page ids, then the
   // prologue operands.
-  if (tid == 0) stage_exp2_table(sm.tab);
-  // (with FUSE from the arguments: a wave-uniform index, scalar loads)
+  // (with FUSE from the arguments: a wave-uniform index, scalar loads that
+  // do not wait for kv_len, since the caller repeats the last block's page
+  // in the entries past it; pinned, so that they are issued with the hot
+  // arguments rather than after the exp table's branch below)
   static_assert(!FUSE || CB <= 32, "first chunk's page ids come from blk_page");
   uint32_t pgs0[BPW];
 #pragma unroll
   for (int i = 0; i < BPW; ++i) {
-    const int jblk = __builtin_amdgcn_readfirstlane(min(wave + NW * i, nblocks - 1));
-    pgs0[i] = FUSE ? a.blk_page[jblk] : table[static_cast<uint32_t>(jblk * 32) / h.page_tokens];
+    if constexpr (FUSE) {
+      pgs0[i] = pin_sgpr(pre_pg[i]);
+    } else {
+      const int jblk = __builtin_amdgcn_readfirstlane(min(wave + NW * i, nblocks - 1));
+      pgs0[i] = table[static_cast<uint32_t>(jblk * 32) / h.page_tokens];
+    }
   }
+  if (tid == 0) stage_exp2_table(sm.tab);
   FusedRegs fr{};
   int8_t q8a = 0, q8b = 0;
   float qsa = 0.0f;
@@ -945,7 +964,7 @@ __device__ __forceinline__ void qkv_store_rows(const GemvArgs &a, const AttnArgs
   const GemvSeg &sg = a.seg[q.si];
   const int4 av = *reinterpret_cast<const int4 *>(a_lds + 16 * lane);
   const float asg = as_lds[lane >> 4];
-  const int grp = t.heads / t.kv_heads;
+  const int grp = t.heads == t.kv_heads ? 1 : 2;  // (attn_decode_supported: 1 or 2)
 #pragma unroll
   for (int r = 0; r < kFusedR; ++r) {
     int acc = sdot4(q.w[r].x, av.x, 0);
@@ -994,16 +1013,36 @@ __device__ __forceinline__ void qkv_gemv_role(const GemvArgs &a, const AttnArgs 
   qkv_store_rows(a, t, q, a_lds, as_lds, N);
 }
 
-template <int PRO>
+// The workgroup's role from its id and the role counts.  HEADS / KVH > 0:
+// the counts are compile-time constants for that head configuration
+// (heads workgroups, then the GEMV's ceil((heads + 2 kv_heads) * 128 /
+// (kFusedWaves * kFusedR))), so no workgroup reads a kernel argument before
+// its role's first batch of reads; each dependent argument read that misses
+// the scalar cache costs ~0.25 us, and the GEMV's outputs are on the
+// attention's critical path.  0: the counts are read from the arguments.
+template <int HEADS, int KVH>
+struct FusedRoles {
+  static constexpr int kGemv = (HEADS + 2 * KVH) * HD / (kFusedWaves * kFusedR) +
+                               ((HEADS + 2 * KVH) * HD % (kFusedWaves * kFusedR) != 0);
+  __device__ static int heads(const AttnArgs &a) { return HEADS > 0 ? HEADS : a.heads; }
+  __device__ static int gemv(int gemv_wgs) { return HEADS > 0 ? kGemv : gemv_wgs; }
+};
+
+template <int PRO, int HEADS, int KVH>
 __global__ void __launch_bounds__(kFusedWaves * 64) qkv_attn_kernel(GemvArgs g, AttnArgs a, int gemv_wgs) {
+  using Roles = FusedRoles<HEADS, KVH>;
   const int bx = static_cast<int>(blockIdx.x);
-  if (bx < a.heads) {
+  const int heads = Roles::heads(a);
+  if (bx < heads) {
     attn_decode_body<1, kFusedWaves, 2, true, true, true>(a, bx, 0);
-  } else if (bx < a.heads + gemv_wgs) {
-    qkv_gemv_role<PRO>(g, a, bx - a.heads, g.seg[2].n1);
+    return;
+  }
+  const int gw = Roles::gemv(gemv_wgs);
+  if (bx < heads + gw) {
+    qkv_gemv_role<PRO>(g, a, bx - heads, g.seg[2].n1);
   } else {
-    const int w = bx - a.heads - gemv_wgs;
-    if (w < a.pf_wgs) prefetch_ranges(a, w, a.heads + gemv_wgs);
+    const int w = bx - heads - gw;
+    if (w < a.pf_wgs) prefetch_ranges(a, w, heads + gw);
   }
 }
 
@@ -1126,16 +1165,22 @@ __device__ __forceinline__ void down_qkv_role(const GemvArgs &d, const GemvArgs 
   qkv_store_rows(a, t, q, a_lds, as_lds, N);
 }
 
+template <int HEADS, int KVH>
 __global__ void __launch_bounds__(kFusedWaves * 64) down_qkv_attn_kernel(GemvArgs d, GemvArgs g, AttnArgs a,
                                                                           int gemv_wgs) {
+  using Roles = FusedRoles<HEADS, KVH>;
   const int bx = static_cast<int>(blockIdx.x);
-  if (bx < a.heads) {
+  const int heads = Roles::heads(a);
+  if (bx < heads) {
     attn_decode_body<1, kFusedWaves, 2, true, true, true>(a, bx, 0);
-  } else if (bx < a.heads + gemv_wgs) {
-    down_qkv_role(d, g, a, bx - a.heads, gemv_wgs);
+    return;
+  }
+  const int gw = Roles::gemv(gemv_wgs);
+  if (bx < heads + gw) {
+    down_qkv_role(d, g, a, bx - heads, gw);
   } else {
-    const int w = bx - a.heads - gemv_wgs;
-    if (w < a.pf_wgs) prefetch_ranges(a, w, a.heads + gemv_wgs);
+    const int w = bx - heads - gw;
+    if (w < a.pf_wgs) prefetch_ranges(a, w, heads + gw);
   }
 }
 
@@ -1221,14 +1266,34 @@ bool qkv_attn_supported(const GemvArgs &g, const AttnArgs &a) {
   return attn_decode_supported(a);
 }
 
+namespace {
+// the Qwen3-0.6B head configuration takes the kernels with compile-time role
+// counts; Q3_DECODE_ROLES=args (read per launch) forces the generic ones
+bool fused_roles_const(const AttnArgs &a) {
+  if (a.heads != 16 || a.kv_heads != 8) return false;
+  const char *e = std::getenv("Q3_DECODE_ROLES");
+  return !(e && std::strcmp(e, "args") == 0);
+}
+}  // namespace
+
 hipError_t launch_qkv_attn(const GemvArgs &g, const AttnArgs &a, hipStream_t s) {
   const int gw = qkv_gemv_wgs(g);
   const int extra = a.pf_n > 0 ? a.pf_wgs : 0;
   const dim3 grid(a.heads + gw + extra);
-  if (g.pro == PRO_EMBED)
-    Q3_LAUNCH((qkv_attn_kernel<PRO_EMBED>), grid, dim3(kFusedWaves * 64), 0, s, g, a, gw);
-  else
-    Q3_LAUNCH((qkv_attn_kernel<PRO_NORM>), grid, dim3(kFusedWaves * 64), 0, s, g, a, gw);
+  const dim3 block(kFusedWaves * 64);
+  const bool c = fused_roles_const(a);
+  static_assert(FusedRoles<16, 8>::kGemv == (4096 + kFusedWaves * kFusedR - 1) / (kFusedWaves * kFusedR), "");
+  if (g.pro == PRO_EMBED) {
+    if (c)
+      Q3_LAUNCH((qkv_attn_kernel<PRO_EMBED, 16, 8>), grid, block, 0, s, g, a, gw);
+    else
+      Q3_LAUNCH((qkv_attn_kernel<PRO_EMBED, 0, 0>), grid, block, 0, s, g, a, gw);
+  } else {
+    if (c)
+      Q3_LAUNCH((qkv_attn_kernel<PRO_NORM, 16, 8>), grid, block, 0, s, g, a, gw);
+    else
+      Q3_LAUNCH((qkv_attn_kernel<PRO_NORM, 0, 0>), grid, block, 0, s, g, a, gw);
+  }
   return hipGetLastError();
 }
 
@@ -1258,7 +1323,10 @@ bool down_qkv_attn_supported(const GemvArgs &d, const GemvArgs &g, const AttnArg
 hipError_t launch_down_qkv_attn(const GemvArgs &d, const GemvArgs &g, const AttnArgs &a, hipStream_t s) {
   const int gw = qkv_gemv_wgs(g);
   const int extra = a.pf_n > 0 ? a.pf_wgs : 0;
-  Q3_LAUNCH(down_qkv_attn_kernel, dim3(a.heads + gw + extra), dim3(kFusedWaves * 64), 0, s, d, g, a, gw);
+  if (fused_roles_const(a))
+    Q3_LAUNCH((down_qkv_attn_kernel<16, 8>), dim3(a.heads + gw + extra), dim3(kFusedWaves * 64), 0, s, d, g, a, gw);
+  else
+    Q3_LAUNCH((down_qkv_attn_kernel<0, 0>), dim3(a.heads + gw + extra), dim3(kFusedWaves * 64), 0, s, d, g, a, gw);
   return hipGetLastError();
 }
 

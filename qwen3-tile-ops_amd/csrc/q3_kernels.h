@@ -257,7 +257,10 @@ struct AttnArgs {
   // blocks (blk_page[j] = table[32 j / page_tokens], j < min(32, blocks)) and of
   // the new token (table[(kv_len - 1) / page_tokens]), copied from the
   // caller's host mirror of the table, so that the first K/V addresses come
-  // from kernel arguments instead of a table load
+  // from kernel arguments instead of a table load.  With fuse_heads every
+  // entry is set: those past the last block repeat its page (the kernel
+  // reads its first chunk's entries without clamping them to the block
+  // count, so the reads do not wait for kv_len)
   uint32_t blk_page[32];
   uint32_t new_page;
   const float *fq, *fk, *fv;

@@ -518,7 +518,7 @@ int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int opti
       // host mirror of the table
       const uint32_t kv_len = pos + rows;
       const uint32_t nblk = std::min<uint32_t>(32, (kv_len + 31) / 32);
-      for (uint32_t j = 0; j < nblk; ++j) t.blk_page[j] = m->htab[j * 32 / kPageTokens];
+      for (uint32_t j = 0; j < 32; ++j) t.blk_page[j] = m->htab[std::min(j, nblk - 1) * 32 / kPageTokens];
       t.new_page = m->htab[(kv_len - 1) / kPageTokens];
       if (ofuse) {
         t.wo = lp.wo;

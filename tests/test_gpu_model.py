@@ -228,6 +228,31 @@ def test_cfg3_greedy(cuda, gold_meta, merge, monkeypatch):
     assert not probs, probs
 
 
+@pytest.mark.parametrize("merge", ["0", "1"])
+def test_cfg3_greedy_generic_roles(cuda, gold_meta, merge, monkeypatch):
+    """The fused launches with their role counts read from the kernel
+    arguments (Q3_DECODE_ROLES=args, as for any head configuration other
+    than 16 / 8) instead of the compile-time counts of the 16 / 8 shape:
+    config 3's greedy ids, fused argmax and last-forward stages stay
+    bit-exact."""
+    note(f"cfg3 greedy with argument role counts, merge={merge}")
+    monkeypatch.setenv("Q3_DECODE_ROLES", "args")
+    monkeypatch.setenv("Q3_DECODE_MERGE_DOWN", merge)
+    lay, blob = host_blob("cfg3")
+    g = load_cfg("cfg3")
+    m = Model(lay, blob)
+    m.generate()
+    assert m.fused_status() == (3 if merge == "1" else 1, 0)
+    ids = m.ids()
+    assert np.array_equal(ids[15:21], g["generated"]), (ids[15:21], g["generated"])
+    best, idx = m.argmax()
+    assert idx == int(np.argmax(g["logits"])) and bits_equal(np.float32(best), g["logits"].max())
+    last = int(g["n_forwards_with_logits"]) - 1
+    probs = stage_problems(g, f"f{last}_", m, 1, 21, lay.layers - 1, last_row_only=True)
+    m.close()
+    assert not probs, probs
+
+
 def test_cfg3_merged_down_launches(cuda, gold_meta, monkeypatch):
     """The merged launch runs: with kernel timing on (eager launches), the
     down GEMV launches drop by layers - 1 per decode token against
