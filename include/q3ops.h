@@ -369,8 +369,8 @@ int q3_model_info(const q3_model *m, q3_layout *lay, void **blob, void **stream)
 
 /* A decode token's Q|K|V projection and attention share one launch
  * (Q3_DECODE_FUSE_QKV at open, default 1): bit 0 of *fused is set when
- * enabled.  With it, layer L's down projection can run in layer L + 1's
- * launch (Q3_DECODE_MERGE_DOWN at open, default 0): bit 1.  Their workgroups hand
+ * enabled.  With it, layer L's down projection runs in layer L + 1's
+ * launch (Q3_DECODE_MERGE_DOWN at open, default 1): bit 1.  Their workgroups hand
  * the projection rows and the new residual row over in device memory with
  * bounded waits, and the merged launch's GEMV workgroups wait for each
  * other, so they must all be resident at once (another kernel holding most

@@ -64,12 +64,12 @@ struct q3_model {
   unsigned long long *xin = nullptr;
   uint32_t *xerr = nullptr;
   // decode (b = 1): layer L's down projection in layer L + 1's Q|K|V +
-  // attention launch (Q3_DECODE_MERGE_DOWN, default 0: the in-launch
-  // exchange of the new residual row costs about what the kernel boundary
-  // does, 0.6456 against 0.6455 ms/token), its new residual row as exchange
-  // words (AttnArgs::xw, kXwWords), cleared by the gate/up launch of every
-  // b = 1 layer while enabled
-  bool merge = false;
+  // attention launch (Q3_DECODE_MERGE_DOWN, default 1: 0.625 against 0.632
+  // ms/token), its new residual row as exchange words (AttnArgs::xw,
+  // kXwWords), cleared by the gate/up launch of every b = 1 layer while
+  // enabled.  Its GEMV workgroups wait for each other, so they need the
+  // device's CUs (down_qkv_attn_supported checks the count)
+  bool merge = true;
   uint32_t *xw = nullptr;
   // event timing of decode kernel classes (q3_model_set_kernel_timing)
   uint32_t kt_mask = 0;

@@ -102,7 +102,7 @@ def test_cfg0_generate_oproj_modes(cuda, gold_meta, fuse_oproj, fuse_qkv, monkey
     m = Model(lay, blob)
     m.set_ctrl(40, 2, 1)
     m.generate()
-    assert m.fused_status() == (int(fuse_qkv), 0)
+    assert m.fused_status() == (3 if fuse_qkv == "1" else 0, 0)
     ids = m.ids()
     assert np.array_equal(ids[40:42], g["generated"]), (ids[40:42], g["generated"])
     got = m.stage("logits", 1)[0]
@@ -207,8 +207,8 @@ def test_cfg2_full_depth(cuda, gold_meta):
 @pytest.mark.parametrize("merge", ["1", "0"])
 def test_cfg3_greedy(cuda, gold_meta, merge, monkeypatch):
     """Config 3's greedy generation on the decode graph, with each layer's
-    down projection on its own (default) and in the next layer's Q|K|V +
-    attention launch (Q3_DECODE_MERGE_DOWN=1)."""
+    down projection in the next layer's Q|K|V + attention launch (default)
+    and on its own (Q3_DECODE_MERGE_DOWN=0)."""
     note(f"cfg3 28 layers, 15-token prompt + 6 greedy tokens, mode 0, merge={merge}")
     monkeypatch.setenv("Q3_DECODE_MERGE_DOWN", merge)
     lay, blob = host_blob("cfg3")
@@ -471,7 +471,7 @@ def test_generate_300_token_prompt(cuda):
     m.generate()
     got = m.ids()[300:304].copy()
     best, idx = m.argmax()
-    assert m.fused_status() == (1, 0)
+    assert m.fused_status() == (3, 0)
     m.close()
     assert np.array_equal(got, gen), (got, gen)
     assert idx == int(np.argmax(logits)) and bits_equal(np.float32(best), logits.max())
