@@ -1266,14 +1266,14 @@ bool qkv_attn_supported(const GemvArgs &g, const AttnArgs &a) {
   return attn_decode_supported(a);
 }
 
-namespace {
-// the Qwen3-0.6B head configuration takes the kernels with compile-time role
-// counts; Q3_DECODE_ROLES=args (read per launch) forces the generic ones
-bool fused_roles_const(const AttnArgs &a) {
-  if (a.heads != 16 || a.kv_heads != 8) return false;
-  const char *e = std::getenv("Q3_DECODE_ROLES");
-  return !(e && std::strcmp(e, "args") == 0);
+bool head_consts(int heads, int kv_heads) {
+  if (heads != 16 || kv_heads != 8) return false;
+  const char *e = std::getenv("Q3_HEAD_CONSTS");
+  return !(e && std::strcmp(e, "0") == 0);
 }
+
+namespace {
+bool fused_roles_const(const AttnArgs &a) { return head_consts(a.heads, a.kv_heads); }
 }  // namespace
 
 hipError_t launch_qkv_attn(const GemvArgs &g, const AttnArgs &a, hipStream_t s) {

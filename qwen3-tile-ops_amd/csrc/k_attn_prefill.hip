@@ -107,7 +107,49 @@ struct Item {
   bool extra;      // the reference's 32-row walk has more (fully masked) blocks
 };
 
-__device__ __forceinline__ Item make_item(const AttnArgs &a, int qb, int kv_len) {
+// The kernel arguments the first copies and Q loads depend on, read together
+// at the top and pinned in SGPRs: read where first used, they form a chain of
+// scalar-cache round trips (~0.25 us each on a miss) before the first load.
+struct PreArgs {
+  int rows, causal, blk_page_n;
+  uint32_t kv_len, page_tokens;
+  const int32_t *kv_len_dev;
+  const uint16_t *table;
+  const int8_t *k, *v;
+  const float *ks, *vs;
+  int64_t page_bytes, row_bytes, scale_page_bytes, scale_row_bytes;
+  const int8_t *q8;
+  int64_t ldq;
+  const float *qs;
+  int64_t ldqs, qs_col;
+};
+
+__device__ __forceinline__ PreArgs pre_args(const AttnArgs &a) {
+  PreArgs p;
+  p.rows = pin_sgpr(a.rows);
+  p.causal = pin_sgpr(a.causal);
+  p.blk_page_n = pin_sgpr(a.blk_page_n);
+  p.kv_len = pin_sgpr(a.kv_len);
+  p.page_tokens = pin_sgpr(a.page_tokens);
+  p.kv_len_dev = pin_sgpr(a.kv_len_dev);
+  p.table = pin_sgpr(a.table);
+  p.k = pin_sgpr(a.k);
+  p.v = pin_sgpr(a.v);
+  p.ks = pin_sgpr(a.ks);
+  p.vs = pin_sgpr(a.vs);
+  p.page_bytes = pin_sgpr(a.page_bytes);
+  p.row_bytes = pin_sgpr(a.row_bytes);
+  p.scale_page_bytes = pin_sgpr(a.scale_page_bytes);
+  p.scale_row_bytes = pin_sgpr(a.scale_row_bytes);
+  p.q8 = pin_sgpr(a.q8);
+  p.ldq = pin_sgpr(a.ldq);
+  p.qs = pin_sgpr(a.qs);
+  p.ldqs = pin_sgpr(a.ldqs);
+  p.qs_col = pin_sgpr(a.qs_col);
+  return p;
+}
+
+__device__ __forceinline__ Item make_item(const PreArgs &a, int qb, int kv_len) {
   Item it;
   it.qi = qb * QB;
   it.nr = min(QB, a.rows - it.qi);
@@ -138,8 +180,12 @@ __device__ __forceinline__ uint32_t pack4(int b0, int b1, int b2, int b3) {
 }
 
 // (the second bound is waves per SIMD: 16 waves per CU, two single-block
-// workgroups or one pair, i.e. at most 128 VGPRs)
-template <int NI>
+// workgroups or one pair, i.e. at most 128 VGPRs).  HEADS / KVH > 0: the
+// head counts as compile-time constants (the grid is heads wide), so a
+// workgroup finds its head and query block without reading an argument or
+// dividing by one; each dependent kernel-argument read that misses the
+// scalar cache costs ~0.25 us before the first copy.  0: read from a.
+template <int NI, int HEADS = 0, int KVH = 0>
 __global__ void __launch_bounds__(Cfg<NI>::NW * 64, 4) attn_prefill_kernel(AttnArgs a) {
   constexpr int CB = Cfg<NI>::CB;
   extern __shared__ __align__(16) int8_t smem[];
@@ -154,15 +200,22 @@ __global__ void __launch_bounds__(Cfg<NI>::NW * 64, 4) attn_prefill_kernel(AttnA
   const int wave = wave_id();
   int lc = lane & 15;
   int lg = lane >> 4;
+  // the first chunk's page id of this wave's block (used where the block is
+  // below blk_page_n; read with the other arguments)
+  static_assert(Cfg<NI>::CB <= 32, "first chunk's page ids come from blk_page");
+  const uint32_t pg_arg0 = a.blk_page[wave];
+  const PreArgs pa = pre_args(a);
   // XCD-aware order: workgroup L runs on XCD L % 8 and takes KV head
   // L % kv_heads, so the workgroups of one XCD share the K/V rows its L2 holds
-  const int group = a.heads / a.kv_heads;
-  const int L_id = blockIdx.x + gridDim.x * blockIdx.y;
-  const int nqb = (a.rows + QB - 1) / QB;
+  const int a_heads = HEADS > 0 ? HEADS : a.heads;
+  const int a_kv_heads = HEADS > 0 ? KVH : a.kv_heads;
+  const int group = a_heads / a_kv_heads;
+  const int L_id = blockIdx.x + (HEADS > 0 ? HEADS : static_cast<int>(gridDim.x)) * blockIdx.y;
+  const int nqb = (pa.rows + QB - 1) / QB;
   int kvh, h, qbA, qbB;
   if constexpr (NI == 2) {  // grid: heads x the pairs
-    kvh = L_id % a.kv_heads;
-    const int r_id = L_id / a.kv_heads;
+    kvh = L_id % a_kv_heads;
+    const int r_id = L_id / a_kv_heads;
     h = kvh * group + r_id % group;
     qbA = r_id / group;
     qbB = nqb - 1 - qbA;
@@ -171,23 +224,23 @@ __global__ void __launch_bounds__(Cfg<NI>::NW * 64, 4) attn_prefill_kernel(AttnA
             // complementary query blocks nqb - 1 - qb and qb of one head; the
             // long (late) query blocks are dispatched first, since the last
             // of them to end sets the launch
-    const int half = nqb / 2 * a.heads;
+    const int half = nqb / 2 * a_heads;
     const int idx = L_id < half ? L_id : L_id - half;
-    const int hs = idx % a.heads;
-    kvh = hs % a.kv_heads;
-    h = kvh * group + hs / a.kv_heads;
-    qbB = L_id < half ? nqb - 1 - idx / a.heads : idx / a.heads;
+    const int hs = idx % a_heads;
+    kvh = hs % a_kv_heads;
+    h = kvh * group + hs / a_kv_heads;
+    qbB = L_id < half ? nqb - 1 - idx / a_heads : idx / a_heads;
     qbA = qbB;
   }
-  int kv_len = static_cast<int>(a.kv_len);
-  if (a.kv_len_dev) kv_len += *a.kv_len_dev;
+  int kv_len = static_cast<int>(pa.kv_len);
+  if (pa.kv_len_dev) kv_len += *pa.kv_len_dev;
   const bool twoA = NI == 2 && qbB > qbA;  // item A exists (else B is the only item)
-  const Item IA = make_item(a, qbA, kv_len);
-  const Item IB = make_item(a, twoA ? qbB : qbA, kv_len);
+  const Item IA = make_item(pa, qbA, kv_len);
+  const Item IB = make_item(pa, twoA ? qbB : qbA, kv_len);
   const int nA = twoA ? IA.nblk : 0;
   const int nB = IB.nblk;
   const int G = (nB + CB - 1) / CB;
-  const int pt_shift = 31 - __builtin_clz(a.page_tokens);  // page_tokens is a power of two
+  const int pt_shift = 31 - __builtin_clz(pa.page_tokens);  // page_tokens is a power of two
   // blocks of item `it` in chunk g
   auto nb_of = [&](int it, int g) { return max(0, min(CB, (it ? nB : nA) - g * CB)); };
   auto last_of = [&](int it, int g) { return (it ? nB : nA) > 0 && ((it ? nB : nA) - 1) / CB == g; };
@@ -204,20 +257,20 @@ __global__ void __launch_bounds__(Cfg<NI>::NW * 64, 4) attn_prefill_kernel(AttnA
     uint32_t p = 0;
     const int j = g * CB + wave;
     if (g < G && wave < nb_of(1, g)) {
-      if (j < a.blk_page_n)
-        p = a.blk_page[j];
+      if (j < pa.blk_page_n)
+        p = g == 0 ? pin_sgpr(pg_arg0) : a.blk_page[j];
       else if (lane == 0)
-        p = a.table[static_cast<uint32_t>(j * KB) >> pt_shift];
+        p = pa.table[static_cast<uint32_t>(j * KB) >> pt_shift];
     }
     return p;
   };
   auto pg = [](uint32_t p) { return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(p), 0)); };
   // in-page offsets fit in 32 bits (checked on the host)
-  const int rb = static_cast<int>(a.row_bytes), srb = static_cast<int>(a.scale_row_bytes);
+  const int rb = static_cast<int>(pa.row_bytes), srb = static_cast<int>(pa.scale_row_bytes);
   auto copy_v = [&](int g, uint32_t page) {
     if (g >= G || wave >= nb_of(1, g)) return;
-    const int slot0 = ((g * CB + wave) * KB) & (a.page_tokens - 1);
-    const int8_t *vb = a.v + static_cast<int64_t>(pg(page)) * a.page_bytes + kvh * HD;
+    const int slot0 = ((g * CB + wave) * KB) & (pa.page_tokens - 1);
+    const int8_t *vb = pa.v + static_cast<int64_t>(pg(page)) * pa.page_bytes + kvh * HD;
     int8_t *dst = L.v[g & 1][wave];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
@@ -228,8 +281,8 @@ __global__ void __launch_bounds__(Cfg<NI>::NW * 64, 4) attn_prefill_kernel(AttnA
   };
   auto load_k = [&](int g, uint32_t page) {
     if (g >= G || wave >= nb_of(1, g)) return;
-    const int slot0 = ((g * CB + wave) * KB) & (a.page_tokens - 1);
-    const int8_t *kb = a.k + static_cast<int64_t>(pg(page)) * a.page_bytes + kvh * HD;
+    const int slot0 = ((g * CB + wave) * KB) & (pa.page_tokens - 1);
+    const int8_t *kb = pa.k + static_cast<int64_t>(pg(page)) * pa.page_bytes + kvh * HD;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
@@ -243,10 +296,10 @@ __global__ void __launch_bounds__(Cfg<NI>::NW * 64, 4) attn_prefill_kernel(AttnA
   float ksr[2][4], vsr[2][4];
   auto load_sc = [&](int g, uint32_t page) {
     if (g >= G || wave >= nb_of(1, g)) return;
-    const int slot0 = ((g * CB + wave) * KB) & (a.page_tokens - 1);
-    const int64_t sp = static_cast<int64_t>(pg(page)) * a.scale_page_bytes + kvh * 4;
-    const int8_t *kb = reinterpret_cast<const int8_t *>(a.ks) + sp;
-    const int8_t *vb = reinterpret_cast<const int8_t *>(a.vs) + sp;
+    const int slot0 = ((g * CB + wave) * KB) & (pa.page_tokens - 1);
+    const int64_t sp = static_cast<int64_t>(pg(page)) * pa.scale_page_bytes + kvh * 4;
+    const int8_t *kb = reinterpret_cast<const int8_t *>(pa.ks) + sp;
+    const int8_t *vb = reinterpret_cast<const int8_t *>(pa.vs) + sp;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
@@ -274,10 +327,10 @@ __global__ void __launch_bounds__(Cfg<NI>::NW * 64, 4) attn_prefill_kernel(AttnA
     for (int it = 0; it < 2; ++it) {
       const Item &I = it ? IB : IA;
       const bool ok = lc < I.nr && (it || twoA);
-      const int8_t *q = a.q8 + static_cast<int64_t>(I.qi + lc) * a.ldq + h * HD + 16 * lg;
+      const int8_t *q = pa.q8 + static_cast<int64_t>(I.qi + lc) * pa.ldq + h * HD + 16 * lg;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) qop[it][ks] = ok ? *reinterpret_cast<const v4i *>(q + 64 * ks) : zero4();
-      qsv[it] = ok ? a.qs[static_cast<int64_t>(I.qi + lc) * a.ldqs + h * a.qs_col] : 0.0f;
+      qsv[it] = ok ? pa.qs[static_cast<int64_t>(I.qi + lc) * pa.ldqs + h * pa.qs_col] : 0.0f;
     }
   };
   load_q(0);
@@ -590,20 +643,32 @@ hipError_t launch_attn_prefill(const AttnArgs &a, hipStream_t s) {
   const int nqb = (a.rows + QB - 1) / QB;
   if (pair) {
     if (!attr_set[1]) {
-      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&attn_prefill_kernel<2>),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, sizeof(Lds<2>));
-      if (e != hipSuccess) return e;
+      for (const void *f : {reinterpret_cast<const void *>(&attn_prefill_kernel<2, 16, 8>),
+                            reinterpret_cast<const void *>(&attn_prefill_kernel<2, 0, 0>)}) {
+        const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, sizeof(Lds<2>));
+        if (e != hipSuccess) return e;
+      }
       attr_set[1] = true;
     }
-    Q3_LAUNCH(attn_prefill_kernel<2>, dim3(a.heads, (nqb + 1) / 2), dim3(Cfg<2>::NW * 64), sizeof(Lds<2>), s, a);
+    if (head_consts(a.heads, a.kv_heads))
+      Q3_LAUNCH((attn_prefill_kernel<2, 16, 8>), dim3(a.heads, (nqb + 1) / 2), dim3(Cfg<2>::NW * 64), sizeof(Lds<2>),
+                s, a);
+    else
+      Q3_LAUNCH((attn_prefill_kernel<2, 0, 0>), dim3(a.heads, (nqb + 1) / 2), dim3(Cfg<2>::NW * 64), sizeof(Lds<2>),
+                s, a);
   } else {
     if (!attr_set[0]) {
-      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&attn_prefill_kernel<1>),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, sizeof(Lds<1>));
-      if (e != hipSuccess) return e;
+      for (const void *f : {reinterpret_cast<const void *>(&attn_prefill_kernel<1, 16, 8>),
+                            reinterpret_cast<const void *>(&attn_prefill_kernel<1, 0, 0>)}) {
+        const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, sizeof(Lds<1>));
+        if (e != hipSuccess) return e;
+      }
       attr_set[0] = true;
     }
-    Q3_LAUNCH(attn_prefill_kernel<1>, dim3(a.heads, nqb), dim3(Cfg<1>::NW * 64), sizeof(Lds<1>), s, a);
+    if (head_consts(a.heads, a.kv_heads))
+      Q3_LAUNCH((attn_prefill_kernel<1, 16, 8>), dim3(a.heads, nqb), dim3(Cfg<1>::NW * 64), sizeof(Lds<1>), s, a);
+    else
+      Q3_LAUNCH((attn_prefill_kernel<1, 0, 0>), dim3(a.heads, nqb), dim3(Cfg<1>::NW * 64), sizeof(Lds<1>), s, a);
   }
   return hipGetLastError();
 }

@@ -456,6 +456,11 @@ hipError_t launch_attn_decode(const AttnArgs &a, hipStream_t s);
 // their head's Q/K/V from a.xin.  g still writes its f32 outputs.
 bool qkv_attn_supported(const GemvArgs &g, const AttnArgs &a);
 hipError_t launch_qkv_attn(const GemvArgs &g, const AttnArgs &a, hipStream_t s);
+// the Qwen3-0.6B head configuration (16 query, 8 kv heads) takes kernels
+// with the head counts as compile-time constants (the fused decode launches'
+// role counts, the prefill attention's workgroup mapping); Q3_HEAD_CONSTS=0,
+// read per launch, forces the generic kernels that read them
+bool head_consts(int heads, int kv_heads);
 // launch_qkv_attn with the previous layer's down projection in the same
 // launch: d is that GEMV (M = 1, K = inter, group 256, PRO_QUANT of the
 // SwiGLU row, one EPI_ADD segment into x with the O partials, d.part, in

@@ -230,13 +230,13 @@ def test_cfg3_greedy(cuda, gold_meta, merge, monkeypatch):
 
 @pytest.mark.parametrize("merge", ["0", "1"])
 def test_cfg3_greedy_generic_roles(cuda, gold_meta, merge, monkeypatch):
-    """The fused launches with their role counts read from the kernel
-    arguments (Q3_DECODE_ROLES=args, as for any head configuration other
-    than 16 / 8) instead of the compile-time counts of the 16 / 8 shape:
-    config 3's greedy ids, fused argmax and last-forward stages stay
-    bit-exact."""
-    note(f"cfg3 greedy with argument role counts, merge={merge}")
-    monkeypatch.setenv("Q3_DECODE_ROLES", "args")
+    """The fused decode launches and the prefill attention with the head
+    counts read from the kernel arguments (Q3_HEAD_CONSTS=0, as for any head
+    configuration other than 16 / 8) instead of the compile-time constants
+    of the 16 / 8 shape: config 3's greedy ids, fused argmax and
+    last-forward stages stay bit-exact."""
+    note(f"cfg3 greedy with argument head counts, merge={merge}")
+    monkeypatch.setenv("Q3_HEAD_CONSTS", "0")
     monkeypatch.setenv("Q3_DECODE_MERGE_DOWN", merge)
     lay, blob = host_blob("cfg3")
     g = load_cfg("cfg3")
