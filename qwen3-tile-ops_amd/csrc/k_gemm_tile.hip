@@ -485,6 +485,28 @@ hipError_t launch_gemm_tile(const TileArgs &a, int epi, hipStream_t s) {
   // even where the stream kernel applies (read at every launch)
   const char *ev = std::getenv("Q3_PREFILL_GEMM");
   const bool stream_ok = !(ev && std::strcmp(ev, "tile") == 0);
+  // Plain and residual stores on row-major weights with at least 256 tiles
+  // of 64 x 128 (config 1's M = 2048 rows, gate+up at M = 512): those tiles
+  // (8 waves of 32 x 32, three 128-byte k-steps in flight) beat the stream
+  // kernel's 32-row tiles, whose weight bytes serve half the rows and whose
+  // gathered 16-row x 64-byte weight loads stream slower than the tile
+  // kernel's whole 128-byte row pieces: 1.5-1.7x at M = 2048 on every
+  // config-1 shape (sweep of 11 tile shapes; the stream kernel stays ahead
+  // on the smaller grids).
+  if ((epi == EPI_STORE || epi == EPI_ADD) && !a.b_packed && a.M > 64 && gemm_tile_supported(a, epi) &&
+      static_cast<int64_t>((a.M + 63) / 64) * (a.N / 128) >= 256) {
+    if (a.bs_ld)
+      return epi == EPI_STORE ? launch_tile<64, 128, 2, 1, 3, 128, EPI_STORE, true>(a, s)
+                              : launch_tile<64, 128, 2, 1, 3, 128, EPI_ADD, true>(a, s);
+    return epi == EPI_STORE ? launch_tile<64, 128, 2, 1, 3, 128, EPI_STORE>(a, s)
+                            : launch_tile<64, 128, 2, 1, 3, 128, EPI_ADD>(a, s);
+  }
+  // gate/up + SwiGLU + quant on row-major weights: this kernel's 32 x 256
+  // tiles of both matrices (whole 128-byte row pieces through LDS) beat the
+  // stream kernel's gathered weight loads (op level, M = 512: 16.3 against
+  // 21.3 us; M = 2048: 44.0 against 59.7 us)
+  if (epi == EPI_SWIGLUQ && !a.b_packed && gemm_tile_supported(a, epi))
+    return launch_tile<32, 256, 1, 2, 2, 128, EPI_SWIGLUQ>(a, s);
   if ((stream_ok || a.b_packed) && gemm_stream_supported(a, epi)) return launch_gemm_stream(a, epi, s);
   if (a.b_packed) return hipErrorInvalidValue;  // only the stream kernel reads packed weights
   if (!gemm_tile_supported(a, epi)) return hipErrorInvalidValue;
