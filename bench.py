@@ -747,15 +747,22 @@ def main() -> int:
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="finish with 3 device-to-device copies of MIB MiB (PMC calibration)")
-    ap.add_argument("--workload", choices=("cfg3", "cfg4", "engine", "prefill", "decode"), default="cfg3",
+    ap.add_argument("--workload", choices=("cfg3", "cfg4", "engine", "prefill", "decode", "cfg1"), default="cfg3",
                     help="cfg3: 512-token prefill + 64 b=1 decode steps (the headline line); "
                          "cfg4: 64-sequence batched paged decode; engine: continuous batching; "
-                         "prefill: the 512-token chunk alone; decode: eager b=1 decode tokens")
+                         "prefill: the 512-token chunk alone; decode: eager b=1 decode tokens; "
+                         "cfg1: the config 1 GEMM sweep alone")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (this build has no multi-GPU path); "
               f"got --gpus {args.gpus}", file=sys.stderr)
         return 2
+    if args.workload == "cfg1":  # the config 1 GEMM sweep alone (for profiling its kernels)
+        import torch
+        assert torch.cuda.is_available(), "bench.py needs a ROCm device"
+        torch.cuda.set_device(0)
+        print(json.dumps(run_cfg1(torch.cuda.Stream())), flush=True)
+        return 0
     if args.workload in ("cfg4", "engine", "prefill", "decode"):
         import torch
         assert torch.cuda.is_available(), "bench.py needs a ROCm device"

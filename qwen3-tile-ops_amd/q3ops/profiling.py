@@ -3,6 +3,7 @@
 files of one of the rocprofv3 commands named in the summary.
 
     python -m q3ops.profiling stats <kernel_stats.csv> --cmd "<command>" [--top N] [--title T]
+        [--no-classes]
         -> markdown table of the per-kernel statistics (stdout)
 
     python -m q3ops.profiling pmc --fetch <counter_collection.csv>
@@ -112,13 +113,16 @@ def class_of(name: str) -> str | None:
     return None
 
 
-def stats_md(path: str, cmd: str, top: int, title: str | None = None) -> str:
+def stats_md(path: str, cmd: str, top: int, title: str | None = None, classes: bool = True) -> str:
+    """classes=False leaves the class column empty (a workload of op-level
+    calls, whose kernels the model-path classes would misname)."""
     rows = list(csv.DictReader(open(path)))
     rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
     out = ([f"# {title}", ""] if title else []) + [f"Command: `{cmd}`", "", f"Source: rocprofv3 `--kernel-trace --stats` ({path.split('/')[-1]})", "",
            "| kernel | class | calls | avg us | min us | max us | % time |", "|---|---|---:|---:|---:|---:|---:|"]
     for r in rows[:top]:
-        out.append(f"| `{short_name(r['Name'])}` | {class_of(r['Name']) or ''} | {r['Calls']} | "
+        cls = (class_of(r["Name"]) or "") if classes else ""
+        out.append(f"| `{short_name(r['Name'])}` | {cls} | {r['Calls']} | "
                    f"{float(r['AverageNs']) / 1e3:.2f} | {float(r['MinNs']) / 1e3:.2f} | "
                    f"{float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.2f} |")
     return "\n".join(out) + "\n"
@@ -226,6 +230,7 @@ def main(argv=None) -> int:
     s.add_argument("--cmd", required=True)
     s.add_argument("--top", type=int, default=20)
     s.add_argument("--title", help="heading of the markdown summary")
+    s.add_argument("--no-classes", action="store_true", help="leave the class column empty")
     p = sub.add_parser("pmc")
     p.add_argument("--fetch", required=True)
     p.add_argument("--write", required=True)
@@ -239,7 +244,7 @@ def main(argv=None) -> int:
     c.add_argument("--clock-ghz", type=float, default=2.4)
     a = ap.parse_args(argv)
     if a.cmd_name == "stats":
-        sys.stdout.write(stats_md(a.csv, a.cmd, a.top, a.title))
+        sys.stdout.write(stats_md(a.csv, a.cmd, a.top, a.title, not a.no_classes))
     elif a.cmd_name == "counters":
         json.dump(counters_json(a.csv, a.cmd, a.cus, a.stats, a.clock_ghz), sys.stdout, indent=1)
         sys.stdout.write("\n")
