@@ -228,6 +228,30 @@ def test_cfg3_greedy(cuda, gold_meta, merge, monkeypatch):
     assert not probs, probs
 
 
+@pytest.mark.parametrize("pf", ["0", "37"])
+def test_cfg3_greedy_prefetch_counts(cuda, gold_meta, pf, monkeypatch):
+    """The decode launches with no prefetch workgroups and with an odd count
+    of them (Q3_DECODE_PREFETCH_WGS, read at open; the default is 176): the
+    prefetch reads only warm the caches, so config 3's greedy ids, fused
+    argmax and last-forward stages stay bit-exact and no bounded wait runs
+    out."""
+    note(f"cfg3 greedy with {pf} prefetch workgroups")
+    monkeypatch.setenv("Q3_DECODE_PREFETCH_WGS", pf)
+    lay, blob = host_blob("cfg3")
+    g = load_cfg("cfg3")
+    m = Model(lay, blob)
+    m.generate()
+    assert m.fused_status() == (3, 0)
+    ids = m.ids()
+    assert np.array_equal(ids[15:21], g["generated"]), (ids[15:21], g["generated"])
+    best, idx = m.argmax()
+    assert idx == int(np.argmax(g["logits"])) and bits_equal(np.float32(best), g["logits"].max())
+    last = int(g["n_forwards_with_logits"]) - 1
+    probs = stage_problems(g, f"f{last}_", m, 1, 21, lay.layers - 1, last_row_only=True)
+    m.close()
+    assert not probs, probs
+
+
 @pytest.mark.parametrize("merge", ["0", "1"])
 def test_cfg3_greedy_generic_roles(cuda, gold_meta, merge, monkeypatch):
     """The fused decode launches and the prefill attention with the head
