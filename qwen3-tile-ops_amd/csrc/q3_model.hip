@@ -548,16 +548,20 @@ int forward_small(q3_model *m, uint32_t pos, uint32_t rows, int lm_out, int opti
       };
       // (with the O projection fused, this layer's Wo is read by the
       // attention itself, so the next layer's is fetched instead)
-      if (!ofuse) add_pf(lp.wo, HH * QW);
-      add_pf(lp.wg, static_cast<int64_t>(I) * H);
-      add_pf(lp.wu, static_cast<int64_t>(I) * H);
-      add_pf(lp.wd, HH * I);
+      // (each matrix with the row scales that follow it in the blob, and
+      // the norm gains of this layer and the next: the small operands every
+      // workgroup of the next launches reads first)
+      if (!ofuse) add_pf(lp.wo, HH * QW + 4 * HH);
+      add_pf(lp.wg, static_cast<int64_t>(I) * H + 4 * I);
+      add_pf(lp.wu, static_cast<int64_t>(I) * H + 4 * I);
+      add_pf(lp.wd, HH * I + 4 * HH);
+      add_pf(reinterpret_cast<const int8_t *>(lp.n1), y.kLAYERN_STRIDE * (is_last ? 1 : 2));
       if (!is_last) {
         const LayerPtrs nx = layer_ptrs(m, L + 1);
-        add_pf(nx.wq, static_cast<int64_t>(QW) * H);
-        add_pf(nx.wk, static_cast<int64_t>(KW) * H);
-        add_pf(nx.wv, static_cast<int64_t>(KW) * H);
-        if (ofuse) add_pf(nx.wo, HH * QW);
+        add_pf(nx.wq, static_cast<int64_t>(QW) * H + 4 * QW);
+        add_pf(nx.wk, static_cast<int64_t>(KW) * H + 4 * KW);
+        add_pf(nx.wv, static_cast<int64_t>(KW) * H + 4 * KW);
+        if (ofuse) add_pf(nx.wo, HH * QW + 4 * HH);
       }
       // the K/V pages (and scales) the next attention reads: the next
       // layer's, or layer 0's for the next token after the last layer; each
