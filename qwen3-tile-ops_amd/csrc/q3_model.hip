@@ -1175,7 +1175,9 @@ extern "C" int q3_model_open(void *blob, const q3_layout *lay, void *stream, q3_
   m->stream = static_cast<hipStream_t>(stream);
   m->n_pages = lay->max_seq / kPageTokens;
   m->keys_ld = lay->vocab / 16 + 64;  // one key per lm_head column block
-  m->pf_wgs = 176;  // of 96-256: 96 0.754, 128 0.718, 176 0.712, 192 0.713, 256 0.716 ms/token
+  // (re-swept with the merged launch, ms/token, two runs each: 69 0.6225, 88 0.670, 104 0.619,
+  // 120 0.6182, 136 0.6182, 152 0.6194, 176 0.6203, 240 0.619)
+  m->pf_wgs = 120;
   if (const char *e = std::getenv("Q3_DECODE_PREFETCH_WGS")) m->pf_wgs = std::max(0, std::atoi(e));
   if (const char *e = std::getenv("Q3_DECODE_FUSE_OPROJ")) m->ofuse = std::atoi(e) != 0;
   if (const char *e = std::getenv("Q3_DECODE_GRAPH")) m->dgraph_on = std::atoi(e) != 0;

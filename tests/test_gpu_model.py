@@ -231,7 +231,7 @@ def test_cfg3_greedy(cuda, gold_meta, merge, monkeypatch):
 @pytest.mark.parametrize("pf", ["0", "37"])
 def test_cfg3_greedy_prefetch_counts(cuda, gold_meta, pf, monkeypatch):
     """The decode launches with no prefetch workgroups and with an odd count
-    of them (Q3_DECODE_PREFETCH_WGS, read at open; the default is 176): the
+    of them (Q3_DECODE_PREFETCH_WGS, read at open; the default is 120): the
     prefetch reads only warm the caches, so config 3's greedy ids, fused
     argmax and last-forward stages stay bit-exact and no bounded wait runs
     out."""
