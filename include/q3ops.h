@@ -70,7 +70,10 @@ enum {
 /* Output form of the lm_head stage: main_big.cpp:142 (LmHeadOut). */
 enum { Q3_LM_NONE = 0, Q3_LM_LOGITS = 1, Q3_LM_ARGMAX = 2 };
 
-/* kernels/matrix.h:27-34 (MatrixView).  data is a device address. */
+/* kernels/matrix.h:27-34 (MatrixView).  data is a device address.  A view
+ * with rows == 0 may have data == NULL (an empty tensor); an operator whose
+ * row count is 0 returns Q3_OK without launching or writing anything, as the
+ * reference's row loops then do nothing. */
 typedef struct q3_view {
   void *data;
   int32_t row_bytes;

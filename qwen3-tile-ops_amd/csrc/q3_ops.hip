@@ -14,9 +14,14 @@ std::atomic<int> g_silent{0};
 
 inline int elem_size(uint8_t dt) { return (dt == Q3_DT_I8 || dt == Q3_DT_U8) ? 1 : 4; }
 
+// A view with no data: NULL data on a view that has rows.  A 0-row view
+// may carry NULL (a caller's empty tensor); the operators then do nothing
+// for it, as the reference's row loops do.
+inline bool no_data(const q3_view *v) { return !v->data && v->rows != 0; }
+
 // A dense-column view of the given dtype with at least `cols` columns.
 int check_view(const q3_view *v, uint8_t dt) {
-  if (!v || !v->data) return Q3_ERR_ARG;
+  if (!v || no_data(v)) return Q3_ERR_ARG;
   if (v->dtype != dt) return Q3_ERR_DTYPE;
   const int es = elem_size(dt);
   if (v->col_bytes != es) return Q3_ERR_VIEW;
@@ -28,7 +33,7 @@ int check_view(const q3_view *v, uint8_t dt) {
 // A per-element vector [n][1] f32 (or a [1][n] row): returns its stride in
 // elements via *stride.
 int check_vec(const q3_view *v, uint32_t n, int64_t *stride) {
-  if (!v || !v->data) return Q3_ERR_ARG;
+  if (!v || no_data(v)) return Q3_ERR_ARG;
   if (v->dtype != Q3_DT_F32) return Q3_ERR_DTYPE;
   if (v->rows >= n && v->cols >= 1) {
     if (v->row_bytes % 4 != 0 || (n > 1 && v->row_bytes < 4)) return Q3_ERR_VIEW;
@@ -46,7 +51,7 @@ int check_vec(const q3_view *v, uint32_t n, int64_t *stride) {
 // (col_bytes a multiple of 4): at least `rows` x `cols`, and each row long
 // enough for its last column.
 int check_scales(const q3_view *v, uint32_t rows, uint32_t cols) {
-  if (!v || !v->data) return Q3_ERR_ARG;
+  if (!v || no_data(v)) return Q3_ERR_ARG;
   if (v->dtype != Q3_DT_F32) return Q3_ERR_DTYPE;
   if (v->row_bytes % 4 || v->col_bytes % 4 || v->col_bytes <= 0) return Q3_ERR_VIEW;
   if (v->rows < rows || v->cols < cols) return Q3_ERR_VIEW;
@@ -68,14 +73,16 @@ int hip_status(hipError_t e) { return e == hipSuccess ? Q3_OK : Q3_ERR_HIP; }
     if (q3_rc_ != Q3_OK) return q3_rc_; \
   } while (0)
 
-// Validates the common GEMM operands; fills the shape fields of g.
+// Validates the common GEMM operands; fills the shape fields of g.  *skip:
+// the caller returns the status without launching (an unsupported shape, or
+// no rows: group_gemm.h:91's row loop then does nothing).
 int gemm_common(const q3_view *a, const q3_view *a_scale, const q3_view *b,
                 const q3_view *b_scale, uint32_t group_k, q3::GemmArgs &g,
                 bool *skip) {
   *skip = false;
   Q3_TRY(check_view(a, Q3_DT_I8));
   Q3_TRY(check_view(b, Q3_DT_I8));
-  if (!a_scale || !a_scale->data || !b_scale || !b_scale->data) return Q3_ERR_ARG;
+  if (!a_scale || no_data(a_scale) || !b_scale || no_data(b_scale)) return Q3_ERR_ARG;
   if (a_scale->dtype != Q3_DT_F32 || b_scale->dtype != Q3_DT_F32) return Q3_ERR_DTYPE;
   const uint32_t K = a->cols, N = b->rows, M = a->rows;
   if (b->cols != K) return Q3_ERR_VIEW;
@@ -114,6 +121,7 @@ int gemm_common(const q3_view *a, const q3_view *a_scale, const q3_view *b,
   g.bs = static_cast<const float *>(b_scale->data);
   g.bs_stride = bss;
   g.bs_ld = bs_ld;
+  *skip = M == 0;
   return Q3_OK;
 }
 
@@ -228,7 +236,7 @@ int q3_embedding_rmsnorm_rows(const q3_view *table, const q3_view *scale,
   Q3_TRY(check_view(table, Q3_DT_I8));
   Q3_TRY(check_view(tmp, Q3_DT_F32));
   Q3_TRY(check_view(out, Q3_DT_F32));
-  if (!ids || !ids->data) return Q3_ERR_ARG;
+  if (!ids || no_data(ids)) return Q3_ERR_ARG;
   if (ids->dtype != Q3_DT_I32 && ids->dtype != Q3_DT_U32) return Q3_ERR_DTYPE;
   const uint32_t rows = ids->rows, cols = table->cols;
   if (tmp->cols < cols || out->cols < cols || tmp->rows < rows || out->rows < rows) return Q3_ERR_VIEW;
@@ -282,7 +290,7 @@ int q3_quant_rows_heads(const q3_view *x, const q3_view *qi8,
                         void *stream) {
   Q3_TRY(check_view(x, Q3_DT_F32));
   Q3_TRY(check_view(qi8, Q3_DT_I8));
-  if (!scale || !scale->data) return Q3_ERR_ARG;
+  if (!scale || no_data(scale)) return Q3_ERR_ARG;
   if (scale->dtype != Q3_DT_F32) return Q3_ERR_DTYPE;
   if (group_cols == 0) return Q3_ERR_ARG;
   if (qi8->rows < x->rows || qi8->cols < x->cols) return Q3_ERR_VIEW;
@@ -433,7 +441,7 @@ int q3_attention_heads_gqa_tokscale_paged(const q3_view *q8,
   Q3_TRY(check_view(q8, Q3_DT_I8));
   Q3_TRY(check_view(o8, Q3_DT_I8));
   Q3_TRY(check_paged(kv));
-  if (!q_scale || !q_scale->data || !os || !os->data) return Q3_ERR_ARG;
+  if (!q_scale || no_data(q_scale) || !os || no_data(os)) return Q3_ERR_ARG;
   if (q_scale->dtype != Q3_DT_F32 || os->dtype != Q3_DT_F32) return Q3_ERR_DTYPE;
   if (head_dim != 128) return unsupported();
   if (heads <= 0 || kv_heads <= 0 || heads % kv_heads) return Q3_ERR_ARG;
@@ -657,7 +665,7 @@ int argmax_common(const q3_view *a, const q3_view *a_scale, const q3_view *b,
     *skip = true;
     return unsupported();
   }
-  if (!best || !best->data || !bidx || !bidx->data) return Q3_ERR_ARG;
+  if (!best || no_data(best) || !bidx || no_data(bidx)) return Q3_ERR_ARG;
   if (best->dtype != Q3_DT_F32) return Q3_ERR_DTYPE;
   if (bidx->dtype != Q3_DT_I32 && bidx->dtype != Q3_DT_U32) return Q3_ERR_DTYPE;
   Q3_TRY(check_vec(best, a->rows, bst));

@@ -151,3 +151,48 @@ def test_group_bscale_only_for_stores(lib):
     assert lib.q3_gemm_nt_group_store(a, as_, b, V(N - 1, K // 256, DT_F32), V(M, N, DT_F32), 256,
                                       None, None, None, None, None, None, C.c_float(0),
                                       None) == ERR_VIEW
+
+
+def test_zero_rows_return_ok_without_launching(lib):
+    """An operator with 0 rows returns Q3_OK before any device call (this
+    runs with no GPU), and 0-row views may carry NULL data, which is what an
+    empty torch tensor hands over: the reference's row loops
+    (group_gemm.h:91, swiglu_quant.h:164, lm_argmax.h:72, rmsnorm.h:34,
+    quant.h:89, norm_rope_quant.h:88, attention_gqa.h:549) do nothing."""
+    def E(cols, dt):
+        es = 1 if dt == DT_I8 else 4
+        return C.byref(_lib.View(None, cols * es, es, 0, cols, dt))
+
+    K, N = 1024, 2048
+    a, as_ = E(K, DT_I8), E(K // 256, DT_F32)
+    b, bs = V(N, K, DT_I8), V(N, 1, DT_F32)
+    assert lib.q3_gemm_nt_group_store(a, as_, b, bs, E(N, DT_F32), 256, None, None, None, None,
+                                      None, None, C.c_float(0), None) == OK
+    assert lib.q3_gemm_nt_group_store(a, as_, b, bs, E(N, DT_F32), 256, E(N, DT_F32), None, None,
+                                      None, None, None, C.c_float(0), None) == OK
+    kv = paged()
+    assert lib.q3_gemm_nt_group_kv_paged(a, as_, V(1024, K, DT_I8), V(1024, 1, DT_F32), 256,
+                                         C.byref(kv), 5, 1, None, None, None, C.c_float(0),
+                                         None) == OK
+    assert lib.q3_gemm_gate_up_swiglu_quant(a, as_, V(3072, K, DT_I8), V(3072, 1, DT_F32),
+                                            V(3072, K, DT_I8), V(3072, 1, DT_F32),
+                                            E(3072, DT_I8), E(12, DT_F32), 256, None) == OK
+    for fn in (lib.q3_gemm_nt_group_argmax, lib.q3_gemm_nt_group_argmax_noalloc):
+        assert fn(a, as_, b, bs, E(1, DT_F32), E(1, DT_I32), 256, None) == OK
+    H = 1024
+    w = V(H, 1, DT_F32)
+    assert lib.q3_rmsnorm_rows(E(H, DT_F32), w, E(H, DT_F32), C.c_float(1 / H), None) == OK
+    assert lib.q3_quant_rows_heads(E(H, DT_F32), E(H, DT_I8), E(8, DT_F32), 128, None) == OK
+    assert lib.q3_embedding_rmsnorm_rows(V(64, H, DT_I8), V(64, 1, DT_F32), E(1, DT_I32),
+                                         E(H, DT_F32), w, E(H, DT_F32), C.c_float(1 / H),
+                                         None) == OK
+    assert lib.q3_norm_rope_quant_heads(E(H, DT_F32), V(128, 1, DT_F32), E(64, DT_F32),
+                                        E(64, DT_F32), E(H, DT_I8), E(8, DT_F32), 8,
+                                        C.c_float(1 / 128), 1, None) == OK
+    for causal in (1, 0):
+        assert lib.q3_attention_heads_gqa_tokscale_paged(
+            E(16 * 128, DT_I8), E(16, DT_F32), C.byref(kv), 40, E(16 * 128, DT_I8),
+            E(16, DT_F32), 16, 8, 128, causal, C.c_float(0.088), None) == OK
+    # a NULL data pointer on a view that has rows is still rejected
+    assert lib.q3_rmsnorm_rows(C.byref(_lib.View(None, 4 * H, 4, 2, H, DT_F32)), w,
+                               V(2, H, DT_F32), C.c_float(1 / H), None) == -1

@@ -711,3 +711,73 @@ def test_quant_guest_fixture(cuda):
     s = torch.zeros((32, 2), dtype=torch.float32, device=cuda)
     ops.quant_rows_heads(dev(g["qh_x"]), q, s, 128)
     assert bits_equal(host(q), g["qh_q"]) and bits_equal(host(s), g["qh_s"])
+
+
+def test_zero_rows_are_no_ops(cuda):
+    """Every row-parallel operator called with 0 rows returns OK and writes
+    nothing, as the reference's row loops then do nothing (group_gemm.h:91,
+    swiglu_quant.h:164, lm_argmax.h:72, attention_gqa.h:549, rmsnorm.h:34,
+    quant.h:89, embedding.h:99).  The 0-row views are empty slices, which
+    torch hands over with a NULL data pointer; the outputs they were sliced
+    from hold a sentinel that must survive."""
+    rng = np.random.default_rng(77)
+    K, N, g = 1024, 2048, 256
+    a, as_, b, bs = rand_gemm(rng, 4, K, N, g)
+    ta, tas, tb, tbs = dev(a)[:0], dev(as_)[:0], dev(b), dev(bs)
+
+    def full(shape, v, dt=torch.float32):
+        return torch.full(shape, v, dtype=dt, device=cuda)
+
+    note("zero rows: gemm store / residual / argmax")
+    out = full((4, N), 7.0)
+    ops.gemm_nt_group_store(ta, tas, tb, tbs, out[:0], g)
+    ops.gemm_nt_group_store(ta, tas, tb, tbs, out[:0], g, add=out[:0])
+    best, bidx = full((4,), -1.0), full((4,), -5, torch.int32)
+    ops.gemm_nt_group_argmax(ta, tas, tb, tbs, best[:0], bidx[:0], g)
+    ops.gemm_nt_group_argmax_noalloc(ta, tas, tb, tbs, best[:0], bidx[:0], g)
+    torch.cuda.synchronize()
+    assert (host(out) == 7.0).all()
+    assert (host(best) == -1.0).all() and (host(bidx) == -5).all()
+
+    note("zero rows: gate/up + SwiGLU + quant")
+    _, _, wg, wgs = rand_gemm(rng, 1, K, 3072, g)
+    _, _, wu, wus = rand_gemm(rng, 1, K, 3072, g)
+    s8, ss = full((4, 3072), 5, torch.int8), full((4, 12), 3.0)
+    ops.gemm_gate_up_swiglu_quant(ta, tas, dev(wg), dev(wgs), dev(wu), dev(wus), s8[:0], ss[:0], g)
+    assert (host(s8) == 5).all() and (host(ss) == 3.0).all()
+
+    note("zero rows: row kernels")
+    H = 1024
+    x = dev(rng.normal(size=(4, H)).astype(F))
+    w = dev((1 + 0.05 * rng.normal(size=H)).astype(F))
+    emb = dev(rng.integers(-127, 128, (64, H)).astype(np.int8))
+    es = dev(rng.uniform(1e-4, 1e-3, 64).astype(F))
+    ids = dev(np.arange(4, dtype=np.int32).reshape(-1, 1))
+    tmp, rout = full((4, H), 2.0), full((4, H), 9.0)
+    ops.embedding_rmsnorm_rows(emb, es, ids[:0], tmp[:0], w, rout[:0], F(1 / H))
+    ops.rmsnorm_rows(x[:0], w, rout[:0], F(1 / H))
+    q, s = full((4, H), 4, torch.int8), full((4, H // 128), 6.0)
+    ops.quant_rows_heads(x[:0], q[:0], s[:0], 128)
+    ang = rng.uniform(0, 100, (4, 64))
+    cos, sin = dev(np.cos(ang).astype(F)), dev(np.sin(ang).astype(F))
+    nw = dev((1 + 0.05 * rng.normal(size=128)).astype(F))
+    ops.norm_rope_quant_heads(x[:0], nw, cos[:0], sin[:0], q[:0], s[:0, :8], 8, F(1 / 128), True)
+    assert (host(tmp) == 2.0).all() and (host(rout) == 9.0).all()
+    assert (host(q) == 4).all() and (host(s) == 6.0).all()
+
+    note("zero rows: K/V page epilogue and attention")
+    table = np.array([2, 0, 1], np.uint16)
+    kp, ksp = full((3, 32, 1024), 1, torch.int8), full((3, 32, 8), 8.0)
+    vp, vsp = full((3, 32, 1024), 1, torch.int8), full((3, 32, 8), 8.0)
+    kv = ops.paged_kv(kp, vp, ksp, vsp, dev(table.view(np.int16)))
+    _, _, bv, bvs = rand_gemm(rng, 1, K, 1024, g)
+    ops.gemm_nt_group_kv_paged(ta, tas, dev(bv), dev(bvs), g, kv, 5, True)
+    q8 = dev(rng.integers(-127, 128, (4, 16 * 128)).astype(np.int8))
+    qs = dev(rng.uniform(1e-3, 5e-2, (4, 16)).astype(F))
+    o8, os_ = full((4, 16 * 128), 3, torch.int8), full((4, 16), 1.5)
+    for causal in (True, False):
+        ops.attention_heads_gqa_tokscale_paged(q8[:0], qs[:0], kv, 40, o8[:0], os_[:0], 16, 8, 128,
+                                               causal, QK)
+    assert (host(kp) == 1).all() and (host(vp) == 1).all()
+    assert (host(ksp) == 8.0).all() and (host(vsp) == 8.0).all()
+    assert (host(o8) == 3).all() and (host(os_) == 1.5).all()
