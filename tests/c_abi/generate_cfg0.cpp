@@ -1,7 +1,6 @@
-// A C++ host driver of the model-level boundary, written as the
-// INTEGRATION.md snippet replaces src/main_big.cpp:332-369 (main): layout ->
-// blob -> q3_model_open -> q3_generate -> copy the blob back and read its
-// ids and logits.  The model is config 0's random-init blob (one layer,
+// A C++ host driver of the model-level boundary, in place of
+// src/main_big.cpp:332-369 (main): layout -> blob -> q3_model_open ->
+// q3_generate -> copy the blob back and read its ids and logits.  The model is config 0's random-init blob (one layer,
 // 1024-token vocab, a 40-token prompt as 32 + 8 rows, 2 greedy tokens) in
 // mode 1, so the last forward's logits are written.  Usage:
 //   generate_cfg0 OUT.bin   -> OUT.bin holds int32 ids[40..41] then the f32

@@ -5,9 +5,9 @@ the ops (src/main_big.cpp:332-369) would use it:
   -pedantic -Werror against include/q3ops.h and linked with libq3ops.so,
   computes blob layouts and hits the host error paths (CPU);
 - a C++ driver (tests/c_abi/generate_cfg0.cpp, built by
-  qwen3-tile-ops_amd/build.py) runs INTEGRATION.md's model-level snippet on
-  config 0 and its ids and logits are compared with the reference's goldens
-  (GPU).
+  qwen3-tile-ops_amd/build.py) runs the model-level replacement of that
+  caller (layout, blob, q3_model_open, q3_generate) on config 0, and its ids
+  and logits are compared with the reference's goldens (GPU).
 """
 from __future__ import annotations
 

@@ -23,7 +23,11 @@ def test_layout_matches_reference():
     assert Layout().header_text() == ref["default_header"]
 
 
-def test_survey_offsets():
+def test_default_layout_offsets():
+    """The default (Qwen3-0.6B, max_seq 256) layout's scratch end and KV
+    strides with per-(token, KV head) scales, tools/pqwf.py:124-135 (the
+    reference's checked-in config/model_big.h predates those scales: one
+    scale per token, a KV stride of 526336)."""
     lay = Layout()
     assert lay["kSCRATCH_END"] == 791_880_192
     assert lay["kKV_STRIDE"] == 540_672
