@@ -541,7 +541,10 @@ __global__ void __launch_bounds__(256) gemv_stream_kernel(GemvArgs a, int ntiles
 // contiguous 16-byte-per-lane reads (probe); with one activation row the
 // MFMA's other 15 rows are idle anyway.  Here a wave reads whole 1 KB
 // weight rows, lane l holding k = 16 l .. 16 l + 15, R rows per step with
-// the next step's loads in flight.  Per row: v_dot4 partials (exact int32),
+// the next step's loads in flight, as non-temporal loads: each row is read
+// once per launch, and the 156 MB of lm_head rows would otherwise displace
+// the last-level cache's lines the next launches read (decode lm_head 27.4
+// -> 26.2 us, 0.619 -> 0.618 ms/token).  Per row: v_dot4 partials (exact int32),
 // the 16 lanes of each 256-column group summed with DPP (exact), then the
 // group GEMM's arithmetic (kernels/lm_argmax.h:72-182, ref_qwen3.py:145-158):
 // p_g = RN(RN(f32(I_g) * bs[n]) * as_g), out = (((0 + p_0) + p_1) + p_2) + p_3.
@@ -572,7 +575,8 @@ __global__ void __launch_bounds__(256) gemv_row_kernel(GemvArgs a, int N) {
     for (int r = 0; r < R; ++r) {
       const int n = min(b0 + r, N - 1);  // past N: reloaded, never used
       bs[r] = sg.bs[n];
-      w[r] = *reinterpret_cast<const int4 *>(sg.b + static_cast<int64_t>(n) * 1024 + 16 * lane);
+      const v4i v = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(sg.b + static_cast<int64_t>(n) * 1024 + 16 * lane));
+      w[r] = make_int4(v.x, v.y, v.z, v.w);
     }
   };
   int4 w0[R], w1[R];
