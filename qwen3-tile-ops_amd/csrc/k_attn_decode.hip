@@ -23,8 +23,10 @@
 // pair's K/V).  NW waves own blocks round-robin, BPW per chunk each.  The
 // kernel is latency-bound, so its global loads are issued in the order they
 // are needed (vector loads return in order): first the prologue's operands,
-// then every K/V row and scale of the chunk; V stays in registers from
-// phase 1 to phase 3 and the exp table lives in LDS.
+// then every K/V row and scale of the chunk; the exp table lives in LDS.
+// Batches keep V in registers from phase 1 to phase 3 (P8.V with v_dot4 on
+// 4x4 byte-transposed V words); the fused b = 1 variants copy V into LDS
+// stages and compute P8.V on the matrix cores (VMF below).
 //
 // Optional prologue (decode fusion): the head epilogues of the new token's
 // Q/K/V projection rows (kernels/norm_rope_quant.h:17-86 for Q and K,
@@ -44,6 +46,35 @@ namespace q3 {
 namespace {
 
 constexpr int HD = 128;
+
+// ---- P8.V on the matrix cores (the fused b = 1 variants) ----
+// A block's V rows go from memory straight into an LDS stage, [32 keys][8 x
+// 16 B] with 16-byte chunk c of key r at position c ^ vswz(r), so that the
+// 8 keys a transposing read gathers fall on 8 different chunks.
+typedef int v4i_d __attribute__((ext_vector_type(4)));
+typedef int v2i_d __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) v2i_d *lds_v2i_ptr_d;
+__device__ __forceinline__ int vswz(int key) { return (key & 3) | ((key >> 2) & 4); }
+
+// 16 bytes per lane global -> LDS (lane l writes lds + 16 l), as inline
+// assembly: the compiler does not count it among the loads in flight, so
+// its waits for later loads only become stricter (loads complete in
+// order), while its own global_load_lds would make it wait for every load
+// before the next use of any.  A copy is issued in front of loads whose
+// wait then covers it.
+__device__ __forceinline__ void lds_copy16(const void *src, const void *lds) {
+  const uint32_t m0v =
+      __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(to_lds(lds))));
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0v)
+               : "memory", "m0");
+}
+
+// Byte position of key c's P8 in a block's 32-byte P8 row, so that lane L's
+// 8 bytes at 8 (L / 16) are the keys 16 (j / 4) + 4 (L / 16) + j % 4,
+// j = 0..7: the keys ds_read_b64_tr_b8 hands lane L of the V operand (in
+// each 16-lane group, result lane i byte j is byte i % 8 of the 8 bytes
+// addressed by source lane 2 j + i / 8).
+__device__ __forceinline__ int p8_pos(int c) { return 8 * ((c & 15) >> 2) + (((c >> 4) << 2) | (c & 3)); }
 
 __device__ __forceinline__ int sdot4(int a, int b, int c) {
   return __builtin_amdgcn_sdot4(a, b, c, false);
@@ -383,6 +414,16 @@ __device__ __forceinline__ void attn_decode_body(const AttnArgs &a, int bx, int 
   static_assert(!POLL || OFUSE, "polled projection rows: the fused b = 1 variant");
   __shared__ __align__(16) Smem<QPW, CB> sm;
   __shared__ __align__(16) SmemO<OFUSE> smo;
+  // VMF (the fused b = 1 variants, one query head): V through LDS stages
+  // and P8.V as v_mfma_i32_16x16x32_i8 with P8 (the query row, replicated
+  // over the 16 rows) as A and the V rows of a 16-dim tile, read with
+  // ds_read_b64_tr_b8, as B: integer sums, exact like the v_dot4 form.
+  // (these launches hold one 12-wave workgroup per CU by registers, so the
+  // stages' LDS does not cost residency)
+  constexpr bool VMF = FUSE;
+  static_assert(!VMF || QPW == 1, "P8.V on the matrix cores: one query head per workgroup");
+  __shared__ __align__(16) int8_t vst[VMF ? NW * BPW * 4096 : 16];
+  __shared__ __align__(16) int8_t p8s[VMF ? NW * BPW * 32 : 16];
   // workgroup barriers: POLL waits only for LDS (s_waitcnt lgkmcnt(0)), not
   // for every outstanding vector memory operation as __syncthreads does,
   // so that the O projection's weight pieces and the page-slot stores stay
@@ -552,6 +593,16 @@ __device__ __forceinline__ void attn_decode_body(const AttnArgs &a, int bx, int 
                           slot0 * h.scale_row_bytes;
       const int8_t *vsb = reinterpret_cast<const int8_t *>(h.vs) + page * h.scale_page_bytes +
                           slot0 * h.scale_row_bytes;
+      // VMF: the V rows into the wave's stage for block i, issued in front
+      // of the K rows so that the wait for those (phase 1) covers them
+      if constexpr (VMF) {
+        int8_t *st = vst + (wave * BPW + i) * 4096;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 8 * e + (lane >> 3);
+          lds_copy16(vb + min(r, last) * h.row_bytes + 16 * ((lane & 7) ^ vswz(r)), st + 1024 * e);
+        }
+      }
       // Without the fused prologue (batches) the K/V rows are read once, by
       // one workgroup: non-temporal loads, so that they do not push the
       // scale and page-table lines the kv heads of a sequence share out of
@@ -576,13 +627,15 @@ __device__ __forceinline__ void attn_decode_body(const AttnArgs &a, int bx, int 
         }
       }
       kscale[i] = reinterpret_cast<const float *>(ksb + min(kcl, last) * h.scale_row_bytes)[kvh];
+      if constexpr (!VMF) {
 #pragma unroll
-      for (int cc = 0; cc < 16; ++cc) {
-        const int *vp = reinterpret_cast<const int *>(vb + min(kh + cc, last) * h.row_bytes + d0);
-        if constexpr (!FUSE)
-          vw[i][cc] = __builtin_nontemporal_load(vp);
-        else
-          vw[i][cc] = *vp;
+        for (int cc = 0; cc < 16; ++cc) {
+          const int *vp = reinterpret_cast<const int *>(vb + min(kh + cc, last) * h.row_bytes + d0);
+          if constexpr (!FUSE)
+            vw[i][cc] = __builtin_nontemporal_load(vp);
+          else
+            vw[i][cc] = *vp;
+        }
       }
       vscale[i] = reinterpret_cast<const float *>(vsb + min(lane & 31, last) * h.scale_row_bytes)[kvh];
     };
@@ -638,11 +691,45 @@ __device__ __forceinline__ void attn_decode_body(const AttnArgs &a, int bx, int 
       }
     };
     auto patch_v = [&](int i, int j) {
-      if constexpr (FUSE) {
+      if constexpr (VMF) {
+        // the new token's row into the stage (its copy has completed: the
+        // block's K rows, issued after it, have been waited for)
+        const int r = pos0 - j;
+        if (r >= 0 && r < 32 && lane < 32) {
+          int8_t *dst = vst + (wave * BPW + i) * 4096 + r * HD;
+          const int g = lane >> 2, q = lane & 3;
+          *reinterpret_cast<int *>(dst + 16 * (g ^ vswz(r)) + 4 * q) =
+              *reinterpret_cast<const int *>(sm.vnew + 16 * g + 4 * q);
+        }
+        if (j + (lane & 31) == pos0) vscale[i] = sm.vsnew;
+      } else if constexpr (FUSE) {
 #pragma unroll
         for (int cc = 0; cc < 16; ++cc)
           if (j + kh + cc == pos0) vw[i][cc] = *reinterpret_cast<const int *>(sm.vnew + d0);
         if (j + (lane & 31) == pos0) vscale[i] = sm.vsnew;
+      }
+    };
+    // VMF: P8.V of the wave's block i (P8 bytes already in p8s) for the 128
+    // dims, f32(sum) * pmh into sm.pv[0][jb]
+    const int tr_key = 16 * (((lane & 15) >> 1) >> 2) + 4 * (lane >> 4) + (((lane & 15) >> 1) & 3);
+    const int tr_base = tr_key * HD + 8 * (lane & 1);
+    const int tr_sw = vswz(tr_key);
+    auto pv_mfma = [&](int i, int jb, float pmh) {
+      const int8_t *st = vst + (wave * BPW + i) * 4096;
+      const long av = *reinterpret_cast<const long *>(p8s + (wave * BPW + i) * 32 + 8 * (lane >> 4));
+      const v4i_d z = {0, 0, 0, 0};
+      v4i_d c[8];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const v2i_d bt =
+            __builtin_amdgcn_ds_read_tr8_b64_v2i32(reinterpret_cast<lds_v2i_ptr_d>(to_lds(st + tr_base + ((t ^ tr_sw) << 4))));
+        long bv;
+        __builtin_memcpy(&bv, &bt, sizeof(bv));
+        c[t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv, z, 0, 0, 0);
+      }
+      if (lane < 16) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) sm.pv[0][jb][16 * t + lane] = __fmul_rn(static_cast<float>(c[t][0]), pmh);
       }
     };
     // ---- phase 1: scores and block maxima ----
@@ -685,7 +772,7 @@ __device__ __forceinline__ void attn_decode_body(const AttnArgs &a, int bx, int 
       }
       if (FUSE && i < BPW - 1) {
         patch_v(i, j);
-        v_transpose(vw[i]);
+        if constexpr (!VMF) v_transpose(vw[i]);
       }
     }
     if constexpr (OFUSE) {
@@ -747,25 +834,31 @@ __device__ __forceinline__ void attn_decode_body(const AttnArgs &a, int bx, int 
         const float pm = __fmul_rn(max32(pv), inv127());
         const int p8 = quant1(pv, pm);
         if (c == 0) sm.psum[0][jbl] = psum;
-        if constexpr (!FUSE) v_transpose(vw[0]);  // (FUSE: done in phase 1)
-        v_transpose(vw[1]);
+        if constexpr (VMF) {
+          p8s[(wave * BPW + hi) * 32 + p8_pos(c)] = static_cast<int8_t>(p8);
+          pv_mfma(0, wave, lane_bcast<0>(pm));
+          pv_mfma(1, wave + NW, lane_bcast<32>(pm));
+        } else {
+          if constexpr (!FUSE) v_transpose(vw[0]);  // (FUSE: done in phase 1)
+          v_transpose(vw[1]);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          int acc[1][4] = {{0, 0, 0, 0}};
-          if (i == 0)
-            pv_dot<1, 0>(vw[0], p8, lane, acc);
-          else
-            pv_dot<1, 1>(vw[1], p8, lane, acc);
+          for (int i = 0; i < 2; ++i) {
+            int acc[1][4] = {{0, 0, 0, 0}};
+            if (i == 0)
+              pv_dot<1, 0>(vw[0], p8, lane, acc);
+            else
+              pv_dot<1, 1>(vw[1], p8, lane, acc);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) acc[0][e] += lane_xor<32>(acc[0][e]);
-          const float pmh = i ? lane_bcast<32>(pm) : lane_bcast<0>(pm);
-          if (lane < 32) {
-            float4 o;
-            o.x = __fmul_rn(static_cast<float>(acc[0][0]), pmh);
-            o.y = __fmul_rn(static_cast<float>(acc[0][1]), pmh);
-            o.z = __fmul_rn(static_cast<float>(acc[0][2]), pmh);
-            o.w = __fmul_rn(static_cast<float>(acc[0][3]), pmh);
-            *reinterpret_cast<float4 *>(&sm.pv[0][wave + NW * i][d0]) = o;
+            for (int e = 0; e < 4; ++e) acc[0][e] += lane_xor<32>(acc[0][e]);
+            const float pmh = i ? lane_bcast<32>(pm) : lane_bcast<0>(pm);
+            if (lane < 32) {
+              float4 o;
+              o.x = __fmul_rn(static_cast<float>(acc[0][0]), pmh);
+              o.y = __fmul_rn(static_cast<float>(acc[0][1]), pmh);
+              o.z = __fmul_rn(static_cast<float>(acc[0][2]), pmh);
+              o.w = __fmul_rn(static_cast<float>(acc[0][3]), pmh);
+              *reinterpret_cast<float4 *>(&sm.pv[0][wave + NW * i][d0]) = o;
+            }
           }
         }
       }
@@ -795,6 +888,11 @@ __device__ __forceinline__ void attn_decode_body(const AttnArgs &a, int bx, int 
         const float pm = __fmul_rn(max32(pv), inv127());
         const int p8 = hok ? quant1(pv, pm) : 0;
         if (hok && c == 0) sm.psum[h][jb] = psum;
+        if constexpr (VMF) {
+          if (lane < 32) p8s[(wave * BPW + i) * 32 + p8_pos(c)] = static_cast<int8_t>(p8);
+          pv_mfma(i, jb, lane_bcast<0>(pm));
+          continue;
+        }
         if (!FUSE || i == BPW - 1) v_transpose(vw[i]);
         int acc[2][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
         pv_dot<(QPW > 1 ? 2 : 1)>(vw[i], p8, lane, reinterpret_cast<int(&)[(QPW > 1 ? 2 : 1)][4]>(acc));
