@@ -24,9 +24,10 @@
 // kernel is latency-bound, so its global loads are issued in the order they
 // are needed (vector loads return in order): first the prologue's operands,
 // then every K/V row and scale of the chunk; the exp table lives in LDS.
-// Batches keep V in registers from phase 1 to phase 3 (P8.V with v_dot4 on
-// 4x4 byte-transposed V words); the fused b = 1 variants copy V into LDS
-// stages and compute P8.V on the matrix cores (VMF below).
+// The fused b = 1 variants and batches copy V into LDS stages and compute
+// P8.V on the matrix cores (VMF below); the unfused b = 1 variant keeps V in
+// registers from phase 1 to phase 3 (P8.V with v_dot4 on 4x4 byte-transposed
+// V words).
 //
 // Optional prologue (decode fusion): the head epilogues of the new token's
 // Q/K/V projection rows (kernels/norm_rope_quant.h:17-86 for Q and K,
@@ -62,11 +63,17 @@ __device__ __forceinline__ int vswz(int key) { return (key & 3) | ((key >> 2) & 
 // order), while its own global_load_lds would make it wait for every load
 // before the next use of any.  A copy is issued in front of loads whose
 // wait then covers it.
+// (NT: a non-temporal read, for rows read once that no prefetch brought in)
+template <bool NT = false>
 __device__ __forceinline__ void lds_copy16(const void *src, const void *lds) {
   const uint32_t m0v =
       __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(to_lds(lds))));
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0v)
-               : "memory", "m0");
+  if constexpr (NT)
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src), "s"(m0v)
+                 : "memory", "m0");
+  else
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0v)
+                 : "memory", "m0");
 }
 
 // Byte position of key c's P8 in a block's 32-byte P8 row, so that lane L's
@@ -420,10 +427,11 @@ __device__ __forceinline__ void attn_decode_body(const AttnArgs &a, int bx, int 
   // ds_read_b64_tr_b8, as B: integer sums, exact like the v_dot4 form.
   // (these launches hold one 12-wave workgroup per CU by registers, so the
   // stages' LDS does not cost residency)
-  constexpr bool VMF = FUSE;
-  static_assert(!VMF || QPW == 1, "P8.V on the matrix cores: one query head per workgroup");
+  // Batches (QPW = 2) the same, with the two heads' P8 in the even and odd
+  // A rows, so that one set of products serves both heads.
+  constexpr bool VMF = FUSE || QPW == 2;
   __shared__ __align__(16) int8_t vst[VMF ? NW * BPW * 4096 : 16];
-  __shared__ __align__(16) int8_t p8s[VMF ? NW * BPW * 32 : 16];
+  __shared__ __align__(16) int8_t p8s[VMF ? NW * BPW * 32 * QPW : 16];
   // workgroup barriers: POLL waits only for LDS (s_waitcnt lgkmcnt(0)), not
   // for every outstanding vector memory operation as __syncthreads does,
   // so that the O projection's weight pieces and the page-slot stores stay
@@ -600,7 +608,7 @@ __device__ __forceinline__ void attn_decode_body(const AttnArgs &a, int bx, int 
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int r = 8 * e + (lane >> 3);
-          lds_copy16(vb + min(r, last) * h.row_bytes + 16 * ((lane & 7) ^ vswz(r)), st + 1024 * e);
+          lds_copy16<!FUSE>(vb + min(r, last) * h.row_bytes + 16 * ((lane & 7) ^ vswz(r)), st + 1024 * e);
         }
       }
       // Without the fused prologue (batches) the K/V rows are read once, by
@@ -691,7 +699,7 @@ __device__ __forceinline__ void attn_decode_body(const AttnArgs &a, int bx, int 
       }
     };
     auto patch_v = [&](int i, int j) {
-      if constexpr (VMF) {
+      if constexpr (VMF && FUSE) {
         // the new token's row into the stage (its copy has completed: the
         // block's K rows, issued after it, have been waited for)
         const int r = pos0 - j;
@@ -714,9 +722,12 @@ __device__ __forceinline__ void attn_decode_body(const AttnArgs &a, int bx, int 
     const int tr_key = 16 * (((lane & 15) >> 1) >> 2) + 4 * (lane >> 4) + (((lane & 15) >> 1) & 3);
     const int tr_base = tr_key * HD + 8 * (lane & 1);
     const int tr_sw = vswz(tr_key);
-    auto pv_mfma = [&](int i, int jb, float pmh) {
+    // (QPW = 2: A row m carries head m % 2's P8, so result register q of a
+    // lane holds head q % 2; pmh1 is head 1's pmax)
+    auto pv_mfma = [&](int i, int jb, float pmh, float pmh1 = 0.0f) {
       const int8_t *st = vst + (wave * BPW + i) * 4096;
-      const long av = *reinterpret_cast<const long *>(p8s + (wave * BPW + i) * 32 + 8 * (lane >> 4));
+      const int hrow = QPW == 2 ? (lane & 1) : 0;
+      const long av = *reinterpret_cast<const long *>(p8s + ((wave * BPW + i) * QPW + hrow) * 32 + 8 * (lane >> 4));
       const v4i_d z = {0, 0, 0, 0};
       v4i_d c[8];
 #pragma unroll
@@ -729,7 +740,10 @@ __device__ __forceinline__ void attn_decode_body(const AttnArgs &a, int bx, int 
       }
       if (lane < 16) {
 #pragma unroll
-        for (int t = 0; t < 8; ++t) sm.pv[0][jb][16 * t + lane] = __fmul_rn(static_cast<float>(c[t][0]), pmh);
+        for (int t = 0; t < 8; ++t) {
+          sm.pv[0][jb][16 * t + lane] = __fmul_rn(static_cast<float>(c[t][0]), pmh);
+          if constexpr (QPW == 2) sm.pv[QPW - 1][jb][16 * t + lane] = __fmul_rn(static_cast<float>(c[t][1]), pmh1);
+        }
       }
     };
     // ---- phase 1: scores and block maxima ----
@@ -835,7 +849,7 @@ __device__ __forceinline__ void attn_decode_body(const AttnArgs &a, int bx, int 
         const int p8 = quant1(pv, pm);
         if (c == 0) sm.psum[0][jbl] = psum;
         if constexpr (VMF) {
-          p8s[(wave * BPW + hi) * 32 + p8_pos(c)] = static_cast<int8_t>(p8);
+          p8s[(wave * BPW + hi) * 32 * QPW + p8_pos(c)] = static_cast<int8_t>(p8);
           pv_mfma(0, wave, lane_bcast<0>(pm));
           pv_mfma(1, wave + NW, lane_bcast<32>(pm));
         } else {
@@ -889,8 +903,8 @@ __device__ __forceinline__ void attn_decode_body(const AttnArgs &a, int bx, int 
         const int p8 = hok ? quant1(pv, pm) : 0;
         if (hok && c == 0) sm.psum[h][jb] = psum;
         if constexpr (VMF) {
-          if (lane < 32) p8s[(wave * BPW + i) * 32 + p8_pos(c)] = static_cast<int8_t>(p8);
-          pv_mfma(i, jb, lane_bcast<0>(pm));
+          if (hok) p8s[((wave * BPW + i) * QPW + h) * 32 + p8_pos(c)] = static_cast<int8_t>(p8);
+          pv_mfma(i, jb, lane_bcast<0>(pm), lane_bcast<32>(pm));
           continue;
         }
         if (!FUSE || i == BPW - 1) v_transpose(vw[i]);
