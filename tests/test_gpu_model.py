@@ -501,6 +501,34 @@ def test_generate_300_token_prompt(cuda):
     assert idx == int(np.argmax(logits)) and bits_equal(np.float32(best), logits.max())
 
 
+SHAPE_1K = ModelShape(layers=2, vocab=1024, seq=512, max_seq=1056)
+INIT_1K = InitConfig(weight_seed=0x5EED1000, n_prompt=1000, n_gen=4, mode=0)
+
+
+def test_generate_1000_token_prompt_two_chunk_decode(cuda):
+    """A 1000-token prompt (prefill chunks of 512 + 488) and four greedy
+    decode steps at 1000-1003 keys: the fused b = 1 attention walks two
+    chunks of key blocks per head (24 + 8), reusing its LDS stages in the
+    second chunk and patching the new token's K/V row there.  The ids and the
+    fused argmax equal the oracle's."""
+    import oracle
+    note("1000-token prompt + 4 greedy tokens, 2 layers (two-chunk decode attention)")
+    lay, blob = host_blob("cfg3_perf", shape=SHAPE_1K, init=INIT_1K)
+    dims = dict(SHAPE_1K.__dict__)
+    dims["seq"] = 32
+    om = oracle.OracleModel(blob, lay.offsets, dims)
+    logits, gen, _, _ = om.generate(lay.global_views(blob)["ids"], 1000, 4, record=False)
+    m = Model(lay, blob)
+    m.set_ctrl(1000, 4, 0)
+    m.generate()
+    got = m.ids()[1000:1004].copy()
+    best, idx = m.argmax()
+    assert m.fused_status() == (3, 0)
+    m.close()
+    assert np.array_equal(got, gen), (got, gen)
+    assert idx == int(np.argmax(logits)) and bits_equal(np.float32(best), logits.max())
+
+
 def test_generate_decode_graph_replays(cuda, monkeypatch):
     """On a stream of its own, q3_generate captures its decode steps as one
     HIP graph and replays it while CTRL and the page table stay the same.
