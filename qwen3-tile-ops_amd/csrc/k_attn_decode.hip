@@ -428,7 +428,9 @@ __device__ __forceinline__ void attn_decode_body(const AttnArgs &a, int bx, int 
   // (these launches hold one 12-wave workgroup per CU by registers, so the
   // stages' LDS does not cost residency)
   // Batches (QPW = 2) the same, with the two heads' P8 in the even and odd
-  // A rows, so that one set of products serves both heads.
+  // A rows, so that one set of products serves both heads; their 48 KiB of
+  // stages still let two 4-wave workgroups share a CU, as their registers
+  // do.
   constexpr bool VMF = FUSE || QPW == 2;
   __shared__ __align__(16) int8_t vst[VMF ? NW * BPW * 4096 : 16];
   __shared__ __align__(16) int8_t p8s[VMF ? NW * BPW * 32 * QPW : 16];
